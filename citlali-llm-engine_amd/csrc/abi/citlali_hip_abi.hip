@@ -1,0 +1,429 @@
+// citlali_hip_abi.hip -- the extern "C" boundary (include/citlali_hip.h).
+//
+// Validates arguments on the host (before anything touches the GPU), then
+// calls the gfx950 launchers.  Errors are reported as status codes plus a
+// thread-local message.
+#include "../kernels/launch.hpp"
+#include "citlali_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+
+#define CITLALI_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+thread_local char g_err[512] = "";
+hipStream_t g_stream = nullptr;
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(hipError_t e, const char* expr, const char* file, int line) {
+    if (e == hipSuccess) return CITLALI_OK;
+    return fail(CITLALI_ERR_HIP, "HIP error at %s:%d for %s: %s", file, line, expr, hipGetErrorString(e));
+}
+#define HIP_TRY(expr)                                                          \
+    do {                                                                       \
+        const int _st = hip_status((expr), #expr, __FILE__, __LINE__);         \
+        if (_st != CITLALI_OK) return _st;                                     \
+    } while (0)
+
+#define REQUIRE(cond, ...)                                  \
+    do {                                                    \
+        if (!(cond)) return fail(CITLALI_ERR_INVALID, __VA_ARGS__); \
+    } while (0)
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+int check_matvec(const char* who, const void* w, const void* x, const void* y, int in_f, int out_f, uintptr_t walign,
+                 uintptr_t yalign) {
+    REQUIRE(w && x && y, "%s received a null buffer", who);
+    REQUIRE(in_f > 0 && out_f > 0, "%s: in_features (%d) and out_features (%d) must be positive", who, in_f, out_f);
+    REQUIRE(in_f % 256 == 0, "%s: in_features (%d) is not a multiple of the 256-value super-block", who, in_f);
+    REQUIRE(in_f <= CITLALI_MAX_IN_FEATURES, "%s: in_features (%d) exceeds %d", who, in_f, CITLALI_MAX_IN_FEATURES);
+    REQUIRE(aligned(w, walign), "%s: weight pointer must be %d-byte aligned", who, (int)walign);
+    REQUIRE(aligned(x, 16), "%s: input pointer must be 16-byte aligned", who);
+    REQUIRE(aligned(y, yalign), "%s: output pointer must be %d-byte aligned", who, (int)yalign);
+    return CITLALI_OK;
+}
+
+// Per-device attention workspace used when the caller's `scores` buffer is
+// too small for the split plan.
+struct Workspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+constexpr int kMaxDevices = 64;
+Workspace g_ws[kMaxDevices];
+std::mutex g_ws_mu;
+
+int workspace_for(size_t bytes, float** out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    REQUIRE(dev >= 0 && dev < kMaxDevices, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace& w = g_ws[dev];
+    if (w.bytes < bytes) {
+        if (w.ptr) HIP_TRY(hipFree(w.ptr));
+        w.ptr = nullptr;
+        w.bytes = 0;
+        HIP_TRY(hipMalloc(&w.ptr, bytes));
+        w.bytes = bytes;
+    }
+    *out = static_cast<float*>(w.ptr);
+    return CITLALI_OK;
+}
+
+constexpr int kAttnTargetBlocks = 512;
+
+}  // namespace
+
+using namespace citlali::hip;
+
+// ---------------------------------------------------------------- runtime
+CITLALI_EXPORT const char* citlali_hip_last_error(void) { return g_err; }
+CITLALI_EXPORT int citlali_hip_abi_version(void) { return CITLALI_HIP_ABI_VERSION; }
+
+CITLALI_EXPORT int citlali_hip_init(int device) {
+    REQUIRE(device >= 0, "device index must be non-negative");
+    HIP_TRY(hipSetDevice(device));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_device_count(int* count) {
+    REQUIRE(count, "null output pointer");
+    HIP_TRY(hipGetDeviceCount(count));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_set_stream(void* stream) {
+    g_stream = static_cast<hipStream_t>(stream);
+    return CITLALI_OK;
+}
+CITLALI_EXPORT void* citlali_hip_get_stream(void) { return g_stream; }
+
+CITLALI_EXPORT int citlali_hip_synchronize(void) {
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    HIP_TRY(hipGetLastError());
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- memory
+CITLALI_EXPORT int citlali_hip_malloc(void** ptr, size_t bytes) {
+    REQUIRE(ptr, "null output pointer");
+    *ptr = nullptr;
+    if (bytes == 0) return CITLALI_OK;
+    HIP_TRY(hipMalloc(ptr, bytes));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_free(void* ptr) {
+    if (ptr) HIP_TRY(hipFree(ptr));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return CITLALI_OK;
+    REQUIRE(dst && src, "copy_from_host received a null pointer");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return CITLALI_OK;
+    REQUIRE(dst && src, "copy_to_host received a null pointer");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_stream));
+    HIP_TRY(hipStreamSynchronize(g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_memcpy_d2d(void* dst, const void* src, size_t bytes) {
+    if (bytes == 0) return CITLALI_OK;
+    REQUIRE(dst && src, "device copy received a null pointer");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_zero(void* ptr, size_t bytes) {
+    if (bytes == 0) return CITLALI_OK;
+    REQUIRE(ptr, "zero received a null pointer");
+    HIP_TRY(launch_fill_zero(ptr, bytes, g_stream));
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- GEMV
+CITLALI_EXPORT int citlali_hip_matvec_q4k(const uint8_t* w, const uint16_t* x, uint16_t* y, int in_f, int out_f) {
+    const int st = check_matvec("matvec_q4k", w, x, y, in_f, out_f, 16, 2);
+    if (st) return st;
+    HIP_TRY(launch_matvec_q4k(w, x, y, false, in_f, out_f, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_q4k_to_float(const uint8_t* w, const uint16_t* x, float* y, int in_f,
+                                                   int out_f) {
+    const int st = check_matvec("matvec_q4k_to_float", w, x, y, in_f, out_f, 16, 4);
+    if (st) return st;
+    HIP_TRY(launch_matvec_q4k(w, x, y, true, in_f, out_f, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_q6k(const uint8_t* w, const uint16_t* x, uint16_t* y, int in_f, int out_f) {
+    const int st = check_matvec("matvec_q6k", w, x, y, in_f, out_f, 4, 2);
+    if (st) return st;
+    HIP_TRY(launch_matvec_q6k(w, x, y, false, in_f, out_f, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_q6k_to_float(const uint8_t* w, const uint16_t* x, float* y, int in_f,
+                                                   int out_f) {
+    const int st = check_matvec("matvec_q6k_to_float", w, x, y, in_f, out_f, 4, 4);
+    if (st) return st;
+    HIP_TRY(launch_matvec_q6k(w, x, y, true, in_f, out_f, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden) {
+    REQUIRE(table && out, "embed_q6k received a null buffer");
+    REQUIRE(token_id >= 0, "token id out of vocab range");
+    REQUIRE(hidden > 0 && hidden % 256 == 0, "embed_q6k: hidden (%d) must be a positive multiple of 256", hidden);
+    HIP_TRY(launch_embed_q6k(table, token_id, out, hidden, g_stream));
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- attention
+static int check_attn_shape(int heads, int kv_heads, int head_dim) {
+    REQUIRE(heads > 0 && kv_heads > 0, "attention: heads and kv_heads must be positive");
+    REQUIRE(heads % kv_heads == 0, "attention head_count must be divisible by head_count_kv");
+    if (!attention_supported(head_dim, heads / kv_heads))
+        return fail(CITLALI_ERR_UNSUPPORTED,
+                    "attention: head_dim %d with %d query heads per kv head is not built (head_dim 64/128, group 1..8)",
+                    head_dim, heads / kv_heads);
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                         float* scores, uint16_t* out, int position, int max_context, int heads,
+                                         int kv_heads, int head_dim) {
+    REQUIRE(q && k_cache && v_cache && out, "attention received a null buffer");
+    REQUIRE(position >= 0 && position < max_context, "position exceeds max_context");
+    int st = check_attn_shape(heads, kv_heads, head_dim);
+    if (st) return st;
+    REQUIRE(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), "attention: q and caches must be 16-byte aligned");
+
+    AttnArgs a{};
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.seq_stride = 0;
+    a.positions = nullptr;
+    a.position = position;
+    a.nseq = 1;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.out = out;
+    const AttnPlan p = plan_attention(position + 1, 1, kv_heads, heads, head_dim, kAttnTargetBlocks);
+    const size_t need = attention_workspace_bytes(p, 1, heads, head_dim);
+    const size_t have = scores ? (size_t)heads * (size_t)max_context * sizeof(float) : 0;
+    if (need == 0) {
+        a.workspace = nullptr;
+    } else if (need <= have && aligned(scores, 16)) {
+        a.workspace = scores;
+    } else {
+        st = workspace_for(need, &a.workspace);
+        if (st) return st;
+    }
+    HIP_TRY(launch_attention(a, p, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT size_t citlali_hip_attention_workspace_bytes(int max_positions_bound, int nseq, int heads,
+                                                            int kv_heads, int head_dim) {
+    if (max_positions_bound <= 0 || nseq <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return 0;
+    const AttnPlan p = plan_attention(max_positions_bound, nseq, kv_heads, heads, head_dim, kAttnTargetBlocks);
+    return attention_workspace_bytes(p, nseq, heads, head_dim);
+}
+
+CITLALI_EXPORT int citlali_hip_attention_batched(const uint16_t* q, const uint16_t* k_cache,
+                                                 const uint16_t* v_cache, long long seq_stride,
+                                                 const int32_t* positions, int max_positions_bound, int nseq,
+                                                 int heads, int kv_heads, int head_dim, void* workspace,
+                                                 size_t workspace_bytes, uint16_t* out) {
+    REQUIRE(q && k_cache && v_cache && out && positions, "attention_batched received a null buffer");
+    REQUIRE(nseq > 0, "attention_batched: nseq must be positive");
+    REQUIRE(max_positions_bound > 0, "attention_batched: max_positions_bound must be positive");
+    REQUIRE(seq_stride >= 0, "attention_batched: negative sequence stride");
+    const int st = check_attn_shape(heads, kv_heads, head_dim);
+    if (st) return st;
+    REQUIRE(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) && (seq_stride % 8) == 0,
+            "attention_batched: q, caches and sequence stride must be 16-byte aligned");
+    const AttnPlan p = plan_attention(max_positions_bound, nseq, kv_heads, heads, head_dim, kAttnTargetBlocks);
+    const size_t need = attention_workspace_bytes(p, nseq, heads, head_dim);
+    REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned(workspace, 16))),
+            "attention_batched: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    AttnArgs a{};
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.seq_stride = seq_stride;
+    a.positions = positions;
+    a.position = 0;
+    a.nseq = nseq;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.workspace = static_cast<float*>(workspace);
+    a.out = out;
+    HIP_TRY(launch_attention(a, p, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_release_workspace(void) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    int cur = 0;
+    HIP_TRY(hipGetDevice(&cur));
+    for (int d = 0; d < kMaxDevices; ++d) {
+        if (!g_ws[d].ptr) continue;
+        HIP_TRY(hipSetDevice(d));
+        HIP_TRY(hipFree(g_ws[d].ptr));
+        g_ws[d].ptr = nullptr;
+        g_ws[d].bytes = 0;
+    }
+    HIP_TRY(hipSetDevice(cur));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
+                                        int position, int kv_size) {
+    REQUIRE(k && v && kc && vc, "store_kv received a null buffer");
+    REQUIRE(position >= 0 && kv_size > 0, "store_kv: bad position (%d) or kv_size (%d)", position, kv_size);
+    HIP_TRY(launch_store_kv(k, v, kc, vc, position, kv_size, g_stream));
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- dequant
+CITLALI_EXPORT int citlali_hip_dequant_q4k_f16(const uint8_t* w, uint64_t count, uint16_t* out) {
+    REQUIRE(w && out, "dequant_q4k received a null buffer");
+    if (count == 0) return CITLALI_OK;
+    HIP_TRY(launch_dequant_q4k_f16(w, count, out, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_dequant_q6k_f16(const uint8_t* w, uint64_t count, uint16_t* out) {
+    REQUIRE(w && out, "dequant_q6k received a null buffer");
+    if (count == 0) return CITLALI_OK;
+    HIP_TRY(launch_dequant_q6k_f16(w, count, out, g_stream));
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- rest of the step
+CITLALI_EXPORT int citlali_hip_embed(const uint16_t* table, int32_t token_id, uint16_t* out, int hidden) {
+    REQUIRE(table && out, "embed received a null buffer");
+    REQUIRE(token_id >= 0 && hidden > 0, "embed: bad token id or hidden size");
+    HIP_TRY(launch_embed_f16(table, token_id, out, hidden, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_copy(const uint16_t* in, uint16_t* out, int n) {
+    REQUIRE(in && out && n > 0, "copy: bad arguments");
+    HIP_TRY(launch_copy(in, out, n, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_add_inplace(uint16_t* t, const uint16_t* d, int n) {
+    REQUIRE(t && d && n > 0, "add_inplace: bad arguments");
+    HIP_TRY(launch_add_inplace(t, d, n, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_add_bias_inplace(uint16_t* t, const uint16_t* b, int n) {
+    REQUIRE(t && b && n > 0, "add_bias_inplace: bad arguments");
+    HIP_TRY(launch_add_inplace(t, b, n, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, int n, float eps) {
+    REQUIRE(in && w && out && n > 0, "rms_norm: bad arguments");
+    HIP_TRY(launch_rms_norm(in, w, out, n, eps, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_rms_norm_heads(const uint16_t* in, const uint16_t* w, uint16_t* out, int heads,
+                                              int head_dim, float eps) {
+    REQUIRE(in && w && out && heads > 0 && head_dim > 0, "rms_norm_heads: bad arguments");
+    HIP_TRY(launch_rms_norm_heads(in, w, out, heads, head_dim, eps, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_fp16(const uint16_t* w, const uint16_t* x, uint16_t* y, int in_f, int out_f) {
+    REQUIRE(w && x && y && in_f > 0 && out_f > 0, "matvec_fp16: bad arguments");
+    REQUIRE((in_f % 8) != 0 || (aligned(w, 16) && aligned(x, 16)), "matvec_fp16: buffers must be 16-byte aligned");
+    HIP_TRY(launch_matvec_f16(w, x, y, false, in_f, out_f, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_fp16_to_float(const uint16_t* w, const uint16_t* x, float* y, int in_f,
+                                                    int out_f) {
+    REQUIRE(w && x && y && in_f > 0 && out_f > 0, "matvec_fp16_to_float: bad arguments");
+    REQUIRE((in_f % 8) != 0 || (aligned(w, 16) && aligned(x, 16)), "matvec_fp16: buffers must be 16-byte aligned");
+    HIP_TRY(launch_matvec_f16(w, x, y, true, in_f, out_f, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, int n) {
+    REQUIRE(g && u && out && n > 0, "swiglu: bad arguments");
+    HIP_TRY(launch_swiglu(g, u, out, n, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_rope(uint16_t* data, int heads, int head_dim, int position, float theta) {
+    REQUIRE(data && heads > 0 && head_dim > 0 && head_dim % 2 == 0 && head_dim <= 2048, "rope: bad arguments");
+    HIP_TRY(launch_rope(data, heads, head_dim, position, theta, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_argmax(const float* logits, int n, int32_t* out_index) {
+    REQUIRE(logits && out_index && n > 0, "argmax: bad arguments");
+    HIP_TRY(launch_argmax(logits, n, out_index, g_stream));
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- events
+CITLALI_EXPORT int citlali_hip_event_create(void** ev) {
+    REQUIRE(ev, "null output pointer");
+    hipEvent_t e = nullptr;
+    HIP_TRY(hipEventCreate(&e));
+    *ev = e;
+    return CITLALI_OK;
+}
+CITLALI_EXPORT int citlali_hip_event_record(void* ev) {
+    REQUIRE(ev, "null event");
+    HIP_TRY(hipEventRecord(static_cast<hipEvent_t>(ev), g_stream));
+    return CITLALI_OK;
+}
+CITLALI_EXPORT int citlali_hip_event_synchronize(void* ev) {
+    REQUIRE(ev, "null event");
+    HIP_TRY(hipEventSynchronize(static_cast<hipEvent_t>(ev)));
+    return CITLALI_OK;
+}
+CITLALI_EXPORT int citlali_hip_event_elapsed_ms(void* a, void* b, float* ms) {
+    REQUIRE(a && b && ms, "null event");
+    HIP_TRY(hipEventElapsedTime(ms, static_cast<hipEvent_t>(a), static_cast<hipEvent_t>(b)));
+    return CITLALI_OK;
+}
+CITLALI_EXPORT int citlali_hip_event_destroy(void* ev) {
+    if (ev) HIP_TRY(hipEventDestroy(static_cast<hipEvent_t>(ev)));
+    return CITLALI_OK;
+}

@@ -1,0 +1,342 @@
+// attention.hip -- single-token decode attention over the per-layer fp16 KV
+// cache, split across workgroups (flash-decoding).
+//
+// Semantics follow kernels.cu:545-649 of the reference: for query head h
+// (kv head h / (heads/kv_heads)) and cached positions t = 0..position,
+// s_t = (q_h . K[t]) / sqrt(head_dim); p = softmax(s); out_h = sum_t p_t V[t],
+// fp32 arithmetic, fp16 output rounded nearest-even.  Cache layout is the
+// reference's [position][kv_head][head_dim] (kernels.cu:524-533).
+//
+// gfx950 design
+//  * One workgroup (4 waves) per (position chunk, kv head, sequence); it
+//    serves every query head of the GQA group, so K and V are read from HBM
+//    once per kv head (the reference re-reads them per query head).
+//  * Each wave streams tiles of positions: coalesced 128-bit loads of the K
+//    and V rows into registers, staged through a wave-private LDS tile, with
+//    the next tile's loads issued before the current tile is consumed.
+//  * Scores: lane = (position, head); q of the lane's head lives in VGPRs as
+//    fp16 pairs and v_dot2_f32_f16 accumulates in fp32.  The running max and
+//    sum of the online softmax are butterflies over the lanes of one head.
+//    Exponentials are taken in base 2 with log2(e) folded into the scale.
+//  * Values: lane = (head, 8-dim slice); p * V accumulates in fp32.
+//  * The four waves merge in LDS; a chunk writes (max, sum, acc[head_dim])
+//    per head, and a second small kernel merges chunks by log-sum-exp.  A
+//    sequence that fits one chunk is finished by the first kernel directly.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+#include <math.h>
+
+namespace citlali::hip {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWaves = kBlock / kWave;
+
+template <int HD, int GP>
+struct Cfg {
+    static_assert(HD == 64 || HD == 128, "head_dim");
+    static_assert(GP == 1 || GP == 2 || GP == 4 || GP == 8, "group");
+    static constexpr int kChunks = HD / 8;                 // 16-byte slices per row
+    static constexpr int kTP = (64 / GP) < 32 ? 64 / GP : 32;   // positions per tile
+    static constexpr int kStride = HD + 8;                 // padded LDS row (halves)
+    static constexpr int kRowsPerLoad = kWave / kChunks;
+    static constexpr int kLoads = kTP / kRowsPerLoad;      // per tile, for K and for V
+    static constexpr int kSlots = kWave / kChunks;         // head slots in the V phase
+    static constexpr int kHPL = GP > kSlots ? GP / kSlots : 1;
+    static constexpr int kPPar = GP < kSlots ? kSlots / GP : 1;
+    static constexpr int kTileHalves = kTP * kStride;
+    // wave-private region: K tile, V tile, p[GP][kTP], alpha[GP]; 16-byte multiple
+    static constexpr size_t kWaveLds =
+        (((size_t)kTileHalves * 2 * 2 + (size_t)GP * kTP * 4 + (size_t)GP * 4) + 15) & ~(size_t)15;
+    static_assert(kLoads >= 1, "tile");
+};
+
+template <int HD, int GP>
+size_t split_lds_bytes() {
+    using C = Cfg<HD, GP>;
+    const size_t tiles = C::kWaveLds * kWaves;
+    const size_t merge = (size_t)kWaves * GP * (HD + 2) * sizeof(float);
+    return tiles > merge ? tiles : merge;
+}
+
+// Grid: (chunk, kv_head, seq).  `positions` (device, per sequence) or the
+// scalar `position` gives the last cached position of each sequence.
+template <int HD, int GP>
+__global__ __launch_bounds__(kBlock) void attn_split_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
+    long long seq_stride, const int32_t* __restrict__ positions, int position, int heads, int kv_heads,
+    int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits, uint16_t* __restrict__ out) {
+    using C = Cfg<HD, GP>;
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int L = (positions ? positions[seq] : position) + 1;
+    const int b0 = split * chunk;
+    if (b0 >= L) return;
+    const int b1 = min(L, b0 + chunk);
+    const int n_valid = (L + chunk - 1) / chunk;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int sub = ((chunk / kWaves + C::kTP - 1) / C::kTP) * C::kTP;
+    const int w0 = min(b1, b0 + wave * sub);
+    const int w1 = min(b1, w0 + sub);
+
+    uint8_t* wl = smem + (size_t)wave * C::kWaveLds;
+    uint16_t* kt = reinterpret_cast<uint16_t*>(wl);
+    uint16_t* vt = kt + C::kTileHalves;
+    float* pt = reinterpret_cast<float*>(vt + C::kTileHalves);   // [GP][kTP]
+    float* at = pt + GP * C::kTP;                                 // [GP]
+
+    const uint16_t* kbase = k_cache + (size_t)seq * seq_stride + (size_t)kvh * HD;
+    const uint16_t* vbase = v_cache + (size_t)seq * seq_stride + (size_t)kvh * HD;
+    const size_t row_step = (size_t)kv_heads * HD;
+
+    // scores-phase identity
+    const int sh = lane % GP, sp = lane / GP;
+    const bool s_head_ok = sh < group;
+    const bool s_lane_ok = sp < C::kTP;
+    uint32_t qv[HD / 2];
+    {
+        const uint16_t* qh = q + ((size_t)seq * heads + (size_t)kvh * group + sh) * HD;
+#pragma unroll
+        for (int c = 0; c < C::kChunks; ++c) {
+            u32x4 v = {0u, 0u, 0u, 0u};
+            if (s_head_ok) v = *reinterpret_cast<const u32x4*>(qh + c * 8);
+            qv[4 * c + 0] = v.x; qv[4 * c + 1] = v.y; qv[4 * c + 2] = v.z; qv[4 * c + 3] = v.w;
+        }
+    }
+    // value-phase identity
+    const int vc = lane % C::kChunks, slot = lane / C::kChunks;
+    int vh[C::kHPL];
+#pragma unroll
+    for (int i = 0; i < C::kHPL; ++i) vh[i] = (C::kHPL == 1) ? (slot % GP) : (slot + C::kSlots * i);
+    const int vpp = (C::kHPL == 1) ? (slot / GP) : 0;
+    float acc[C::kHPL][8];
+#pragma unroll
+    for (int i = 0; i < C::kHPL; ++i)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[i][k] = 0.f;
+
+    float m_run = -INFINITY, l_run = 0.f;   // per scores lane (head sh)
+
+    // load identity
+    const int lrow = lane / C::kChunks, lc = lane % C::kChunks;
+    u32x4 kr[C::kLoads], vr[C::kLoads];
+    auto load_tile = [&](int t0) {
+#pragma unroll
+        for (int i = 0; i < C::kLoads; ++i) {
+            const int pos = t0 + i * C::kRowsPerLoad + lrow;
+            if (pos < w1) {
+                kr[i] = *reinterpret_cast<const u32x4*>(kbase + (size_t)pos * row_step + lc * 8);
+                vr[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pos * row_step + lc * 8);
+            }
+        }
+    };
+
+    if (w0 < w1) load_tile(w0);
+    for (int t0 = w0; t0 < w1; t0 += C::kTP) {
+        const int nv = min(C::kTP, w1 - t0);
+#pragma unroll
+        for (int i = 0; i < C::kLoads; ++i) {
+            const int r = i * C::kRowsPerLoad + lrow;
+            if (r < nv) {
+                *reinterpret_cast<u32x4*>(kt + r * C::kStride + lc * 8) = kr[i];
+                *reinterpret_cast<u32x4*>(vt + r * C::kStride + lc * 8) = vr[i];
+            }
+        }
+        wave_lds_sync();
+        if (t0 + C::kTP < w1) load_tile(t0 + C::kTP);
+
+        // ---- scores + online softmax (lane = position sp, head sh) ----
+        float s2 = -INFINITY;
+        if (s_lane_ok && s_head_ok && sp < nv) {
+            const uint16_t* kr_row = kt + sp * C::kStride;
+            float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+            for (int c = 0; c < C::kChunks; ++c) {
+                const u32x4 kk = *reinterpret_cast<const u32x4*>(kr_row + c * 8);
+                a0 = dot2(qv[4 * c + 0], kk.x, a0);
+                a1 = dot2(qv[4 * c + 1], kk.y, a1);
+                a0 = dot2(qv[4 * c + 2], kk.z, a0);
+                a1 = dot2(qv[4 * c + 3], kk.w, a1);
+            }
+            s2 = (a0 + a1) * scale_log2;
+        }
+        float mt = s2;
+#pragma unroll
+        for (int off = GP; off < kWave; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, kWave));
+        const float m_new = fmaxf(m_run, mt);
+        const bool live = m_new != -INFINITY;
+        const float alpha = live ? exp2f(m_run - m_new) : 1.f;
+        float pw = live ? exp2f(s2 - m_new) : 0.f;
+        float ps = pw;
+#pragma unroll
+        for (int off = GP; off < kWave; off <<= 1) ps += __shfl_xor(ps, off, kWave);
+        l_run = l_run * alpha + ps;
+        m_run = m_new;
+        if (s_lane_ok) pt[sh * C::kTP + sp] = pw;
+        if (sp == 0) at[sh] = alpha;
+        wave_lds_sync();
+
+        // ---- values (lane = head slot, 8-dim slice vc) ----
+#pragma unroll
+        for (int i = 0; i < C::kHPL; ++i) {
+            const float al = at[vh[i]];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[i][k] *= al;
+        }
+        for (int p = vpp; p < nv; p += C::kPPar) {
+            const u32x4 vv = *reinterpret_cast<const u32x4*>(vt + p * C::kStride + vc * 8);
+            const float v8[8] = {h2f(vv.x & 0xffffu), h2f(vv.x >> 16), h2f(vv.y & 0xffffu), h2f(vv.y >> 16),
+                                 h2f(vv.z & 0xffffu), h2f(vv.z >> 16), h2f(vv.w & 0xffffu), h2f(vv.w >> 16)};
+#pragma unroll
+            for (int i = 0; i < C::kHPL; ++i) {
+                const float pp = pt[vh[i] * C::kTP + p];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[i][k] = fmaf(pp, v8[k], acc[i][k]);
+            }
+        }
+        wave_lds_sync();
+    }
+
+    // combine the position-parallel partial sums of the value phase
+    if constexpr (C::kPPar > 1) {
+#pragma unroll
+        for (int off = GP * C::kChunks; off < kWave; off <<= 1)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) acc[0][k] += __shfl_xor(acc[0][k], off, kWave);
+    }
+
+    // ---- merge the four waves of the workgroup ----
+    __syncthreads();   // every wave is done with its tiles
+    float* ms = reinterpret_cast<float*>(smem);               // [kWaves][GP][HD + 2]
+    if (sp == 0) {
+        float* e = ms + ((size_t)wave * GP + sh) * (HD + 2);
+        e[HD] = m_run;
+        e[HD + 1] = l_run;
+    }
+    if (vpp == 0) {
+#pragma unroll
+        for (int i = 0; i < C::kHPL; ++i) {
+            float* e = ms + ((size_t)wave * GP + vh[i]) * (HD + 2) + vc * 8;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) e[k] = acc[i][k];
+        }
+    }
+    __syncthreads();
+
+    for (int idx = threadIdx.x; idx < group * HD; idx += kBlock) {
+        const int h = idx / HD, d = idx - h * HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ms[((size_t)w * GP + h) * (HD + 2) + HD]);
+        float Ls = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float* e = ms + ((size_t)w * GP + h) * (HD + 2);
+            const float f = e[HD] == -INFINITY ? 0.f : exp2f(e[HD] - M);
+            Ls += e[HD + 1] * f;
+            A += e[d] * f;
+        }
+        const int hq = kvh * group + h;
+        if (n_valid == 1) {
+            out[((size_t)seq * heads + hq) * HD + d] = f2h_rne(A / Ls);
+        } else {
+            float* pe = part + (((size_t)seq * heads + hq) * n_splits + split) * (HD + 2);
+            pe[d] = A;
+            if (d == 0) {
+                pe[HD] = M;
+                pe[HD + 1] = Ls;
+            }
+        }
+    }
+}
+
+// Grid: (head, seq); block: HD threads.  Log-sum-exp merge of the chunks.
+template <int HD>
+__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ part,
+                                                        const int32_t* __restrict__ positions, int position,
+                                                        int heads, int chunk, int n_splits,
+                                                        uint16_t* __restrict__ out) {
+    const int hq = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+    const int L = (positions ? positions[seq] : position) + 1;
+    const int n_valid = (L + chunk - 1) / chunk;
+    if (n_valid <= 1) return;   // finished by the split kernel
+    const float* pe = part + ((size_t)seq * heads + hq) * n_splits * (HD + 2);
+    float M = -INFINITY;
+    for (int s = 0; s < n_valid; ++s) M = fmaxf(M, pe[(size_t)s * (HD + 2) + HD]);
+    float Ls = 0.f, A = 0.f;
+    for (int s = 0; s < n_valid; ++s) {
+        const float* e = pe + (size_t)s * (HD + 2);
+        const float f = exp2f(e[HD] - M);
+        Ls += e[HD + 1] * f;
+        A += e[d] * f;
+    }
+    out[((size_t)seq * heads + hq) * HD + d] = f2h_rne(A / Ls);
+}
+
+template <int HD, int GP>
+hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
+    const size_t lds = split_lds_bytes<HD, GP>();
+    const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)HD));
+    hipLaunchKernelGGL((attn_split_kernel<HD, GP>), dim3(p.n_splits, a.kv_heads, a.nseq), dim3(kBlock), lds,
+                       stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions, a.position, a.heads,
+                       a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2, a.workspace, p.n_splits, a.out);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.n_splits <= 1) return e;
+    hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.heads, a.nseq), dim3(HD), 0, stream, a.workspace,
+                       a.positions, a.position, a.heads, p.chunk, p.n_splits, a.out);
+    return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_hd(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
+    switch (p.gp) {
+        case 1: return launch_split<HD, 1>(a, p, s);
+        case 2: return launch_split<HD, 2>(a, p, s);
+        case 4: return launch_split<HD, 4>(a, p, s);
+        case 8: return launch_split<HD, 8>(a, p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace
+
+bool attention_supported(int head_dim, int group) {
+    return (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 8;
+}
+
+// Work split: about `target_blocks` workgroups over all (sequence, kv head)
+// units, whole tiles per wave, chunk a multiple of 4 tiles.
+AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
+    AttnPlan p{};
+    const int group = heads / kv_heads;
+    p.gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
+    const int tp = (64 / p.gp) < 32 ? 64 / p.gp : 32;
+    const int quantum = tp * kWaves;
+    const long long units = (long long)nseq * kv_heads;
+    long long per_unit = (target_blocks + units - 1) / units;
+    if (per_unit < 1) per_unit = 1;
+    long long chunk = (max_len + per_unit - 1) / per_unit;
+    chunk = ((chunk + quantum - 1) / quantum) * quantum;
+    if (chunk < quantum) chunk = quantum;
+    p.chunk = (int)chunk;
+    p.n_splits = (int)((max_len + chunk - 1) / chunk);
+    (void)head_dim;
+    return p;
+}
+
+size_t attention_workspace_bytes(const AttnPlan& p, int nseq, int heads, int head_dim) {
+    if (p.n_splits <= 1) return 0;
+    return (size_t)nseq * heads * p.n_splits * (head_dim + 2) * sizeof(float);
+}
+
+hipError_t launch_attention(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
+    if (a.head_dim == 128) return launch_hd<128>(a, p, s);
+    if (a.head_dim == 64) return launch_hd<64>(a, p, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace citlali::hip

@@ -1,0 +1,97 @@
+// device_common.hpp -- small device helpers shared by the gfx950 kernels.
+//
+// All kernels are written for CDNA4 wave64.  fp16 values travel as uint16_t
+// bit patterns (the reference's convention, kernels.h:8-61).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace citlali::hip {
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+// A 16-byte vector that the compiler may only assume 4-byte aligned: used for
+// Q6_K super-blocks, which start on 2-byte boundaries.
+typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+
+constexpr int kWave = 64;
+constexpr int kQK = 256;          // values per K-quant super-block
+constexpr int kQ4KBytes = 144;    // d, dmin, scales[12], qs[128]
+constexpr int kQ6KBytes = 210;    // ql[128], qh[64], scales[16], d
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+// Nearest-even fp32 -> fp16 (v_cvt_f16_f32 under the default round mode):
+// the rule of the reference's device stores (__float2half, kernels.cu:21-24).
+__device__ __forceinline__ uint16_t f2h_rne(float f) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// The reference's host rule (dtype.cpp:136-176): nearest with ties away from
+// zero, NaN and overflow -> signed Inf, |x| < 2^-25 -> signed zero.  Used
+// where device output must equal the host dequant routines bit for bit.
+__device__ __forceinline__ uint16_t f2h_ties_away(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    const uint32_t s = (u >> 16) & 0x8000u;
+    const int e16 = static_cast<int>((u >> 23) & 0xffu) - 112;
+    const uint32_t frac = u & 0x7fffffu;
+    uint32_t h;
+    if (e16 >= 31) {
+        h = 0x7c00u;
+    } else if (e16 > 0) {
+        h = ((static_cast<uint32_t>(e16) << 10) | (frac >> 13)) + ((frac >> 12) & 1u);
+    } else if (e16 < -10) {
+        h = 0u;
+    } else {
+        const uint32_t sig = frac | 0x800000u;
+        const uint32_t sh = static_cast<uint32_t>(14 - e16);
+        h = (sig >> sh) + ((sig >> (sh - 1u)) & 1u);
+    }
+    return static_cast<uint16_t>(s | h);
+}
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
+// v_dot2_f32_f16: a.x*b.x + a.y*b.y + c with fp32 accumulation.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// Butterfly reductions over the 64 lanes of a wave (every lane gets the
+// result).  `Width` limits the butterfly to groups of that many lanes.
+template <int Width = kWave>
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = Width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+    return v;
+}
+
+template <int Width = kWave>
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = Width / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+    return v;
+}
+
+// Orders LDS traffic between lanes of one wave (no workgroup barrier): the
+// fence makes earlier LDS writes visible, the wave barrier stops the compiler
+// from moving memory operations across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Loads 4 bytes at a 2-byte aligned address as an aligned 8-byte window and
+// funnel-shifts: lo/hi are the dwords covering [a & ~3, (a & ~3) + 8).
+__device__ __forceinline__ uint32_t align_bytes(uint32_t lo, uint32_t hi, uint32_t shift_bytes) {
+    return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
+}
+
+}  // namespace citlali::hip

@@ -1,0 +1,251 @@
+// elementwise.hip -- the remaining kernels of one decode step
+// (kernels.cu:27-124, 381-533 of the reference) and a device greedy argmax.
+//
+// Arithmetic follows the reference: fp16 loads widened exactly, fp32 math,
+// fp16 stores rounded nearest-even.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+#include <math.h>
+
+namespace citlali::hip {
+namespace {
+
+constexpr int kBlk = 256;
+
+__global__ void store_kv_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+                                uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int position, int kv_size) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < kv_size) {
+        const size_t o = (size_t)position * kv_size + i;
+        kc[o] = k[i];
+        vc[o] = v[i];
+    }
+}
+
+__global__ void embed_f16_kernel(const uint16_t* __restrict__ t, int32_t token_id, uint16_t* __restrict__ out,
+                                 int hidden) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < hidden) out[i] = t[(size_t)token_id * hidden + i];
+}
+
+__global__ void copy_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = in[i];
+}
+
+__global__ void add_inplace_kernel(uint16_t* __restrict__ t, const uint16_t* __restrict__ d, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) t[i] = f2h_rne(h2f(t[i]) + h2f(d[i]));
+}
+
+// sum of squares over one block, result in every thread
+__device__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+    const int nw = blockDim.x / kWave;
+    for (int w = 0; w < nw; ++w) s += red[w];
+    __syncthreads();
+    return s;
+}
+
+// one block per vector (rms_norm: 1 vector; rms_norm_heads: `heads` vectors,
+// weight shared by all heads)
+__global__ void rms_norm_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ w,
+                                uint16_t* __restrict__ out, int n, float eps) {
+    __shared__ float red[16];
+    const size_t base = (size_t)blockIdx.x * n;
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = h2f(in[base + i]);
+        s += v * v;
+    }
+    s = block_sum(s, red);
+    const float inv = rsqrtf(s / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[base + i] = f2h_rne(h2f(in[base + i]) * inv * h2f(w[i]));
+}
+
+// NeoX pairs (i, i + hd/2), angle = position * theta^(-2i/hd) (kernels.cu:485-521)
+__global__ void rope_kernel(uint16_t* __restrict__ data, int head_dim, int position, float theta) {
+    const int head = blockIdx.x, i = threadIdx.x, half = head_dim / 2;
+    if (i >= half) return;
+    const size_t base = (size_t)head * head_dim;
+    const float inv_freq = powf(theta, -(float)(2 * i) / (float)head_dim);
+    const float angle = (float)position * inv_freq;
+    float s, c;
+    sincosf(angle, &s, &c);
+    const float x0 = h2f(data[base + i]), x1 = h2f(data[base + half + i]);
+    data[base + i] = f2h_rne(x0 * c - x1 * s);
+    data[base + half + i] = f2h_rne(x0 * s + x1 * c);
+}
+
+__global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,
+                              uint16_t* __restrict__ out, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float gv = h2f(g[i]);
+        out[i] = f2h_rne(gv / (1.0f + expf(-gv)) * h2f(u[i]));
+    }
+}
+
+// fp16 weights [N][K] (the DequantizeToFp16 path): one wave per row, 128-bit
+// loads when K is a multiple of 8, fp32 accumulation.
+template <bool kF32>
+__global__ __launch_bounds__(kBlk) void matvec_f16_kernel(const uint16_t* __restrict__ w,
+                                                          const uint16_t* __restrict__ x, void* __restrict__ y,
+                                                          int K, int N) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int row = blockIdx.x * (kBlk / kWave) + threadIdx.x / kWave;
+    if (row >= N) return;
+    const uint16_t* r = w + (size_t)row * K;
+    float a = 0.f;
+    if ((K & 7) == 0) {
+        for (int k = lane * 8; k < K; k += kWave * 8) {
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(r + k);
+            const u32x4 xv = *reinterpret_cast<const u32x4*>(x + k);
+            a = dot2(wv.x, xv.x, a);
+            a = dot2(wv.y, xv.y, a);
+            a = dot2(wv.z, xv.z, a);
+            a = dot2(wv.w, xv.w, a);
+        }
+    } else {
+        for (int k = lane; k < K; k += kWave) a = fmaf(h2f(r[k]), h2f(x[k]), a);
+    }
+    a = wave_sum(a);
+    if (lane == 0) {
+        if constexpr (kF32) static_cast<float*>(y)[row] = a;
+        else static_cast<uint16_t*>(y)[row] = f2h_rne(a);
+    }
+}
+
+// Greedy argmax with the host rule of qwen_model.cpp:455-463: the first
+// (lowest index) strictly greatest finite value wins; all non-finite -> 0.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                      int32_t* __restrict__ out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = logits[i];
+        if (isfinite(v) && (v > best || (v == best && i < idx))) {
+            best = v;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, kWave);
+        const int oi = __shfl_xor(idx, off, kWave);
+        if (ov > best || (ov == best && oi < idx)) {
+            best = ov;
+            idx = oi;
+        }
+    }
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    if (lane == 0) {
+        bv[wave] = best;
+        bi[wave] = idx;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = -INFINITY;
+        int id = 0x7fffffff;
+        for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
+            if (bv[w] > b || (bv[w] == b && bi[w] < id)) {
+                b = bv[w];
+                id = bi[w];
+            }
+        }
+        out[0] = (id == 0x7fffffff) ? 0 : id;
+    }
+}
+
+__global__ void fill_zero_kernel(uint32_t* __restrict__ p, size_t nwords) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nwords; i += stride) p[i] = 0u;
+}
+
+__global__ void fill_zero_bytes_kernel(uint8_t* __restrict__ p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+inline dim3 grid_for(int n) { return dim3((unsigned)((n + kBlk - 1) / kBlk)); }
+
+}  // namespace
+
+hipError_t launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc, int position,
+                           int kv_size, hipStream_t s) {
+    hipLaunchKernelGGL(store_kv_kernel, grid_for(kv_size), dim3(kBlk), 0, s, k, v, kc, vc, position, kv_size);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_f16(const uint16_t* t, int32_t token_id, uint16_t* out, int hidden, hipStream_t s) {
+    hipLaunchKernelGGL(embed_f16_kernel, grid_for(hidden), dim3(kBlk), 0, s, t, token_id, out, hidden);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy(const uint16_t* in, uint16_t* out, int n, hipStream_t s) {
+    hipLaunchKernelGGL(copy_kernel, grid_for(n), dim3(kBlk), 0, s, in, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_inplace(uint16_t* t, const uint16_t* d, int n, hipStream_t s) {
+    hipLaunchKernelGGL(add_inplace_kernel, grid_for(n), dim3(kBlk), 0, s, t, d, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, int n, float eps, hipStream_t s) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(1024), 0, s, in, w, out, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_heads(const uint16_t* in, const uint16_t* w, uint16_t* out, int heads, int head_dim,
+                                 float eps, hipStream_t s) {
+    hipLaunchKernelGGL(rms_norm_kernel, dim3(heads), dim3(kWave * 2), 0, s, in, w, out, head_dim, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(uint16_t* data, int heads, int head_dim, int position, float theta, hipStream_t s) {
+    const int threads = ((head_dim / 2 + kWave - 1) / kWave) * kWave;
+    hipLaunchKernelGGL(rope_kernel, dim3(heads), dim3(threads), 0, s, data, head_dim, position, theta);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, int n, hipStream_t s) {
+    hipLaunchKernelGGL(swiglu_kernel, grid_for(n), dim3(kBlk), 0, s, g, u, out, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                             hipStream_t s) {
+    const dim3 g((unsigned)((N + (kBlk / kWave) - 1) / (kBlk / kWave)));
+    if (f32_out) hipLaunchKernelGGL(matvec_f16_kernel<true>, g, dim3(kBlk), 0, s, w, x, y, K, N);
+    else hipLaunchKernelGGL(matvec_f16_kernel<false>, g, dim3(kBlk), 0, s, w, x, y, K, N);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, out_index);
+    return hipGetLastError();
+}
+
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
+    if (bytes == 0) return hipSuccess;
+    if (((uintptr_t)p & 3u) == 0 && (bytes & 3u) == 0) {
+        const size_t words = bytes / 4;
+        size_t blocks = (words + kBlk - 1) / kBlk;
+        if (blocks > 65536) blocks = 65536;
+        hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(kBlk), 0, s, (uint32_t*)p, words);
+    } else {
+        size_t blocks = (bytes + kBlk - 1) / kBlk;
+        hipLaunchKernelGGL(fill_zero_bytes_kernel, dim3((unsigned)blocks), dim3(kBlk), 0, s, (uint8_t*)p, bytes);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace citlali::hip

@@ -1,0 +1,62 @@
+// launch.hpp -- internal launchers of the gfx950 kernels, called by the
+// C-ABI layer (csrc/abi/citlali_hip.hip) after it has validated arguments.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace citlali::hip {
+
+// ---- fused dequant GEMV (matvec_kquant.hip) ----
+size_t matvec_lds_bytes(int kind, int K);
+hipError_t launch_matvec_q4k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                             hipStream_t s);
+hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                             hipStream_t s);
+
+// ---- decode attention (attention.hip) ----
+struct AttnArgs {
+    const uint16_t* q;         // [nseq][heads][head_dim]
+    const uint16_t* k_cache;   // sequence s at k_cache + s*seq_stride: [pos][kv_heads][head_dim]
+    const uint16_t* v_cache;
+    long long seq_stride;      // elements
+    const int32_t* positions;  // device [nseq] or null (then `position`)
+    int position;
+    int nseq, heads, kv_heads, head_dim;
+    float* workspace;          // chunk partials, attention_workspace_bytes()
+    uint16_t* out;             // [nseq][heads][head_dim]
+};
+struct AttnPlan {
+    int gp;        // padded GQA group (1, 2, 4, 8)
+    int chunk;     // positions per workgroup
+    int n_splits;  // chunks of the longest sequence
+};
+bool attention_supported(int head_dim, int group);
+AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks);
+size_t attention_workspace_bytes(const AttnPlan& p, int nseq, int heads, int head_dim);
+hipError_t launch_attention(const AttnArgs& a, const AttnPlan& p, hipStream_t s);
+
+// ---- embedding / dequant (dequant.hip) ----
+hipError_t launch_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden, hipStream_t s);
+hipError_t launch_dequant_q4k_f16(const uint8_t* w, uint64_t count, uint16_t* out, hipStream_t s);
+hipError_t launch_dequant_q6k_f16(const uint8_t* w, uint64_t count, uint16_t* out, hipStream_t s);
+
+// ---- the rest of the decode step (elementwise.hip) ----
+hipError_t launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc, int position,
+                           int kv_size, hipStream_t s);
+hipError_t launch_embed_f16(const uint16_t* table, int32_t token_id, uint16_t* out, int hidden, hipStream_t s);
+hipError_t launch_copy(const uint16_t* in, uint16_t* out, int n, hipStream_t s);
+hipError_t launch_add_inplace(uint16_t* t, const uint16_t* d, int n, hipStream_t s);
+hipError_t launch_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, int n, float eps,
+                           hipStream_t s);
+hipError_t launch_rms_norm_heads(const uint16_t* in, const uint16_t* w, uint16_t* out, int heads, int head_dim,
+                                 float eps, hipStream_t s);
+hipError_t launch_rope(uint16_t* data, int heads, int head_dim, int position, float theta, hipStream_t s);
+hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, int n, hipStream_t s);
+hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                             hipStream_t s);
+hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s);
+hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
+
+}  // namespace citlali::hip

@@ -1,0 +1,385 @@
+// matvec_kquant.hip -- fused dequant + GEMV for raw GGUF Q4_K / Q6_K rows.
+//
+// Semantics follow kernels.cu:195-338 of the reference: y[row] = sum over the
+// row's 256-value super-blocks of value(e) * x[256*b + e], where value(e) is
+// the exact fp32 dequantised weight (never rounded to fp16) and the sum is
+// accumulated in fp32; fp16 outputs are rounded nearest-even.
+//
+// gfx950 design
+//  * Four lanes own one super-block; a wave covers 16 consecutive
+//    super-blocks per step.  A Q4_K lane reads the 16-byte header and its
+//    32 bytes of quants (group pair j = lane&3) with 128-bit loads; a Q6_K
+//    lane (half h, 16-value slice ih) reads its three 16-byte byte ranges
+//    through dword-aligned windows, because 210-byte blocks start on 2-byte
+//    boundaries.
+//  * The block stages x once in LDS, with every run of four values stored as
+//    (x0, x2, x1, x3), so that a 32-bit quant word splits into half2 operands
+//    with one AND (bytes 0/2) or one shift + AND (bytes 1/3).  Quant codes
+//    are placed in the mantissa of an fp16 with a zero exponent (value =
+//    code * 2^-24, exact), which v_dot2_f32_f16 multiplies by the matching
+//    x pair and accumulates in fp32 -- no per-value int->float conversion.
+//  * The per-group offset terms (Q4_K "- dmin*m", Q6_K "- 32") need
+//    sum(x) over each group; the block computes those sums while staging x.
+//  * No MFMA: M = 1 is not a dense contraction.  The bound is HBM.
+#include "device_common.hpp"
+#include "launch.hpp"
+
+namespace citlali::hip {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / kWave;
+constexpr int kSbPerStep = 16;   // super-blocks per wave step (4 lanes each)
+constexpr int kBatch = 4;        // wave steps whose loads are issued together
+
+// ---------------------------------------------------------------------------
+// x staging: permuted fp16 pairs + per-group sums.
+// ---------------------------------------------------------------------------
+
+// Q4_K lanes need sum(x) over each 32-value group (index b*8 + g).
+// Q6_K lanes need sum(x) over 16-value slices, stored in the order
+// [b][h][ih][k] so one lane's four slices are contiguous.
+template <bool kQ6>
+__device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int K, uint32_t* xp, float* sx) {
+    const int n8 = K >> 3;
+    for (int v8 = threadIdx.x; v8 < n8; v8 += kBlock) {
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(x + (size_t)v8 * 8);
+        u32x4 perm;
+        perm.x = __builtin_amdgcn_perm(raw.y, raw.x, 0x05040100u);
+        perm.y = __builtin_amdgcn_perm(raw.y, raw.x, 0x07060302u);
+        perm.z = __builtin_amdgcn_perm(raw.w, raw.z, 0x05040100u);
+        perm.w = __builtin_amdgcn_perm(raw.w, raw.z, 0x07060302u);
+        *reinterpret_cast<u32x4*>(xp + (size_t)v8 * 4) = perm;
+        float s = 0.f;
+        s += h2f(raw.x & 0xffffu) + h2f(raw.x >> 16);
+        s += h2f(raw.y & 0xffffu) + h2f(raw.y >> 16);
+        s += h2f(raw.z & 0xffffu) + h2f(raw.z >> 16);
+        s += h2f(raw.w & 0xffffu) + h2f(raw.w >> 16);
+        if constexpr (!kQ6) {
+            // four consecutive threads hold one 32-value group (256 % 4 == 0)
+            s += __shfl_xor(s, 1, kWave);
+            s += __shfl_xor(s, 2, kWave);
+            if ((v8 & 3) == 0) sx[v8 >> 2] = s;
+        } else {
+            s += __shfl_xor(s, 1, kWave);
+            if ((v8 & 1) == 0) {
+                const int v = v8 * 8;
+                const int b = v >> 8, in = v & 255;
+                const int h = in >> 7, k = (in & 127) >> 5, ih = (in & 31) >> 4;
+                sx[b * 16 + h * 8 + ih * 4 + k] = s;
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K: d(f16) dmin(f16) scales[12] qs[128]   (weight_loader.cpp:150-161)
+// ---------------------------------------------------------------------------
+struct Q4K {
+    static constexpr int kBytes = kQ4KBytes;
+    static constexpr int kSxPerBlock = 8;
+    struct Frag { u32x4 hdr, q0, q1; };
+
+    __device__ static __forceinline__ Frag load(const uint8_t* sb, int j) {
+        Frag f;
+        f.hdr = *reinterpret_cast<const u32x4*>(sb);
+        f.q0 = *reinterpret_cast<const u32x4*>(sb + 16 + 32 * j);
+        f.q1 = *reinterpret_cast<const u32x4*>(sb + 32 + 32 * j);
+        return f;
+    }
+
+    // Contribution of lane j (group pair 2j, 2j+1) of super-block b.
+    __device__ static __forceinline__ float dot(const Frag& f, int j, const uint32_t* xp, const float* sx, int b) {
+        // 6-bit (scale, min) codes of groups 2j, 2j+1 (kernels.cu:174-186):
+        // work on the two bytes k, k+1 of each 4-byte scale word at once.
+        const uint32_t sh = (uint32_t)((2 * j) & 3) * 8u;
+        const uint32_t a = (f.hdr.y >> sh) & 0xffffu;   // scales[k], [k+1]
+        const uint32_t bq = (f.hdr.z >> sh) & 0xffffu;  // scales[k+4], [k+5]
+        const uint32_t c = (f.hdr.w >> sh) & 0xffffu;   // scales[k+8], [k+9]
+        uint32_t sc, mn;
+        if (j < 2) {
+            sc = a & 0x3f3fu;
+            mn = bq & 0x3f3fu;
+        } else {
+            sc = (c & 0x0f0fu) | ((a >> 2) & 0x3030u);
+            mn = ((c >> 4) & 0x0f0fu) | ((bq >> 2) & 0x3030u);
+        }
+        const float d = h2f(f.hdr.x & 0xffffu);
+        const float dmin = h2f(f.hdr.x >> 16);
+
+        const uint32_t* xl = xp + ((b * kQK + 64 * j) >> 1);
+        const u32x4 xl0 = *reinterpret_cast<const u32x4*>(xl + 0);
+        const u32x4 xl1 = *reinterpret_cast<const u32x4*>(xl + 4);
+        const u32x4 xl2 = *reinterpret_cast<const u32x4*>(xl + 8);
+        const u32x4 xl3 = *reinterpret_cast<const u32x4*>(xl + 12);
+        const u32x4 xh0 = *reinterpret_cast<const u32x4*>(xl + 16);
+        const u32x4 xh1 = *reinterpret_cast<const u32x4*>(xl + 20);
+        const u32x4 xh2 = *reinterpret_cast<const u32x4*>(xl + 24);
+        const u32x4 xh3 = *reinterpret_cast<const u32x4*>(xl + 28);
+        const uint32_t q[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
+        const uint32_t XL[16] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w,
+                                 xl2.x, xl2.y, xl2.z, xl2.w, xl3.x, xl3.y, xl3.z, xl3.w};
+        const uint32_t XH[16] = {xh0.x, xh0.y, xh0.z, xh0.w, xh1.x, xh1.y, xh1.z, xh1.w,
+                                 xh2.x, xh2.y, xh2.z, xh2.w, xh3.x, xh3.y, xh3.z, xh3.w};
+        float plo = 0.f, phi = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t w = q[t];
+            const uint32_t w8 = w >> 8;
+            plo = dot2(w & 0x000f000fu, XL[2 * t], plo);       // q * 2^-24
+            plo = dot2(w8 & 0x000f000fu, XL[2 * t + 1], plo);
+            phi = dot2(w & 0x00f000f0u, XH[2 * t], phi);       // q * 2^-20
+            phi = dot2(w8 & 0x00f000f0u, XH[2 * t + 1], phi);
+        }
+        const f32x2 s = *reinterpret_cast<const f32x2*>(sx + b * 8 + 2 * j);
+        const float a_lo = d * (float)(sc & 0xffu) * 16777216.0f;
+        const float a_hi = d * (float)(sc >> 8) * 1048576.0f;
+        const float m_lo = dmin * (float)(mn & 0xffu);
+        const float m_hi = dmin * (float)(mn >> 8);
+        return (a_lo * plo - m_lo * s.x) + (a_hi * phi - m_hi * s.y);
+    }
+};
+
+// ---------------------------------------------------------------------------
+// Q6_K: ql[128] qh[64] scales int8[16] d(f16)   (weight_loader.cpp:247-257)
+// ---------------------------------------------------------------------------
+struct Q6K {
+    static constexpr int kBytes = kQ6KBytes;
+    static constexpr int kSxPerBlock = 16;
+    struct Frag { uint32_t wa[4], wb[4], u[4]; uint32_t s0, s1, dbits; };
+
+    // 16 bytes at a 2-byte aligned address `p`, through the dword-aligned
+    // window [p - s, p - s + 20), s = p & 3 in {0, 2}.  The window never
+    // leaves the super-block for the ranges used here.
+    __device__ static __forceinline__ void load16(const uint8_t* p, uint32_t s, uint32_t out[4]) {
+        const uint8_t* base = p - s;
+        const u32x4 v = *reinterpret_cast<const u32x4_a4*>(base);
+        const uint32_t e = *reinterpret_cast<const uint32_t*>(base + 16);
+        const uint32_t sb = s;  // bytes
+        out[0] = align_bytes(v.x, v.y, sb);
+        out[1] = align_bytes(v.y, v.z, sb);
+        out[2] = align_bytes(v.z, v.w, sb);
+        out[3] = align_bytes(v.w, e, sb);
+    }
+
+    // lane_in_sb = 2*h + ih
+    __device__ static __forceinline__ Frag load(const uint8_t* sb, int l4) {
+        const int h = l4 >> 1, ih = l4 & 1;
+        const uint32_t s = (uint32_t)((uintptr_t)sb & 3u);
+        Frag f;
+        load16(sb + 64 * h + 16 * ih, s, f.wa);
+        load16(sb + 64 * h + 32 + 16 * ih, s, f.wb);
+        load16(sb + 128 + 32 * h + 16 * ih, s, f.u);
+        // scales[8h .. 8h+8): dword window starting 4 - s bytes before them
+        // (ends at most at byte 210 of the block)
+        const uint8_t* sw = sb + 192 + 8 * h - (4 - s);
+        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(sw);
+        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(sw + 4);
+        const uint32_t w2 = *reinterpret_cast<const uint32_t*>(sw + 8);
+        f.s0 = s ? align_bytes(w0, w1, 2u) : w1;
+        f.s1 = s ? align_bytes(w1, w2, 2u) : w2;
+        f.dbits = *reinterpret_cast<const uint16_t*>(sb + 208);
+        return f;
+    }
+
+    __device__ static __forceinline__ float dot(const Frag& f, int l4, const uint32_t* xp, const float* sx, int b) {
+        const int h = l4 >> 1, ih = l4 & 1;
+        const float d = h2f((uint16_t)f.dbits);
+        // int8 scales sc[8h + ih + 2k], k = 0..3 (kernels.cu:166-167)
+        const uint32_t sh = (uint32_t)ih * 8u;
+        const float sc0 = (float)__builtin_amdgcn_sbfe(f.s0, sh, 8u);
+        const float sc1 = (float)__builtin_amdgcn_sbfe(f.s0, sh + 16u, 8u);
+        const float sc2 = (float)__builtin_amdgcn_sbfe(f.s1, sh, 8u);
+        const float sc3 = (float)__builtin_amdgcn_sbfe(f.s1, sh + 16u, 8u);
+
+        // x pairs of slice k: values 128h + 32k + 16ih + [0,16)
+        const uint32_t* xb = xp + ((b * kQK + 128 * h + 16 * ih) >> 1);
+        float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t wa = f.wa[t], wb = f.wb[t], u = f.u[t];
+            const uint32_t wa8 = wa >> 8, wb8 = wb >> 8, u8 = u >> 8;
+            // 6-bit code = low nibble (ql) | two qh bits << 4, in bits 0..5
+            // of each fp16 half (bytes 0/2 of the word, then bytes 1/3).
+            const uint32_t c0a = (wa & 0x000f000fu) | ((u << 4) & 0x00300030u);
+            const uint32_t c0b = (wa8 & 0x000f000fu) | ((u8 << 4) & 0x00300030u);
+            const uint32_t c1a = (wb & 0x000f000fu) | ((u << 2) & 0x00300030u);
+            const uint32_t c1b = (wb8 & 0x000f000fu) | ((u8 << 2) & 0x00300030u);
+            const uint32_t c2a = ((wa >> 4) & 0x000f000fu) | (u & 0x00300030u);
+            const uint32_t c2b = ((wa8 >> 4) & 0x000f000fu) | (u8 & 0x00300030u);
+            const uint32_t c3a = ((wb >> 4) & 0x000f000fu) | ((u >> 2) & 0x00300030u);
+            const uint32_t c3b = ((wb8 >> 4) & 0x000f000fu) | ((u8 >> 2) & 0x00300030u);
+            const u32x2 x0 = *reinterpret_cast<const u32x2*>(xb + 0 * 16 + 2 * t);
+            const u32x2 x1 = *reinterpret_cast<const u32x2*>(xb + 1 * 16 + 2 * t);
+            const u32x2 x2 = *reinterpret_cast<const u32x2*>(xb + 2 * 16 + 2 * t);
+            const u32x2 x3 = *reinterpret_cast<const u32x2*>(xb + 3 * 16 + 2 * t);
+            p0 = dot2(c0b, x0.y, dot2(c0a, x0.x, p0));
+            p1 = dot2(c1b, x1.y, dot2(c1a, x1.x, p1));
+            p2 = dot2(c2b, x2.y, dot2(c2a, x2.x, p2));
+            p3 = dot2(c3b, x3.y, dot2(c3a, x3.x, p3));
+        }
+        const f32x4 s = *reinterpret_cast<const f32x4*>(sx + b * 16 + h * 8 + ih * 4);
+        // sum (q6 - 32) x = 2^24 P - 32 S
+        const float t0 = sc0 * (p0 * 16777216.0f - 32.0f * s.x);
+        const float t1 = sc1 * (p1 * 16777216.0f - 32.0f * s.y);
+        const float t2 = sc2 * (p2 * 16777216.0f - 32.0f * s.z);
+        const float t3 = sc3 * (p3 * 16777216.0f - 32.0f * s.w);
+        return d * ((t0 + t1) + (t2 + t3));
+    }
+};
+
+template <bool kF32>
+__device__ __forceinline__ void store_y(void* y, int row, float v) {
+    if constexpr (kF32) {
+        static_cast<float*>(y)[row] = v;
+    } else {
+        static_cast<uint16_t*>(y)[row] = f2h_rne(v);
+    }
+}
+
+// Rows whose super-block count is a multiple of 16: every wave step stays
+// inside one row, so the row of a step is wave-uniform.
+template <class QT, bool kF32>
+__global__ __launch_bounds__(kBlock) void matvec_rows16_kernel(const uint8_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ x,
+                                                               void* __restrict__ y, int K, int N,
+                                                               int rows_per_wave) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
+    float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
+    stage_x<QT::kSxPerBlock == 16>(x, K, xp, sx);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int l4 = lane & 3;
+    const int sub = lane >> 2;
+    const int nb = K >> 8;
+    const int steps_per_row = nb / kSbPerStep;
+    const int row0 = (blockIdx.x * kWavesPerBlock + wave) * rows_per_wave;
+    const int rows = min(rows_per_wave, N - row0);
+    const int total = rows * steps_per_row;
+
+    float acc = 0.f;
+    for (int t0 = 0; t0 < total; t0 += kBatch) {
+        typename QT::Frag fr[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int t = t0 + u;
+            if (t < total) {
+                const int r = t / steps_per_row;
+                const int i = t - r * steps_per_row;
+                const size_t f = (size_t)(row0 + r) * nb + (size_t)i * kSbPerStep + sub;
+                fr[u] = QT::load(w + f * QT::kBytes, l4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const int t = t0 + u;
+            if (t < total) {
+                const int r = t / steps_per_row;
+                const int i = t - r * steps_per_row;
+                acc += QT::dot(fr[u], l4, xp, sx, i * kSbPerStep + sub);
+                if (i == steps_per_row - 1) {
+                    const float s = wave_sum(acc);
+                    if (lane == 0) store_y<kF32>(y, row0 + r, s);
+                    acc = 0.f;
+                }
+            }
+        }
+    }
+}
+
+// Any super-block count: a wave owns kRows rows and walks their super-blocks
+// as one flat list; a lane's row is found by multiply-high division.
+template <class QT, bool kF32, int kRows>
+__global__ __launch_bounds__(kBlock) void matvec_flat_kernel(const uint8_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ x,
+                                                             void* __restrict__ y, int K, int N,
+                                                             uint32_t magic) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
+    float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
+    stage_x<QT::kSxPerBlock == 16>(x, K, xp, sx);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int l4 = lane & 3;
+    const int sub = lane >> 2;
+    const int nb = K >> 8;
+    const int row0 = (blockIdx.x * kWavesPerBlock + wave) * kRows;
+    const int rows = min(kRows, N - row0);
+    const int nflat = rows > 0 ? rows * nb : 0;
+
+    float acc[kRows];
+#pragma unroll
+    for (int k = 0; k < kRows; ++k) acc[k] = 0.f;
+
+    for (int f0 = 0; f0 < nflat; f0 += kBatch * kSbPerStep) {
+        typename QT::Frag fr[kBatch];
+        int rl[kBatch], bl[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            const uint32_t f = (uint32_t)(f0 + u * kSbPerStep + sub);
+            const uint32_t r = __umulhi(f, magic);
+            rl[u] = (int)f < nflat ? (int)r : -1;
+            bl[u] = (int)(f - r * (uint32_t)nb);
+            if (rl[u] >= 0) fr[u] = QT::load(w + ((size_t)row0 * nb + f) * QT::kBytes, l4);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+            if (rl[u] >= 0) {
+                const float c = QT::dot(fr[u], l4, xp, sx, bl[u]);
+#pragma unroll
+                for (int k = 0; k < kRows; ++k) acc[k] += (rl[u] == k) ? c : 0.f;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kRows; ++k) {
+        const float s = wave_sum(acc[k]);
+        if (lane == 0 && k < rows) store_y<kF32>(y, row0 + k, s);
+    }
+}
+
+template <class QT, bool kF32>
+hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, int N, hipStream_t stream) {
+    const int nb = K / kQK;
+    const size_t lds = (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float);
+    if (nb % kSbPerStep == 0) {
+        // aim for >= 512 blocks, up to 8 rows per wave
+        int rpw = N / (kWavesPerBlock * 512);
+        rpw = rpw < 1 ? 1 : (rpw > 8 ? 8 : rpw);
+        const int rows_per_block = rpw * kWavesPerBlock;
+        const int grid = (N + rows_per_block - 1) / rows_per_block;
+        hipLaunchKernelGGL((matvec_rows16_kernel<QT, kF32>), dim3(grid), dim3(kBlock), lds, stream, w, x, y, K,
+                           N, rpw);
+    } else {
+        // smallest row count per wave that keeps whole 16-block steps busy
+        constexpr int kRows = 4;
+        const uint32_t magic = (uint32_t)((((uint64_t)1) << 32) / (uint64_t)nb + 1u);
+        const int rows_per_block = kRows * kWavesPerBlock;
+        const int grid = (N + rows_per_block - 1) / rows_per_block;
+        hipLaunchKernelGGL((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x, y,
+                           K, N, magic);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t matvec_lds_bytes(int kind, int K) {
+    return (size_t)K * 2 + (size_t)(K / kQK) * (kind == 6 ? 16 : 8) * sizeof(float);
+}
+
+hipError_t launch_matvec_q4k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                             hipStream_t s) {
+    return f32_out ? launch_matvec<Q4K, true>(w, x, y, K, N, s) : launch_matvec<Q4K, false>(w, x, y, K, N, s);
+}
+
+hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                             hipStream_t s) {
+    return f32_out ? launch_matvec<Q6K, true>(w, x, y, K, N, s) : launch_matvec<Q6K, false>(w, x, y, K, N, s);
+}
+
+}  // namespace citlali::hip

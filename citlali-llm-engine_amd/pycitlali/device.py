@@ -1,0 +1,141 @@
+"""Device memory and thin call wrappers over the C ABI.
+
+DeviceArray mirrors the reference's DeviceBuffer (tensor.h:10-54): it owns
+one device allocation, copies from/to host numpy arrays and frees on close.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+
+
+class DeviceArray:
+    def __init__(self, nbytes: int):
+        lib = _lib.load()
+        p = ctypes.c_void_p()
+        _lib.check(lib.citlali_hip_malloc(ctypes.byref(p), ctypes.c_size_t(int(nbytes))))
+        self.ptr = p.value or 0
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_numpy(cls, arr: np.ndarray) -> "DeviceArray":
+        arr = np.ascontiguousarray(arr)
+        d = cls(arr.nbytes)
+        d.upload(arr)
+        return d
+
+    def upload(self, arr: np.ndarray, offset: int = 0) -> None:
+        arr = np.ascontiguousarray(arr)
+        if offset + arr.nbytes > self.nbytes:
+            raise ValueError("upload exceeds the allocation")
+        _lib.call("citlali_hip_memcpy_h2d", ctypes.c_void_p(self.ptr + offset), arr.ctypes.data_as(ctypes.c_void_p),
+                  ctypes.c_size_t(arr.nbytes))
+
+    def download(self, dtype, count: int | None = None, offset: int = 0) -> np.ndarray:
+        dtype = np.dtype(dtype)
+        if count is None:
+            count = (self.nbytes - offset) // dtype.itemsize
+        out = np.empty(count, dtype=dtype)
+        if offset + out.nbytes > self.nbytes:
+            raise ValueError("download exceeds the allocation")
+        _lib.call("citlali_hip_memcpy_d2h", out.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(self.ptr + offset),
+                  ctypes.c_size_t(out.nbytes))
+        return out
+
+    def zero(self) -> None:
+        _lib.call("citlali_hip_zero", ctypes.c_void_p(self.ptr), ctypes.c_size_t(self.nbytes))
+
+    def at(self, offset: int) -> ctypes.c_void_p:
+        return ctypes.c_void_p(self.ptr + offset)
+
+    @property
+    def vp(self) -> ctypes.c_void_p:
+        return ctypes.c_void_p(self.ptr)
+
+    def close(self) -> None:
+        if self.ptr:
+            _lib.load().citlali_hip_free(ctypes.c_void_p(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def synchronize() -> None:
+    _lib.call("citlali_hip_synchronize")
+
+
+class Event:
+    def __init__(self):
+        p = ctypes.c_void_p()
+        _lib.check(_lib.load().citlali_hip_event_create(ctypes.byref(p)))
+        self.h = p
+
+    def record(self) -> None:
+        _lib.call("citlali_hip_event_record", self.h)
+
+    def synchronize(self) -> None:
+        _lib.call("citlali_hip_event_synchronize", self.h)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        _lib.check(_lib.load().citlali_hip_event_elapsed_ms(self.h, end.h, ctypes.byref(ms)))
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            _lib.load().citlali_hip_event_destroy(self.h)
+        except Exception:
+            pass
+
+
+def _vp(x) -> ctypes.c_void_p:
+    if isinstance(x, DeviceArray):
+        return x.vp
+    if isinstance(x, ctypes.c_void_p):
+        return x
+    return ctypes.c_void_p(int(x))
+
+
+def matvec(kind: str, w, x, y, in_features: int, out_features: int, f32_out: bool = False) -> None:
+    """kind in {"q4k", "q6k", "fp16"}; y fp16 unless f32_out."""
+    name = {("q4k", False): "citlali_hip_matvec_q4k", ("q4k", True): "citlali_hip_matvec_q4k_to_float",
+            ("q6k", False): "citlali_hip_matvec_q6k", ("q6k", True): "citlali_hip_matvec_q6k_to_float",
+            ("fp16", False): "citlali_hip_matvec_fp16", ("fp16", True): "citlali_hip_matvec_fp16_to_float"}[
+        (kind, bool(f32_out))]
+    _lib.call(name, _vp(w), _vp(x), _vp(y), int(in_features), int(out_features))
+
+
+def attention(q, k_cache, v_cache, scores, out, position: int, max_context: int, heads: int, kv_heads: int,
+              head_dim: int) -> None:
+    _lib.call("citlali_hip_attention", _vp(q), _vp(k_cache), _vp(v_cache),
+              _vp(scores) if scores is not None else ctypes.c_void_p(0), _vp(out), int(position), int(max_context),
+              int(heads), int(kv_heads), int(head_dim))
+
+
+def attention_workspace_bytes(max_positions_bound: int, nseq: int, heads: int, kv_heads: int, head_dim: int) -> int:
+    return int(_lib.load().citlali_hip_attention_workspace_bytes(int(max_positions_bound), int(nseq), int(heads),
+                                                                 int(kv_heads), int(head_dim)))
+
+
+def attention_batched(q, k_cache, v_cache, seq_stride: int, positions, max_positions_bound: int, nseq: int,
+                      heads: int, kv_heads: int, head_dim: int, workspace, workspace_bytes: int, out) -> None:
+    _lib.call("citlali_hip_attention_batched", _vp(q), _vp(k_cache), _vp(v_cache), ctypes.c_longlong(seq_stride),
+              _vp(positions), int(max_positions_bound), int(nseq), int(heads), int(kv_heads), int(head_dim),
+              _vp(workspace) if workspace is not None else ctypes.c_void_p(0), ctypes.c_size_t(workspace_bytes),
+              _vp(out))
+
+
+def embed_q6k(table, token_id: int, out, hidden: int) -> None:
+    _lib.call("citlali_hip_embed_q6k", _vp(table), ctypes.c_int32(token_id), _vp(out), int(hidden))
+
+
+def dequant_f16(kind: str, w, count: int, out) -> None:
+    name = "citlali_hip_dequant_q4k_f16" if kind == "q4k" else "citlali_hip_dequant_q6k_f16"
+    _lib.call(name, _vp(w), ctypes.c_uint64(count), _vp(out))

@@ -1,0 +1,165 @@
+/*
+ * citlali_hip.h -- C ABI of the MI355X (gfx950) decode hot path.
+ *
+ * This is the drop-in boundary that replaces the reference's CUDA layer
+ * (include/citlali/compute/cuda/{kernels.h,tensor.h,cuda_utils.h} and
+ * src/compute/cuda/{kernels.cu,tensor.cu}).  Plain pointers and sizes only.
+ *
+ * Conventions (same as the reference's launch_* functions, kernels.h:8-61):
+ *  - fp16 values are uint16_t bit patterns, quantised weights raw GGUF
+ *    super-blocks (uint8_t), fp32 values float; all pointers are device
+ *    pointers unless a parameter says "host".
+ *  - weights are row-major [out_features][in_features/256] super-blocks.
+ *  - every call returns CITLALI_OK or an error code; the message of the last
+ *    error of the calling thread is citlali_hip_last_error().  Argument
+ *    checks run before anything touches the GPU.  HIP failures read
+ *    "HIP error at <file>:<line> for <expr>: <message>" (the shape of the
+ *    reference's CITLALI_CUDA_CHECK, cuda_utils.h:17-22).
+ *  - launches are asynchronous on the library's current stream (default: the
+ *    null stream, like the reference's <<<>>> launches); D2H copies and
+ *    citlali_hip_synchronize() wait for it.
+ *  - alignment: quantised Q4_K weights and x vectors 16-byte aligned, Q6_K
+ *    weights 4-byte aligned (any hipMalloc'd buffer qualifies).
+ */
+#ifndef CITLALI_HIP_H
+#define CITLALI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CITLALI_OK 0
+#define CITLALI_ERR_INVALID 1     /* rejected argument, nothing launched */
+#define CITLALI_ERR_UNSUPPORTED 2 /* valid for the reference, not built here */
+#define CITLALI_ERR_HIP 3         /* HIP runtime error */
+
+#define CITLALI_HIP_ABI_VERSION 1
+
+/* ---- errors and runtime ------------------------------------------------- */
+
+/* Replaces check_cuda/CITLALI_CUDA_CHECK (cuda_utils.h:17-26): message of the
+ * calling thread's last failed call ("" if none). */
+const char* citlali_hip_last_error(void);
+int citlali_hip_abi_version(void);
+
+/* Selects the device for this thread (the reference always uses device 0). */
+int citlali_hip_init(int device);
+int citlali_hip_device_count(int* count);
+
+/* Stream used by every launch (hipStream_t; NULL = null stream, the
+ * reference's legacy default stream). */
+int citlali_hip_set_stream(void* stream);
+void* citlali_hip_get_stream(void);
+
+/* Replaces QwenModel::synchronize's cudaDeviceSynchronize
+ * (qwen_model.cpp:443-445): waits for the current stream and reports any
+ * asynchronous kernel fault. */
+int citlali_hip_synchronize(void);
+
+/* ---- device memory: DeviceBuffer (tensor.h:10-54, tensor.cu:49-104) ------ */
+
+int citlali_hip_malloc(void** ptr, size_t bytes);              /* tensor.cu:49-59 (bytes == 0 -> *ptr = NULL) */
+int citlali_hip_free(void* ptr);                               /* tensor.cu:67-73 */
+int citlali_hip_memcpy_h2d(void* dst, const void* host_src, size_t bytes); /* tensor.cu:76-78 */
+int citlali_hip_memcpy_d2h(void* host_dst, const void* src, size_t bytes); /* tensor.cu:88-90, waits */
+int citlali_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
+/* cuda_zero (kernels.h:8, kernels.cu:655-657); a fill kernel, so it is safe
+ * inside captured graphs. */
+int citlali_hip_zero(void* ptr, size_t bytes);
+
+/* ---- hot path: fused dequant GEMV ---------------------------------------- *
+ * y[r] = sum_k W[r,k] x[k], W dequantised in fp32 (never rounded to fp16),
+ * fp32 accumulation.  in_features must be a positive multiple of 256 (the
+ * reference truncates silently, kernels.cu:204; this ABI rejects it) and at
+ * most CITLALI_MAX_IN_FEATURES. */
+#define CITLALI_MAX_IN_FEATURES 28672
+
+/* launch_matvec_q4k (kernels.h:26, kernels.cu:772-776); y fp16 (RNE) */
+int citlali_hip_matvec_q4k(const uint8_t* w, const uint16_t* x, uint16_t* y, int in_features, int out_features);
+/* Q4_K with fp32 output: no reference launcher; same kernel, fp32 store
+ * (the fp32-output form the reference has for Q6_K, kernels.h:30). */
+int citlali_hip_matvec_q4k_to_float(const uint8_t* w, const uint16_t* x, float* y, int in_features,
+                                    int out_features);
+/* launch_matvec_q6k (kernels.h:28, kernels.cu:779-783); y fp16 (RNE) */
+int citlali_hip_matvec_q6k(const uint8_t* w, const uint16_t* x, uint16_t* y, int in_features, int out_features);
+/* launch_matvec_q6k_to_float (kernels.h:30, kernels.cu:786-796); logits */
+int citlali_hip_matvec_q6k_to_float(const uint8_t* w, const uint16_t* x, float* y, int in_features,
+                                    int out_features);
+
+/* launch_embed_q6k (kernels.h:32, kernels.cu:670-683): row token_id of a
+ * Q6_K table -> fp16, rounded with the host rule of dequant_q6_k (ties
+ * away from zero), i.e. bit-identical to the reference's fp16 path. */
+int citlali_hip_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden);
+
+/* ---- hot path: decode attention ------------------------------------------ *
+ * launch_attention (kernels.h:38-47, kernels.cu:846-876).  Same arguments.
+ * caches [max_context][kv_heads][head_dim] fp16, positions 0..position
+ * inclusive.  `scores` (heads*max_context floats, as the reference sizes it,
+ * qwen_model.cpp:233) is used as the split-KV workspace when large enough;
+ * otherwise the library keeps its own per-device workspace (allocated on the
+ * first call that needs it, kept until citlali_hip_release_workspace()).
+ * It no longer receives the raw scores.  head_dim 64 or 128, heads/kv_heads
+ * between 1 and 8. */
+int citlali_hip_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* scores,
+                          uint16_t* out, int position, int max_context, int heads, int kv_heads, int head_dim);
+
+/* Many independent sequences in one launch (no reference counterpart: the
+ * reference decodes one sequence; per sequence the result equals
+ * launch_attention).  q/out [nseq][heads][head_dim]; sequence s uses the
+ * caches at k_cache + s*seq_stride (elements); positions: device int32
+ * [nseq], each < max_positions_bound; workspace of
+ * citlali_hip_attention_workspace_bytes() bytes (may be NULL if that is 0). */
+int citlali_hip_attention_batched(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                  long long seq_stride, const int32_t* positions, int max_positions_bound,
+                                  int nseq, int heads, int kv_heads, int head_dim, void* workspace,
+                                  size_t workspace_bytes, uint16_t* out);
+size_t citlali_hip_attention_workspace_bytes(int max_positions_bound, int nseq, int heads, int kv_heads,
+                                             int head_dim);
+int citlali_hip_release_workspace(void);
+
+/* launch_store_kv (kernels.h:36, kernels.cu:829-843): the cache layout
+ * contract, cache[position*kv_size + i] = k[i]. */
+int citlali_hip_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* k_cache, uint16_t* v_cache, int position,
+                         int kv_size);
+
+/* ---- load-time dequant on the device ------------------------------------- *
+ * dequant_q4_k / dequant_q6_k of weight_loader.cpp:147-323 (host rule
+ * rounding, bit-exact); `count` values from ceil(count/256) blocks. */
+int citlali_hip_dequant_q4k_f16(const uint8_t* w, uint64_t count, uint16_t* out);
+int citlali_hip_dequant_q6k_f16(const uint8_t* w, uint64_t count, uint16_t* out);
+
+/* ---- the rest of forward_token (kernels.h:10-36) -------------------------- */
+int citlali_hip_embed(const uint16_t* table, int32_t token_id, uint16_t* out, int hidden);   /* kernels.h:10 */
+int citlali_hip_copy(const uint16_t* in, uint16_t* out, int n);                              /* kernels.h:12 */
+int citlali_hip_add_inplace(uint16_t* target, const uint16_t* delta, int n);                 /* kernels.h:14 */
+int citlali_hip_add_bias_inplace(uint16_t* target, const uint16_t* bias, int n);             /* kernels.h:16 */
+int citlali_hip_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, int n, float eps); /* kernels.h:18 */
+int citlali_hip_rms_norm_heads(const uint16_t* in, const uint16_t* w, uint16_t* out, int heads, int head_dim,
+                               float eps);                                                    /* kernels.h:20 */
+int citlali_hip_matvec_fp16(const uint16_t* w, const uint16_t* x, uint16_t* y, int in_features,
+                            int out_features);                                                /* kernels.h:22 */
+int citlali_hip_matvec_fp16_to_float(const uint16_t* w, const uint16_t* x, float* y, int in_features,
+                                     int out_features);                                       /* kernels.h:24 */
+int citlali_hip_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, int n);      /* kernels.h:34 */
+int citlali_hip_rope(uint16_t* data, int heads, int head_dim, int position, float theta);    /* kernels.h:35 */
+
+/* Greedy sampling on the device: index of the first greatest finite logit
+ * (0 if none), written to device int32 *out_index.  Replaces the host loop
+ * of sample_greedy_from_logits (qwen_model.cpp:448-465). */
+int citlali_hip_argmax(const float* logits, int n, int32_t* out_index);
+
+/* ---- timing (bench and tests) --------------------------------------------- */
+int citlali_hip_event_create(void** event);
+int citlali_hip_event_record(void* event);                  /* on the current stream */
+int citlali_hip_event_synchronize(void* event);
+int citlali_hip_event_elapsed_ms(void* start, void* stop, float* ms);
+int citlali_hip_event_destroy(void* event);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CITLALI_HIP_H */

@@ -1,0 +1,153 @@
+"""ctypes bindings of oracle/liboracle.so (the CPU restatement) and of
+oracle/_ref/libcitlali_ref.so (the reference's own host routines, compiled
+from /root/reference).  Test infrastructure only."""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_double, c_float, c_int, c_int32, c_size_t, c_uint64, c_void_p
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_SO = os.path.join(ROOT, "oracle", "_ref", "libcitlali_ref.so")
+
+_P = c_void_p
+
+
+def _p(a: np.ndarray) -> c_void_p:
+    return a.ctypes.data_as(c_void_p)
+
+
+class Oracle:
+    SIGS = {
+        "orc_f2h": (ctypes.c_uint16, [c_float]),
+        "orc_h2f": (c_float, [ctypes.c_uint16]),
+        "orc_f2h_rne": (ctypes.c_uint16, [c_float]),
+        "orc_f2h_array": (None, [_P, c_size_t, _P]),
+        "orc_f2h_rne_array": (None, [_P, c_size_t, _P]),
+        "orc_h2f_array": (None, [_P, c_size_t, _P]),
+        "orc_dequant_q4k_f16": (None, [_P, c_uint64, _P]),
+        "orc_dequant_q6k_f16": (None, [_P, c_uint64, _P]),
+        "orc_dequant_q4k_f32": (None, [_P, c_uint64, _P]),
+        "orc_dequant_q6k_f32": (None, [_P, c_uint64, _P]),
+        "orc_matvec_q4k": (None, [_P, _P, _P, c_int, c_int, c_int]),
+        "orc_matvec_q6k": (None, [_P, _P, _P, c_int, c_int, c_int]),
+        "orc_matvec_q4k_f16dot": (None, [_P, _P, _P, c_int, c_int, c_int]),
+        "orc_matvec_q6k_f16dot": (None, [_P, _P, _P, c_int, c_int, c_int]),
+        "orc_matvec_f16": (None, [_P, _P, _P, c_int, c_int, c_int]),
+        "orc_embed_q6k": (None, [_P, c_int32, _P, c_int]),
+        "orc_attention": (None, [_P, _P, _P, c_int, c_int, c_int, c_int, _P]),
+        "orc_attention_f32": (None, [_P, _P, _P, c_int, c_int, c_int, c_int, _P, c_int]),
+        "orc_rms_norm": (None, [_P, _P, _P, c_int, c_float]),
+        "orc_rms_norm_heads": (None, [_P, _P, _P, c_int, c_int, c_float]),
+        "orc_rope": (None, [_P, c_int, c_int, c_int, c_float]),
+        "orc_swiglu": (None, [_P, _P, _P, c_int]),
+        "orc_add_inplace": (None, [_P, _P, c_int]),
+        "orc_store_kv": (None, [_P, _P, _P, _P, c_int, c_int]),
+        "orc_argmax": (c_int32, [_P, c_int]),
+        "orc_num_threads": (c_int, []),
+    }
+
+    def __init__(self, path: str = ORACLE_SO):
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} missing: run `make -C oracle`")
+        self.lib = ctypes.CDLL(path)
+        for name, (res, args) in self.SIGS.items():
+            fn = getattr(self.lib, name)
+            fn.restype = res
+            fn.argtypes = args
+
+    # fp16
+    def f2h(self, f) -> np.ndarray:
+        f = np.ascontiguousarray(f, dtype=np.float32)
+        out = np.empty(f.shape, np.uint16)
+        self.lib.orc_f2h_array(_p(f), f.size, _p(out))
+        return out
+
+    def f2h_rne(self, f) -> np.ndarray:
+        f = np.ascontiguousarray(f, dtype=np.float32)
+        out = np.empty(f.shape, np.uint16)
+        self.lib.orc_f2h_rne_array(_p(f), f.size, _p(out))
+        return out
+
+    def h2f(self, h) -> np.ndarray:
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        out = np.empty(h.shape, np.float32)
+        self.lib.orc_h2f_array(_p(h), h.size, _p(out))
+        return out
+
+    # dequant
+    def dequant_f16(self, kind: str, blocks: np.ndarray, count: int) -> np.ndarray:
+        out = np.empty(count, np.uint16)
+        getattr(self.lib, f"orc_dequant_{kind}_f16")(_p(np.ascontiguousarray(blocks)), count, _p(out))
+        return out
+
+    def dequant_f32(self, kind: str, blocks: np.ndarray, count: int) -> np.ndarray:
+        out = np.empty(count, np.float32)
+        getattr(self.lib, f"orc_dequant_{kind}_f32")(_p(np.ascontiguousarray(blocks)), count, _p(out))
+        return out
+
+    # GEMV
+    def matvec(self, kind: str, w: np.ndarray, x: np.ndarray, in_f: int, out_f: int, nthreads: int = 0) -> np.ndarray:
+        y = np.empty(out_f, np.float64)
+        getattr(self.lib, f"orc_matvec_{kind}")(_p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(x)), _p(y),
+                                                in_f, out_f, nthreads)
+        return y
+
+    def matvec_f16dot(self, kind: str, w, x, in_f, out_f, nthreads=0) -> np.ndarray:
+        y = np.empty(out_f, np.float32)
+        getattr(self.lib, f"orc_matvec_{kind}_f16dot")(_p(w), _p(x), _p(y), in_f, out_f, nthreads)
+        return y
+
+    def embed_q6k(self, table, token_id: int, hidden: int) -> np.ndarray:
+        out = np.empty(hidden, np.uint16)
+        self.lib.orc_embed_q6k(_p(table), token_id, _p(out), hidden)
+        return out
+
+    def attention(self, q, kc, vc, position, heads, kv_heads, head_dim) -> np.ndarray:
+        out = np.empty(heads * head_dim, np.float64)
+        self.lib.orc_attention(_p(q), _p(kc), _p(vc), position, heads, kv_heads, head_dim, _p(out))
+        return out
+
+    def attention_f32(self, q, kc, vc, position, heads, kv_heads, head_dim, nthreads=0) -> np.ndarray:
+        out = np.empty(heads * head_dim, np.float32)
+        self.lib.orc_attention_f32(_p(q), _p(kc), _p(vc), position, heads, kv_heads, head_dim, _p(out), nthreads)
+        return out
+
+
+class RefLib:
+    """The reference's own host fp16 and dequant routines (oracle/_ref)."""
+
+    def __init__(self, path: str = REF_SO):
+        self.lib = ctypes.CDLL(path)
+        self.lib.ref_f2h_array.argtypes = [_P, c_uint64, _P]
+        self.lib.ref_h2f_array.argtypes = [_P, c_uint64, _P]
+        self.lib.ref_bf16_to_half_array.argtypes = [_P, c_uint64, _P]
+        self.lib.ref_dequant_q4k.argtypes = [_P, c_uint64, c_uint64, _P]
+        self.lib.ref_dequant_q6k.argtypes = [_P, c_uint64, c_uint64, _P]
+        self.lib.ref_tensor_nbytes.argtypes = [ctypes.c_uint32, c_uint64]
+        self.lib.ref_tensor_nbytes.restype = c_uint64
+
+    @classmethod
+    def try_load(cls):
+        return cls() if os.path.exists(REF_SO) else None
+
+    def f2h(self, f) -> np.ndarray:
+        f = np.ascontiguousarray(f, dtype=np.float32)
+        out = np.empty(f.shape, np.uint16)
+        self.lib.ref_f2h_array(_p(f), f.size, _p(out))
+        return out
+
+    def h2f(self, h) -> np.ndarray:
+        h = np.ascontiguousarray(h, dtype=np.uint16)
+        out = np.empty(h.shape, np.float32)
+        self.lib.ref_h2f_array(_p(h), h.size, _p(out))
+        return out
+
+    def dequant(self, kind: str, blocks: np.ndarray, count: int) -> np.ndarray:
+        blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
+        out = np.empty(count, np.uint16)
+        getattr(self.lib, f"ref_dequant_{kind}")(_p(blocks), blocks.size, count, _p(out))
+        return out

@@ -1,0 +1,125 @@
+"""The C ABI without a GPU: the libraries load, export every symbol the
+headers declare, and reject bad arguments before touching the device (the
+failure cases of SURVEY-listed reference checks: null buffers, in_features
+not a multiple of 256, head_count % head_count_kv, position >= max_context)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def declared_c_symbols():
+    names = set()
+    for fn in os.listdir(INCLUDE):
+        if fn.endswith(".h"):
+            text = open(os.path.join(INCLUDE, fn)).read()
+            names.update(re.findall(r"\b(citlali_hip_\w+)\s*\(", text))
+    return sorted(names)
+
+
+def test_every_declared_symbol_is_exported():
+    import pycitlali
+    lib = pycitlali.load()
+    names = declared_c_symbols()
+    assert len(names) >= 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    out = subprocess.run(["nm", "-D", "--defined-only", pycitlali._lib.HIP_LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (citlali_hip_\w+)", out))
+    assert set(names) <= exported
+    # the binding declares exactly the header's functions
+    assert sorted(n for n, _, _ in pycitlali._lib.SIGNATURES) == names
+
+
+def test_abi_version():
+    import pycitlali
+    assert pycitlali.load().citlali_hip_abi_version() == 1
+
+
+def _status(fn, *args):
+    import pycitlali
+    lib = pycitlali.load()
+    st = getattr(lib, fn)(*args)
+    return st, pycitlali.last_error()
+
+
+P = ctypes.c_void_p
+
+
+@pytest.mark.parametrize("fn", ["citlali_hip_matvec_q4k", "citlali_hip_matvec_q6k", "citlali_hip_matvec_q4k_to_float",
+                                "citlali_hip_matvec_q6k_to_float"])
+def test_matvec_validation(fn):
+    fake = P(0x10000)
+    st, msg = _status(fn, P(0), fake, fake, 256, 4)
+    assert st == 1 and "null buffer" in msg
+    st, msg = _status(fn, fake, fake, fake, 1000, 4)
+    assert st == 1 and "multiple of the 256-value super-block" in msg
+    st, msg = _status(fn, fake, fake, fake, 0, 4)
+    assert st == 1 and "positive" in msg
+    st, msg = _status(fn, fake, fake, fake, 256, 0)
+    assert st == 1
+    st, msg = _status(fn, fake, fake, fake, 28672 + 256, 4)
+    assert st == 1 and "exceeds" in msg
+    st, msg = _status(fn, P(0x10001), fake, fake, 256, 4)
+    assert st == 1 and "aligned" in msg
+
+
+def test_attention_validation():
+    fake = P(0x10000)
+    st, msg = _status("citlali_hip_attention", fake, fake, fake, fake, fake, 5, 5, 16, 8, 128)
+    assert st == 1 and "position exceeds max_context" in msg
+    st, msg = _status("citlali_hip_attention", fake, fake, fake, fake, fake, 0, 5, 12, 8, 128)
+    assert st == 1 and "divisible" in msg
+    st, msg = _status("citlali_hip_attention", fake, fake, fake, fake, fake, 0, 5, 16, 8, 96)
+    assert st == 2 and "not built" in msg
+    st, msg = _status("citlali_hip_attention", fake, fake, fake, fake, fake, 0, 5, 128, 8, 128)
+    assert st == 2
+    st, msg = _status("citlali_hip_attention", P(0), fake, fake, fake, fake, 0, 5, 16, 8, 128)
+    assert st == 1 and "null" in msg
+
+
+def test_embed_and_dequant_validation():
+    fake = P(0x10000)
+    st, msg = _status("citlali_hip_embed_q6k", fake, -1, fake, 1024)
+    assert st == 1 and "vocab" in msg
+    st, msg = _status("citlali_hip_embed_q6k", fake, 3, fake, 1000)
+    assert st == 1
+    st, msg = _status("citlali_hip_dequant_q4k_f16", P(0), ctypes.c_uint64(256), fake)
+    assert st == 1
+
+
+def test_workspace_query_is_host_only():
+    import pycitlali
+    lib = pycitlali.load()
+    n = lib.citlali_hip_attention_workspace_bytes(32768, 16, 32, 8, 128)
+    assert n > 0 and n % 4 == 0
+    assert lib.citlali_hip_attention_workspace_bytes(64, 1, 32, 8, 128) == 0
+    assert lib.citlali_hip_attention_workspace_bytes(100, 1, 12, 8, 128) == 0
+
+
+def test_device_array_fails_loudly_without_library(tmp_path, monkeypatch):
+    import pycitlali._lib as L
+    monkeypatch.setattr(L, "_lib", None)
+    monkeypatch.setattr(L, "HIP_LIB_PATH", str(tmp_path / "missing.so"))
+    with pytest.raises(ImportError, match="not built"):
+        L.load()
+
+
+def test_synth_is_deterministic_and_shaped():
+    from pycitlali import synth
+    a = synth.quant_matrix("q4k", synth.Rng(0), 4, 512)
+    b = synth.quant_matrix("q4k", synth.Rng(0), 4, 512)
+    assert a.size == 4 * 2 * 144 and np.array_equal(a, b)
+    d = a.reshape(-1, 144)[:, 0:2].copy().view(np.float16).astype(np.float64)
+    assert np.all((d >= 1e-3 * 0.999) & (d <= 1e-2 * 1.001))
+    z = synth.Rng(1).normal(200000)
+    assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01

@@ -1,0 +1,139 @@
+"""GPU parity of decode attention (kernels.cu:545-649) against the oracle,
+through the C ABI.
+
+Bar (north star): |gpu - ref| <= 2e-3 + 1e-2*|ref| against the double
+precision oracle.  Closed forms: one position gives V[0]; q = 0 gives the
+mean of V; query heads sharing a kv head with equal q give equal outputs;
+the result does not depend on how the positions are split into chunks.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import tol_ok
+
+pytestmark = pytest.mark.gpu
+
+
+def _cache(hip, seed, L, kv_heads, hd, max_ctx=None, scale=1.0):
+    rng = hip.synth.Rng(seed)
+    max_ctx = max_ctx or L
+    k = hip.synth.normal_f16(rng, max_ctx * kv_heads * hd, scale)
+    v = hip.synth.normal_f16(rng, max_ctx * kv_heads * hd)
+    return k, v
+
+
+def _run(hip, q, k, v, position, max_ctx, heads, kv_heads, hd, scores=True):
+    dq = hip.DeviceArray.from_numpy(q)
+    dk = hip.DeviceArray.from_numpy(k)
+    dv = hip.DeviceArray.from_numpy(v)
+    ds = hip.DeviceArray(heads * max_ctx * 4) if scores else None
+    do = hip.DeviceArray(heads * hd * 2)
+    hip.device.attention(dq, dk, dv, ds, do, position, max_ctx, heads, kv_heads, hd)
+    return do.download(np.uint16, heads * hd).view(np.float16).astype(np.float64)
+
+
+CASES = [
+    # (heads, kv_heads, head_dim, L, max_ctx)
+    (16, 8, 128, 1024, 1024),    # cfg2: Qwen3-0.6B
+    (32, 8, 128, 8192, 8192),    # cfg3: Qwen3-8B at L = 8192
+    (32, 8, 128, 1, 64),
+    (32, 8, 128, 17, 64),
+    (32, 8, 128, 65, 2048),
+    (32, 8, 128, 1000, 1024),
+    (16, 8, 128, 3000, 4096),
+    (40, 8, 128, 777, 1024),     # group 5 (Qwen3-14B shape)
+    (64, 8, 128, 513, 600),      # group 8
+    (8, 8, 128, 300, 300),       # group 1
+    (16, 8, 64, 700, 700),       # head_dim 64
+    (32, 4, 64, 129, 200),
+]
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd,L,max_ctx", CASES)
+def test_attention_matches_oracle(hip, orc, heads, kv_heads, hd, L, max_ctx):
+    print(f"[attention] heads={heads} kv={kv_heads} hd={hd} L={L} max_ctx={max_ctx}", flush=True)
+    k, v = _cache(hip, 100 + L + heads, L, kv_heads, hd, max_ctx)
+    q = hip.synth.normal_f16(hip.synth.Rng(L * 7 + hd), heads * hd)
+    got = _run(hip, q, k, v, L - 1, max_ctx, heads, kv_heads, hd)
+    ref = orc.attention(q, k, v, L - 1, heads, kv_heads, hd)
+    bad = ~tol_ok(got, ref)
+    assert not bad.any(), f"{bad.sum()} values out of tolerance; max err {np.abs(got - ref).max()}"
+    # within one fp16 rounding plus fp32 noise
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2 ** -10 + 1e-4)
+
+
+def test_attention_without_scores_buffer(hip, orc):
+    heads, kv, hd, L = 32, 8, 128, 4096
+    k, v = _cache(hip, 5, L, kv, hd)
+    q = hip.synth.normal_f16(hip.synth.Rng(6), heads * hd)
+    got = _run(hip, q, k, v, L - 1, L, heads, kv, hd, scores=False)
+    assert np.all(tol_ok(got, orc.attention(q, k, v, L - 1, heads, kv, hd)))
+
+
+def test_single_position_returns_v0(hip):
+    heads, kv, hd = 32, 8, 128
+    k, v = _cache(hip, 9, 16, kv, hd)
+    q = hip.synth.normal_f16(hip.synth.Rng(10), heads * hd)
+    got = _run(hip, q, k, v, 0, 16, heads, kv, hd)
+    v0 = v[: kv * hd].view(np.float16).astype(np.float64).reshape(kv, hd)
+    np.testing.assert_array_equal(got.reshape(heads, hd), np.repeat(v0, heads // kv, axis=0))
+
+
+def test_zero_query_gives_mean_of_values(hip):
+    heads, kv, hd, L = 16, 8, 128, 2500
+    k, v = _cache(hip, 12, L, kv, hd)
+    q = np.zeros(heads * hd, np.uint16)
+    got = _run(hip, q, k, v, L - 1, L, heads, kv, hd).reshape(heads, hd)
+    mean = v.view(np.float16).astype(np.float64).reshape(L, kv, hd).mean(axis=0)
+    ref = np.repeat(mean, heads // kv, axis=0)
+    assert np.all(np.abs(got - ref) <= 2e-3 + 1e-2 * np.abs(ref))
+
+
+def test_gqa_heads_with_equal_queries_agree(hip):
+    heads, kv, hd, L = 32, 8, 128, 1500
+    k, v = _cache(hip, 13, L, kv, hd)
+    qh = hip.synth.normal_f16(hip.synth.Rng(14), kv * hd).reshape(kv, 1, hd)
+    q = np.ascontiguousarray(np.repeat(qh, heads // kv, axis=1).reshape(-1))
+    got = _run(hip, q, k, v, L - 1, L, heads, kv, hd).reshape(kv, heads // kv, hd)
+    for g in range(1, heads // kv):
+        np.testing.assert_array_equal(got[:, g], got[:, 0])
+
+
+def test_batched_matches_single_sequence_calls(hip, orc):
+    """16 sequences in one launch == 16 single-sequence launches (cfg4 shape,
+    shortened so the oracle stays fast)."""
+    nseq, heads, kv, hd, max_ctx = 16, 32, 8, 128, 3000
+    rng = hip.synth.Rng(2024)
+    lens = (rng.u64(nseq) % np.uint64(max_ctx)).astype(np.int64) + 1
+    lens[0], lens[1] = 1, max_ctx
+    stride = max_ctx * kv * hd
+    k = hip.synth.normal_f16(rng, nseq * stride)
+    v = hip.synth.normal_f16(rng, nseq * stride)
+    q = hip.synth.normal_f16(rng, nseq * heads * hd)
+    pos = (lens - 1).astype(np.int32)
+    ws_bytes = hip.device.attention_workspace_bytes(max_ctx, nseq, heads, kv, hd)
+    dws = hip.DeviceArray(max(ws_bytes, 16))
+    dq, dk, dv = (hip.DeviceArray.from_numpy(a) for a in (q, k, v))
+    dpos = hip.DeviceArray.from_numpy(pos)
+    do = hip.DeviceArray(nseq * heads * hd * 2)
+    hip.device.attention_batched(dq, dk, dv, stride, dpos, max_ctx, nseq, heads, kv, hd, dws, ws_bytes, do)
+    got = do.download(np.uint16).view(np.float16).astype(np.float64).reshape(nseq, heads * hd)
+    for s in range(nseq):
+        sl = slice(s * stride, (s + 1) * stride)
+        qs = q[s * heads * hd:(s + 1) * heads * hd]
+        ref = orc.attention(qs, k[sl], v[sl], int(pos[s]), heads, kv, hd)
+        assert np.all(tol_ok(got[s], ref)), f"sequence {s} (L={lens[s]})"
+        single = _run(hip, qs, k[sl], v[sl], int(pos[s]), max_ctx, heads, kv, hd)
+        assert np.all(np.abs(single - got[s]) <= np.abs(ref) * 2 ** -10 + 1e-4)
+
+
+def test_batched_rejects_small_workspace(hip):
+    heads, kv, hd, nseq, max_ctx = 32, 8, 128, 4, 4096
+    need = hip.device.attention_workspace_bytes(max_ctx, nseq, heads, kv, hd)
+    assert need > 0
+    d = hip.DeviceArray(1 << 20)
+    pos = hip.DeviceArray.from_numpy(np.full(nseq, max_ctx - 1, np.int32))
+    with pytest.raises(hip.CitlaliError, match="workspace"):
+        hip.device.attention_batched(d, d, d, 0, pos, max_ctx, nseq, heads, kv, hd, d, need - 16, d)

@@ -1,0 +1,80 @@
+"""GPU bit-exactness of the Q6_K embedding gather and of whole-tensor Q4_K /
+Q6_K -> fp16 dequantisation against the reference's host routines
+(weight_loader.cpp:147-323, ties-away rounding of dtype.cpp:136-176): the
+golden vectors written by the compiled reference, and the oracle."""
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _golden(name):
+    path = os.path.join(GOLDEN, name)
+    if not os.path.exists(path):
+        pytest.skip(f"{name} not generated")
+    return np.load(path, allow_pickle=False)
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("fixture", ["random", "realistic"])
+def test_device_dequant_matches_reference_golden(hip, kind, fixture):
+    g = _golden(f"dequant_{kind}_{fixture}.npz")
+    blocks, expect = g["blocks"], g["fp16"]
+    dw = hip.DeviceArray.from_numpy(blocks)
+    do = hip.DeviceArray(expect.size * 2)
+    hip.device.dequant_f16(kind, dw, expect.size, do)
+    np.testing.assert_array_equal(do.download(np.uint16, expect.size), expect)
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("count", [1, 255, 256, 257, 4096 * 3 + 100])
+def test_device_dequant_ragged_counts(hip, orc, kind, count):
+    rng = hip.synth.Rng(count)
+    nb = (count + 255) // 256
+    blocks = hip.synth.q4k_blocks(rng, nb) if kind == "q4k" else hip.synth.q6k_blocks(rng, nb)
+    dw = hip.DeviceArray.from_numpy(blocks)
+    do = hip.DeviceArray(count * 2 + 64)
+    do.zero()
+    hip.device.dequant_f16(kind, dw, count, do)
+    out = do.download(np.uint16, count + 32)
+    np.testing.assert_array_equal(out[:count], orc.dequant_f16(kind, blocks, count))
+    assert not out[count:].any(), "wrote past count"
+
+
+@pytest.mark.parametrize("hidden", [1024, 4096])
+def test_embed_q6k_is_bit_exact(hip, orc, hidden):
+    vocab = 1000
+    rng = hip.synth.Rng(hidden)
+    table = hip.synth.q6k_blocks(rng, vocab * hidden // 256)
+    dt = hip.DeviceArray.from_numpy(table)
+    do = hip.DeviceArray(hidden * 2)
+    for tok in [0, 1, 17, 500, vocab - 1]:
+        hip.device.embed_q6k(dt, tok, do, hidden)
+        got = do.download(np.uint16, hidden)
+        np.testing.assert_array_equal(got, orc.embed_q6k(table, tok, hidden), err_msg=f"token {tok}")
+
+
+def test_embed_q6k_rounds_ties_away_from_zero(hip):
+    """d = 1 + 3*2^-10, scale 1, q - 32 = 3: value 3 + 9*2^-10 lies exactly
+    between two fp16 neighbours whose lower one is even; the host rule rounds
+    it up (away from zero), the nearest-even rule would round down."""
+    hidden = 256
+    blk = np.zeros(210, np.uint8)
+    # ql low nibble 3, qh bits 2 -> q6 = 35 -> q = 3 for every value
+    blk[:128] = 0x33
+    blk[128:192] = 0xAA
+    blk[192:208] = 1
+    blk[208:210] = np.array([0x3C03], np.uint16).view(np.uint8)
+    dt = hip.DeviceArray.from_numpy(blk)
+    do = hip.DeviceArray(hidden * 2)
+    hip.device.embed_q6k(dt, 0, do, hidden)
+    got = do.download(np.uint16, hidden)
+    v = np.float32(1.0 + 3 * 2 ** -10) * np.float32(3.0)
+    rne = np.array([v], np.float32).astype(np.float16).view(np.uint16)[0]
+    assert np.all(got == rne + 1), (hex(got[0]), hex(rne))

@@ -1,0 +1,119 @@
+"""GPU parity of the fused-dequant GEMVs (kernels.cu:195-338) against the
+oracle, through the C ABI.
+
+Bar (north star): |gpu - ref| <= 2e-3 + 1e-2*|ref| with ref the exact fp32
+weights accumulated in double; fp16 outputs additionally within one fp16
+rounding of ref.  One-hot inputs pin the layout bit-exactly: with x = e_k and
+fp32 output every kernel must return the fp32 weight column W[:, k] exactly.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import tol_ok
+
+pytestmark = pytest.mark.gpu
+
+# (kind, out_features, in_features): BASELINE configs 1 and 3 plus edges
+SHAPES = [
+    ("q4k", 3072, 1024),     # cfg1: Qwen3-0.6B ffn_gate (nb = 4)
+    ("q4k", 1024, 3072),     # same bytes, nb = 12 (ffn_down orientation)
+    ("q4k", 4096, 4096),     # cfg3 attn_q / attn_o
+    ("q4k", 1024, 4096),     # cfg3 attn_k
+    ("q4k", 12288, 4096),    # cfg3 ffn_gate / ffn_up
+    ("q6k", 1024, 4096),     # cfg3 attn_v
+    ("q6k", 4096, 12288),    # cfg3 ffn_down (nb = 48)
+    ("q6k", 1024, 1024),     # Qwen3-0.6B attn_v (nb = 4, 840-byte rows)
+    ("q6k", 1024, 3072),     # Qwen3-0.6B ffn_down (nb = 12)
+    ("q4k", 1, 256),         # one row, one block
+    ("q6k", 1, 256),
+    ("q4k", 37, 768),        # ragged rows, nb = 3
+    ("q6k", 37, 768),
+    ("q6k", 3, 28672),       # the largest in_features the ABI takes
+    ("q4k", 5, 28672),
+]
+
+
+def _inputs(hip, kind, n, k, seed):
+    rng = hip.synth.Rng(seed)
+    w = hip.synth.quant_matrix(kind, rng, n, k)
+    x = hip.synth.normal_f16(rng, k)
+    return w, x
+
+
+@pytest.mark.parametrize("kind,n,k", SHAPES)
+@pytest.mark.parametrize("f32_out", [False, True])
+def test_matvec_matches_oracle(hip, orc, kind, n, k, f32_out):
+    print(f"[matvec] kind={kind} n={n} k={k} f32={f32_out}", flush=True)
+    w, x = _inputs(hip, kind, n, k, seed=1000 + n + k)
+    dw = hip.DeviceArray.from_numpy(w)
+    dx = hip.DeviceArray.from_numpy(x)
+    dy = hip.DeviceArray(n * (4 if f32_out else 2))
+    hip.device.matvec(kind, dw, dx, dy, k, n, f32_out=f32_out)
+    got = dy.download(np.float32 if f32_out else np.uint16, n)
+    if not f32_out:
+        got = got.view(np.float16).astype(np.float64)
+    ref = orc.matvec(kind, w, x, k, n)
+    bad = ~tol_ok(got, ref)
+    assert not bad.any(), f"{bad.sum()} rows out of tolerance, e.g. got {got[bad][:4]} ref {ref[bad][:4]}"
+    if not f32_out:
+        # at most one fp16 step away from the correctly rounded reference
+        r16 = ref.astype(np.float16).astype(np.float64)
+        step = np.abs(np.nextafter(ref.astype(np.float16), np.float16(np.inf)).astype(np.float64) - r16)
+        assert np.all(np.abs(got - r16) <= step + 1e-12)
+    else:
+        # fp32 accumulation error stays far inside the bar
+        err = np.abs(got - ref)
+        print(f"[matvec] max abs err {err.max():.3g}, max |y| {np.abs(ref).max():.3g}", flush=True)
+        assert np.all(err <= 1e-4 * (1.0 + np.abs(ref)))
+
+
+@pytest.mark.parametrize("kind,n,k", [("q4k", 64, 1024), ("q6k", 64, 1024), ("q4k", 19, 3072), ("q6k", 19, 3072)])
+def test_one_hot_input_returns_exact_weight_column(hip, orc, kind, n, k):
+    w, _ = _inputs(hip, kind, n, k, seed=7)
+    wf = orc.dequant_f32(kind, w, n * k).reshape(n, k)
+    dw = hip.DeviceArray.from_numpy(w)
+    dy = hip.DeviceArray(n * 4)
+    rng = np.random.default_rng(3)
+    for col in sorted(set([0, 1, 2, 3, 31, 32, 63, 64, 127, 128, 255, 256, k - 1] + list(rng.integers(0, k, 12)))):
+        x = np.zeros(k, np.uint16)
+        x[col] = 0x3C00  # 1.0
+        dx = hip.DeviceArray.from_numpy(x)
+        hip.device.matvec(kind, dw, dx, dy, k, n, f32_out=True)
+        got = dy.download(np.float32, n)
+        np.testing.assert_array_equal(got.view(np.uint32), wf[:, col].view(np.uint32), err_msg=f"column {col}")
+
+
+def test_linearity_and_row_sums(hip, orc):
+    n, k = 256, 2048
+    rng = hip.synth.Rng(11)
+    w = hip.synth.quant_matrix("q4k", rng, n, k)
+    x = hip.synth.normal_f16(rng, k)
+    dw = hip.DeviceArray.from_numpy(w)
+    dy = hip.DeviceArray(n * 4)
+    # x = 1 gives the row sums of the fp32 weights
+    ones = np.full(k, 0x3C00, np.uint16)
+    hip.device.matvec("q4k", dw, hip.DeviceArray.from_numpy(ones), dy, k, n, f32_out=True)
+    rs = orc.dequant_f32("q4k", w, n * k).reshape(n, k).astype(np.float64).sum(axis=1)
+    assert np.all(tol_ok(dy.download(np.float32, n), rs, atol=1e-3, rtol=1e-5))
+    # y(2x) == 2 y(x) exactly (power-of-two scaling commutes with rounding)
+    x2 = (x.view(np.float16) * np.float16(2)).view(np.uint16)
+    hip.device.matvec("q4k", dw, hip.DeviceArray.from_numpy(x), dy, k, n, f32_out=True)
+    y1 = dy.download(np.float32, n)
+    hip.device.matvec("q4k", dw, hip.DeviceArray.from_numpy(x2), dy, k, n, f32_out=True)
+    np.testing.assert_array_equal(dy.download(np.float32, n), 2 * y1)
+
+
+def test_rows_permute_with_weights(hip):
+    n, k = 96, 1024
+    rng = hip.synth.Rng(5)
+    w = hip.synth.quant_matrix("q6k", rng, n, k).reshape(n, -1)
+    x = hip.synth.normal_f16(rng, k)
+    perm = np.random.default_rng(0).permutation(n)
+    dx = hip.DeviceArray.from_numpy(x)
+    dy = hip.DeviceArray(n * 4)
+    hip.device.matvec("q6k", hip.DeviceArray.from_numpy(w), dx, dy, k, n, f32_out=True)
+    y = dy.download(np.float32, n)
+    hip.device.matvec("q6k", hip.DeviceArray.from_numpy(np.ascontiguousarray(w[perm])), dx, dy, k, n, f32_out=True)
+    np.testing.assert_array_equal(dy.download(np.float32, n), y[perm])
