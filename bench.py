@@ -1,0 +1,251 @@
+#!/usr/bin/env python3
+"""Decode hot-path benchmark on one MI355X.
+
+Workload: one Qwen3-8B decoder layer of single-token
+decode through the hot path -- attn_q/attn_k Q4_K, attn_v Q6_K, GQA attention
+(32 query / 8 kv heads, head_dim 128) over an fp16 KV cache of 8192
+positions, attn_o Q4_K, ffn_gate/ffn_up Q4_K 12288x4096, ffn_down Q6_K
+4096x12288.  A step is one such layer; steps rotate over LAYERS distinct
+copies of weights and caches (>= 512 MB in total) so every byte comes from
+HBM, not the 256 MB Infinity Cache.  Inputs are synthetic (seeded random
+quant blocks with d, dmin in [1e-3, 1e-2]; N(0,1) fp16 activations/caches)
+and are resident in HBM before timing starts.
+
+value = algorithmic bytes per step / time per step (GB/s, all kernels of the
+step).  roofline: the kernel with the largest share of step time, its
+algorithmic bytes per launch over its average launch duration measured with
+HIP events on the launch stream inside the timed steps.  cpu_baseline: the
+oracle's restatement of the reference's host arithmetic (dequant to fp16 with
+the host rule, fp32 dot; fp32 attention) on a bounded sample of the same
+layer, on this machine's host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "citlali-llm-engine_amd"))
+
+HBM_PEAK_GBPS = 8000.0
+LAYERS = 4
+HIDDEN, FFN, HEADS, KV_HEADS, HEAD_DIM, CTX = 4096, 12288, 32, 8, 128, 8192
+
+# (name, kind, rows=out_features, cols=in_features, input, output)
+GEMVS = [
+    ("attn_q", "q4k", HEADS * HEAD_DIM, HIDDEN, "x", "q"),
+    ("attn_k", "q4k", KV_HEADS * HEAD_DIM, HIDDEN, "x", "k"),
+    ("attn_v", "q6k", KV_HEADS * HEAD_DIM, HIDDEN, "x", "v"),
+    ("attn_o", "q4k", HIDDEN, HEADS * HEAD_DIM, "att", "o"),
+    ("ffn_gate", "q4k", FFN, HIDDEN, "x", "gate"),
+    ("ffn_up", "q4k", FFN, HIDDEN, "x", "up"),
+    ("ffn_down", "q6k", HIDDEN, FFN, "up", "down"),
+]
+ORDER = ["attn_q", "attn_k", "attn_v", "attention", "attn_o", "ffn_gate", "ffn_up", "ffn_down"]
+SB_BYTES = {"q4k": 144, "q6k": 210}
+
+
+def gemv_bytes(kind, rows, cols):
+    """Algorithmic bytes: weights once, x once, y once (fp16)."""
+    return rows * (cols // 256) * SB_BYTES[kind] + cols * 2 + rows * 2
+
+
+def attention_bytes(L):
+    return 2 * L * KV_HEADS * HEAD_DIM * 2 + 2 * HEADS * HEAD_DIM * 2
+
+
+def kernel_bytes():
+    b = {n: gemv_bytes(k, r, c) for n, k, r, c, _, _ in GEMVS}
+    b["attention"] = attention_bytes(CTX)
+    return b
+
+
+class Layer:
+    def __init__(self, hip, host):
+        self.w = {n: hip.DeviceArray.from_numpy(host[n]) for n, *_ in GEMVS}
+        self.kc = hip.DeviceArray.from_numpy(host["k_cache"])
+        self.vc = hip.DeviceArray.from_numpy(host["v_cache"])
+
+
+def make_host_layer(hip):
+    rng = hip.synth.Rng(0)
+    host = {n: hip.synth.quant_matrix(k, rng, r, c) for n, k, r, c, _, _ in GEMVS}
+    host["k_cache"] = hip.synth.normal_f16(rng, CTX * KV_HEADS * HEAD_DIM)
+    host["v_cache"] = hip.synth.normal_f16(rng, CTX * KV_HEADS * HEAD_DIM)
+    host["x"] = hip.synth.normal_f16(rng, HIDDEN)
+    return host
+
+
+def run_gpu(args):
+    import pycitlali as hip
+    lib = hip.load()
+    hip.check(lib.citlali_hip_init(0))
+    host = make_host_layer(hip)
+    layers = [Layer(hip, host) for _ in range(LAYERS)]
+    act = {"x": hip.DeviceArray.from_numpy(host["x"])}
+    for name, size in (("q", HEADS * HEAD_DIM), ("k", KV_HEADS * HEAD_DIM), ("v", KV_HEADS * HEAD_DIM),
+                       ("att", HEADS * HEAD_DIM), ("o", HIDDEN), ("gate", FFN), ("up", FFN), ("down", HIDDEN)):
+        act[name] = hip.DeviceArray(size * 2)
+    scores = hip.DeviceArray(HEADS * CTX * 4)
+    spec = {n: (k, r, c, i, o) for n, k, r, c, i, o in GEMVS}
+
+    def launch(name, layer):
+        if name == "attention":
+            hip.device.attention(act["q"], layer.kc, layer.vc, scores, act["att"], CTX - 1, CTX, HEADS, KV_HEADS,
+                                 HEAD_DIM)
+        else:
+            k, r, c, i, o = spec[name]
+            hip.device.matvec(k, layer.w[name], act[i], act[o], c, r)
+
+    def step(s, timed_kernel=None, evs=None):
+        layer = layers[s % LAYERS]
+        for name in ORDER:
+            if name == timed_kernel:
+                evs[0].record()
+                launch(name, layer)
+                evs[1].record()
+            else:
+                launch(name, layer)
+
+    # warmup, and a per-kernel pass to find the kernel with the largest share
+    for s in range(args.warmup):
+        step(s)
+    hip.synchronize()
+    per = {n: 0.0 for n in ORDER}
+    ev = [hip.Event() for _ in range(len(ORDER) + 1)]
+    cal = max(4, LAYERS)
+    for s in range(cal):
+        layer = layers[s % LAYERS]
+        ev[0].record()
+        for j, name in enumerate(ORDER):
+            launch(name, layer)
+            ev[j + 1].record()
+        ev[-1].synchronize()
+        for j, name in enumerate(ORDER):
+            per[name] += ev[j].elapsed_ms(ev[j + 1]) / cal
+    dominant = max(per, key=per.get)
+
+    # timed region: K steps, events around the dominant kernel's launches
+    hip.synchronize()
+    t0, t1 = hip.Event(), hip.Event()
+    kev = [(hip.Event(), hip.Event()) for _ in range(args.steps)]
+    t0.record()
+    for s in range(args.steps):
+        step(s, dominant, kev[s])
+    t1.record()
+    t1.synchronize()
+    hip.synchronize()
+    total_ms = t0.elapsed_ms(t1)
+    dom_ms = sum(a.elapsed_ms(b) for a, b in kev) / args.steps
+
+    # measured HBM read ceiling: 2 GiB streamed once per launch
+    big = hip.DeviceArray(2 << 30)
+    sink = hip.DeviceArray(16)
+    e0, e1 = hip.Event(), hip.Event()
+    hip.check(lib.citlali_hip_stream_read(big.vp, big.nbytes, sink.vp))
+    e0.record()
+    for _ in range(5):
+        hip.check(lib.citlali_hip_stream_read(big.vp, big.nbytes, sink.vp))
+    e1.record()
+    e1.synchronize()
+    stream_gbps = 5 * big.nbytes / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    big.close()
+    return total_ms, dominant, dom_ms, per, stream_gbps, host
+
+
+def cpu_baseline(host, budget_s):
+    """The oracle (restated reference arithmetic) on the host cores: one
+    layer step -- every GEMV as repo dequant to fp16 + fp32 dot, attention in
+    fp32 -- repeated until ~budget_s seconds have passed."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    from oracle_binding import Oracle
+    orc = Oracle()
+    threads = int(orc.lib.orc_num_threads())
+    x = host["x"]
+    q = np.ascontiguousarray(host["x"][: HEADS * HEAD_DIM])
+    up = np.ascontiguousarray(np.resize(host["x"], FFN))
+    ins = {"x": x, "att": q, "up": up}
+    runs, t_start = 0, time.perf_counter()
+    while True:
+        for n, k, r, c, i, _ in GEMVS:
+            orc.matvec_f16dot(k, host[n], ins[i], c, r, threads)
+        orc.attention_f32(q, host["k_cache"], host["v_cache"], CTX - 1, HEADS, KV_HEADS, HEAD_DIM, threads)
+        runs += 1
+        el = time.perf_counter() - t_start
+        if el >= budget_s:
+            break
+    step_bytes = sum(kernel_bytes().values())
+    return {"value": round(step_bytes * runs / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{runs} full Qwen3-8B layer step(s) (7 GEMVs dequant->fp16->fp32 dot + fp32 attention "
+                      f"at L={CTX}) in {el:.1f} s"}
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (profiles/<kernel>_pmc.txt, line 'traffic_bytes_per_launch: N')."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the decode hot path here is a single-GPU build "
+              "(multi-GPU sharding is a design note, not a measured mode)", file=sys.stderr)
+        sys.exit(2)
+
+    total_ms, dominant, dom_ms, per, stream_gbps, host = run_gpu(args)
+    kb = kernel_bytes()
+    step_bytes = sum(kb.values())
+    ms_step = total_ms / args.steps
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    achieved = kb[dominant] / (dom_ms * 1e-3) / 1e9
+    line = {
+        "metric": "achieved HBM GB/s (decode attn, Q4_K/Q6_K matvec); Qwen3-8B decode tok/s",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 3: Qwen3-8B one-layer decode (7 Q4_K/Q6_K fused GEMVs + "
+                               "32/8-head attention, head_dim 128, L=8192)",
+                   "layers_rotated": LAYERS, "bytes_per_step": step_bytes,
+                   "layer_tok_per_s_equiv": round(1000.0 / ms_step, 1)},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "bytes_per_launch": kb[dominant], "us_per_launch": round(dom_ms * 1e3, 3),
+                     "traffic": read_traffic(dominant)},
+        "kernels_us": {n: round(per[n] * 1e3, 2) for n in ORDER},
+        "kernels_GBps": {n: round(kb[n] / (per[n] * 1e-3) / 1e9, 1) for n in ORDER},
+        "stream_read_GBps": round(stream_gbps, 1),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

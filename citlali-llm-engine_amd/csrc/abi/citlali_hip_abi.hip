@@ -400,6 +400,12 @@ CITLALI_EXPORT int citlali_hip_argmax(const float* logits, int n, int32_t* out_i
     return CITLALI_OK;
 }
 
+CITLALI_EXPORT int citlali_hip_stream_read(const void* buf, size_t bytes, void* sink) {
+    REQUIRE(buf && sink && aligned(buf, 16) && aligned(sink, 4), "stream_read: bad arguments");
+    HIP_TRY(launch_stream_read(buf, bytes, static_cast<uint32_t*>(sink), g_stream));
+    return CITLALI_OK;
+}
+
 // ---------------------------------------------------------------- events
 CITLALI_EXPORT int citlali_hip_event_create(void** ev) {
     REQUIRE(ev, "null output pointer");

@@ -18,6 +18,16 @@ __device__ __forceinline__ float blk_half(const uint8_t* p) {
     return h2f((uint16_t)(p[0] | (p[1] << 8)));
 }
 
+// The host routines run on x86-64, where a NaN operand propagates with its
+// sign (the first operand's when both are NaN) and an invalid operation
+// (Inf * 0, Inf - Inf) yields the negative default NaN; the host fp16 rule
+// then keeps that sign on the resulting infinity.  AMD hardware makes
+// positive default NaNs, so NaN results get their host sign explicitly.
+// (Only reachable when a block's d or dmin is Inf or NaN.)
+__device__ __forceinline__ float host_nan(bool negative) {
+    return __builtin_bit_cast(float, negative ? 0xffc00000u : 0x7fc00000u);
+}
+
 // element e of a Q4_K block (kernels.cu:209-230)
 __device__ __forceinline__ float q4k_value(const uint8_t* blk, int e) {
     const int j = e >> 6, hi = (e & 63) >= 32;
@@ -33,7 +43,14 @@ __device__ __forceinline__ float q4k_value(const uint8_t* blk, int e) {
     }
     const uint8_t b = blk[16 + 32 * j + (e & 31)];
     const int q = hi ? (b >> 4) : (b & 0x0f);
-    return blk_half(blk) * (float)sc * (float)q - blk_half(blk + 2) * (float)m;
+    const float d = blk_half(blk), dmin = blk_half(blk + 2);
+    const float v = d * (float)sc * (float)q - dmin * (float)m;
+    if (!__builtin_isnan(v)) return v;
+    // host order: (d*sc)*q - dmin*m
+    if (__builtin_isnan(d)) return host_nan(__builtin_signbit(d));
+    if (__builtin_isinf(d) && (sc == 0 || q == 0)) return host_nan(true);
+    if (__builtin_isnan(dmin)) return host_nan(__builtin_signbit(dmin));
+    return host_nan(true);   // dmin*0 with dmin = Inf, or Inf - Inf
 }
 
 // element e of a Q6_K block (kernels.cu:134-172)
@@ -44,7 +61,10 @@ __device__ __forceinline__ float q6k_value(const uint8_t* blk, int e) {
     const int hi2 = (blk[128 + 32 * h + i] >> (2 * part)) & 3;
     const int q = (lo | (hi2 << 4)) - 32;
     const int8_t sc = (int8_t)blk[192 + 8 * h + i / 16 + 2 * part];
-    return blk_half(blk + 208) * (float)sc * (float)q;
+    const float d = blk_half(blk + 208);
+    const float v = d * (float)sc * (float)q;
+    if (!__builtin_isnan(v)) return v;
+    return host_nan(__builtin_isnan(d) ? __builtin_signbit(d) : true);   // NaN d, or Inf * 0
 }
 
 __global__ void embed_q6k_kernel(const uint8_t* __restrict__ table, int32_t token_id, uint16_t* __restrict__ out,

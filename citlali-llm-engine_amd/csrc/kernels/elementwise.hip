@@ -174,6 +174,25 @@ __global__ void fill_zero_bytes_kernel(uint8_t* __restrict__ p, size_t n) {
     if (i < n) p[i] = 0u;
 }
 
+// Streaming read of a large buffer (the achievable HBM read ceiling): every
+// lane reads 16 B per step with a grid-stride loop; the xor of the data is
+// written only if it equals a value the caller never stores, so the loads
+// cannot be dropped.
+__global__ __launch_bounds__(kBlk) void stream_read_kernel(const u32x4* __restrict__ p, size_t n16,
+                                                           uint32_t* __restrict__ sink) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + stride < n16; i += 2 * stride) {
+        a ^= p[i];
+        b ^= p[i + stride];
+    }
+    if (i < n16) a ^= p[i];
+    a ^= b;
+    const uint32_t v = a.x ^ a.y ^ a.z ^ a.w;
+    if (v == 0x9e3779b9u) sink[0] = v;
+}
+
 inline dim3 grid_for(int n) { return dim3((unsigned)((n + kBlk - 1) / kBlk)); }
 
 }  // namespace
@@ -231,6 +250,16 @@ hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool
 
 hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s) {
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, out_index);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hipStream_t s) {
+    int dev = 0, cus = 256;
+    (void)hipGetDevice(&dev);
+    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const size_t n16 = bytes / 16;
+    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)(cus * 8)), dim3(kBlk), 0, s,
+                       static_cast<const u32x4*>(buf), n16, sink);
     return hipGetLastError();
 }
 

@@ -58,5 +58,6 @@ hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool
                              hipStream_t s);
 hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
+hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hipStream_t s);
 
 }  // namespace citlali::hip

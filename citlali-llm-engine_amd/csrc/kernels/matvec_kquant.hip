@@ -187,11 +187,12 @@ struct Q6K {
         const int h = l4 >> 1, ih = l4 & 1;
         const float d = h2f((uint16_t)f.dbits);
         // int8 scales sc[8h + ih + 2k], k = 0..3 (kernels.cu:166-167)
+        // (int8_t casts: the result must be converted as a signed value)
         const uint32_t sh = (uint32_t)ih * 8u;
-        const float sc0 = (float)__builtin_amdgcn_sbfe(f.s0, sh, 8u);
-        const float sc1 = (float)__builtin_amdgcn_sbfe(f.s0, sh + 16u, 8u);
-        const float sc2 = (float)__builtin_amdgcn_sbfe(f.s1, sh, 8u);
-        const float sc3 = (float)__builtin_amdgcn_sbfe(f.s1, sh + 16u, 8u);
+        const float sc0 = (float)(int8_t)(f.s0 >> sh);
+        const float sc1 = (float)(int8_t)(f.s0 >> (sh + 16u));
+        const float sc2 = (float)(int8_t)(f.s1 >> sh);
+        const float sc3 = (float)(int8_t)(f.s1 >> (sh + 16u));
 
         // x pairs of slice k: values 128h + 32k + 16ih + [0,16)
         const uint32_t* xb = xp + ((b * kQK + 128 * h + 16 * ih) >> 1);
@@ -296,7 +297,7 @@ template <class QT, bool kF32, int kRows>
 __global__ __launch_bounds__(kBlock) void matvec_flat_kernel(const uint8_t* __restrict__ w,
                                                              const uint16_t* __restrict__ x,
                                                              void* __restrict__ y, int K, int N,
-                                                             uint32_t magic) {
+                                                             uint64_t magic) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
@@ -321,7 +322,7 @@ __global__ __launch_bounds__(kBlock) void matvec_flat_kernel(const uint8_t* __re
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
             const uint32_t f = (uint32_t)(f0 + u * kSbPerStep + sub);
-            const uint32_t r = __umulhi(f, magic);
+            const uint32_t r = (uint32_t)(((uint64_t)f * magic) >> 32);
             rl[u] = (int)f < nflat ? (int)r : -1;
             bl[u] = (int)(f - r * (uint32_t)nb);
             if (rl[u] >= 0) fr[u] = QT::load(w + ((size_t)row0 * nb + f) * QT::kBytes, l4);
@@ -357,7 +358,8 @@ hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, in
     } else {
         // smallest row count per wave that keeps whole 16-block steps busy
         constexpr int kRows = 4;
-        const uint32_t magic = (uint32_t)((((uint64_t)1) << 32) / (uint64_t)nb + 1u);
+        // floor(f / nb) == (f * magic) >> 32 for every f < 2^20 (nb <= 112)
+        const uint64_t magic = ((uint64_t)1 << 32) / (uint64_t)nb + 1u;
         const int rows_per_block = kRows * kWavesPerBlock;
         const int grid = (N + rows_per_block - 1) / rows_per_block;
         hipLaunchKernelGGL((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x, y,

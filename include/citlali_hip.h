@@ -152,6 +152,9 @@ int citlali_hip_rope(uint16_t* data, int heads, int head_dim, int position, floa
 int citlali_hip_argmax(const float* logits, int n, int32_t* out_index);
 
 /* ---- timing (bench and tests) --------------------------------------------- */
+/* Reads `bytes` (16-byte multiple) of a device buffer once, as fast as the
+ * memory system allows: the measured HBM read ceiling.  `sink`: 4 bytes. */
+int citlali_hip_stream_read(const void* buf, size_t bytes, void* sink);
 int citlali_hip_event_create(void** event);
 int citlali_hip_event_record(void* event);                  /* on the current stream */
 int citlali_hip_event_synchronize(void* event);

@@ -1,6 +1,9 @@
 """ctypes bindings of oracle/liboracle.so (the CPU restatement) and of
 oracle/_ref/libcitlali_ref.so (the reference's own host routines, compiled
-from /root/reference).  Test infrastructure only."""
+from /root/reference).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() as
+the checker and by the cpu_baseline leg of bench.py -- never by the product."""
 from __future__ import annotations
 
 import ctypes
@@ -9,9 +12,9 @@ from ctypes import c_double, c_float, c_int, c_int32, c_size_t, c_uint64, c_void
 
 import numpy as np
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-ORACLE_SO = os.path.join(ROOT, "oracle", "liboracle.so")
-REF_SO = os.path.join(ROOT, "oracle", "_ref", "libcitlali_ref.so")
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libcitlali_ref.so")
 
 _P = c_void_p
 

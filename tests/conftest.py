@@ -13,8 +13,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "citlali-llm-engine_amd")
 if PKG not in sys.path:
     sys.path.insert(0, PKG)
-if os.path.join(ROOT, "tests") not in sys.path:
-    sys.path.insert(0, os.path.join(ROOT, "tests"))
+for _p in (os.path.join(ROOT, "tests"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
 
 from oracle_binding import Oracle, RefLib  # noqa: E402
 
