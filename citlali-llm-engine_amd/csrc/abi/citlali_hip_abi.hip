@@ -58,31 +58,53 @@ int check_matvec(const char* who, const void* w, const void* x, const void* y, i
     return CITLALI_OK;
 }
 
-// Per-device attention workspace used when the caller's `scores` buffer is
-// too small for the split plan.
+// Per-device attention buffers kept by the library: the split-KV partials
+// when the caller's `scores` buffer is too small, and the chunk counters of
+// the fused merge (zeroed when allocated; every launch leaves them at zero).
+// Both grow on demand; launches that overlap on one device would share them.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
 constexpr int kMaxDevices = 64;
 Workspace g_ws[kMaxDevices];
+Workspace g_counters[kMaxDevices];
 std::mutex g_ws_mu;
 
-int workspace_for(size_t bytes, float** out) {
+int grow(Workspace* table, size_t bytes, bool zero, void** out) {
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     REQUIRE(dev >= 0 && dev < kMaxDevices, "device index %d out of range", dev);
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[dev];
+    Workspace& w = table[dev];
     if (w.bytes < bytes) {
-        if (w.ptr) HIP_TRY(hipFree(w.ptr));
+        if (w.ptr) {
+            HIP_TRY(hipStreamSynchronize(g_stream));
+            HIP_TRY(hipFree(w.ptr));
+        }
         w.ptr = nullptr;
         w.bytes = 0;
         HIP_TRY(hipMalloc(&w.ptr, bytes));
+        if (zero) HIP_TRY(hipMemset(w.ptr, 0, bytes));
         w.bytes = bytes;
     }
-    *out = static_cast<float*>(w.ptr);
+    *out = w.ptr;
     return CITLALI_OK;
+}
+
+int workspace_for(size_t bytes, float** out) {
+    void* p = nullptr;
+    const int st = grow(g_ws, bytes, false, &p);
+    *out = static_cast<float*>(p);
+    return st;
+}
+
+int counters_for(int n, int** out) {
+    void* p = nullptr;
+    const size_t bytes = ((size_t)n * sizeof(int) + 255) & ~(size_t)255;
+    const int st = grow(g_counters, bytes, true, &p);
+    *out = static_cast<int*>(p);
+    return st;
 }
 
 constexpr int kAttnTargetBlocks = 512;
@@ -237,12 +259,17 @@ CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_ca
     const AttnPlan p = plan_attention(position + 1, 1, kv_heads, heads, head_dim, kAttnTargetBlocks);
     const size_t need = attention_workspace_bytes(p, 1, heads, head_dim);
     const size_t have = scores ? (size_t)heads * (size_t)max_context * sizeof(float) : 0;
+    a.counters = nullptr;
     if (need == 0) {
         a.workspace = nullptr;
-    } else if (need <= have && aligned(scores, 16)) {
-        a.workspace = scores;
     } else {
-        st = workspace_for(need, &a.workspace);
+        if (need <= have && aligned(scores, 16)) {
+            a.workspace = scores;
+        } else {
+            st = workspace_for(need, &a.workspace);
+            if (st) return st;
+        }
+        st = counters_for(kv_heads, &a.counters);
         if (st) return st;
     }
     HIP_TRY(launch_attention(a, p, g_stream));
@@ -285,6 +312,11 @@ CITLALI_EXPORT int citlali_hip_attention_batched(const uint16_t* q, const uint16
     a.kv_heads = kv_heads;
     a.head_dim = head_dim;
     a.workspace = static_cast<float*>(workspace);
+    a.counters = nullptr;
+    if (need > 0) {
+        const int cst = counters_for(nseq * kv_heads, &a.counters);
+        if (cst) return cst;
+    }
     a.out = out;
     HIP_TRY(launch_attention(a, p, g_stream));
     return CITLALI_OK;
@@ -294,12 +326,15 @@ CITLALI_EXPORT int citlali_hip_release_workspace(void) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     int cur = 0;
     HIP_TRY(hipGetDevice(&cur));
-    for (int d = 0; d < kMaxDevices; ++d) {
-        if (!g_ws[d].ptr) continue;
-        HIP_TRY(hipSetDevice(d));
-        HIP_TRY(hipFree(g_ws[d].ptr));
-        g_ws[d].ptr = nullptr;
-        g_ws[d].bytes = 0;
+    for (Workspace* table : {g_ws, g_counters}) {
+        for (int d = 0; d < kMaxDevices; ++d) {
+            if (!table[d].ptr) continue;
+            HIP_TRY(hipSetDevice(d));
+            HIP_TRY(hipDeviceSynchronize());
+            HIP_TRY(hipFree(table[d].ptr));
+            table[d].ptr = nullptr;
+            table[d].bytes = 0;
+        }
     }
     HIP_TRY(hipSetDevice(cur));
     return CITLALI_OK;

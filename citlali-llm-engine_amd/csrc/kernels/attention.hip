@@ -20,8 +20,11 @@
 //    Exponentials are taken in base 2 with log2(e) folded into the scale.
 //  * Values: lane = (head, 8-dim slice); p * V accumulates in fp32.
 //  * The four waves merge in LDS; a chunk writes (max, sum, acc[head_dim])
-//    per head, and a second small kernel merges chunks by log-sum-exp.  A
-//    sequence that fits one chunk is finished by the first kernel directly.
+//    per head and a second kernel merges the chunks of each query head by
+//    log-sum-exp.  A sequence that fits one chunk is written directly.  A
+//    fused variant (kFused) lets the last workgroup of a (sequence, kv head)
+//    -- found with an agent-scope counter it resets -- do that merge in the
+//    same launch; it is kept for callers that want one launch.
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -32,6 +35,7 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / kWave;
+constexpr int kMaxSplits = 512;   // plan_attention never makes more chunks
 
 template <int HD, int GP>
 struct Cfg {
@@ -57,16 +61,75 @@ size_t split_lds_bytes() {
     using C = Cfg<HD, GP>;
     const size_t tiles = C::kWaveLds * kWaves;
     const size_t merge = (size_t)kWaves * GP * (HD + 2) * sizeof(float);
-    return tiles > merge ? tiles : merge;
+    // tail merge: weights [GP][kMaxSplits], lsum[GP] (padded to 16 B), red[kBlock] float4
+    const size_t tail = ((size_t)GP * (kMaxSplits + 4)) * sizeof(float) + (size_t)kBlock * 16;
+    const size_t m2 = merge > tail ? merge : tail;
+    return tiles > m2 ? tiles : m2;
+}
+
+// Log-sum-exp merge of the chunk partials of `nh` (<= NH) consecutive query
+// heads by one workgroup.  hp: first head's entries ([head][chunk][HD + 4]:
+// acc[HD], max, sum), out: first head's output row.  Phase 1: one wave per
+// head finds the max and keeps the chunk weights exp2(m - max) in LDS;
+// phase 2: thread = (head, 4 dims, chunk subset) with 16-byte loads.
+template <int HD, int NH>
+__device__ __forceinline__ void merge_heads(uint8_t* smem, const float* __restrict__ hp, int nh, int n_splits,
+                                            int n_valid, uint16_t* __restrict__ out) {
+    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+    float* wts = reinterpret_cast<float*>(smem);                  // [NH][kMaxSplits]
+    float* lsum = wts + NH * kMaxSplits;                           // [NH], 4 NH floats reserved
+    const size_t ent = HD + 4;
+    for (int h = wave; h < nh; h += kWaves) {
+        const float* e = hp + (size_t)h * n_splits * ent;
+        float M = -INFINITY;
+        for (int s = lane; s < n_valid; s += kWave) M = fmaxf(M, e[(size_t)s * ent + HD]);
+        M = wave_max(M);
+        float Ls = 0.f;
+        for (int s = lane; s < n_valid; s += kWave) {
+            const float w = exp2f(e[(size_t)s * ent + HD] - M);
+            wts[h * kMaxSplits + s] = w;
+            Ls += e[(size_t)s * ent + HD + 1] * w;
+        }
+        Ls = wave_sum(Ls);
+        if (lane == 0) lsum[h] = Ls;
+    }
+    __syncthreads();
+    constexpr int kQuads = NH * HD / 4;          // <= kBlock
+    constexpr int kGroups = kBlock / kQuads;
+    f32x4* red = reinterpret_cast<f32x4*>(lsum + 4 * NH);
+    const int qd = threadIdx.x % kQuads, g = threadIdx.x / kQuads;
+    const int h = qd / (HD / 4), d4 = qd % (HD / 4);
+    const bool ok = h < nh;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    if (ok) {
+        const float* e = hp + (size_t)h * n_splits * ent + 4 * d4;
+#pragma unroll 8
+        for (int s = g; s < n_valid; s += kGroups)
+            a += *reinterpret_cast<const f32x4*>(e + (size_t)s * ent) * wts[h * kMaxSplits + s];
+    }
+    red[threadIdx.x] = a;
+    __syncthreads();
+    if (ok && g == 0) {
+        for (int gg = 1; gg < kGroups; ++gg) a += red[gg * kQuads + qd];
+        const float inv = 1.f / lsum[h];
+        uint16_t* o = out + (size_t)h * HD + 4 * d4;
+        o[0] = f2h_rne(a.x * inv);
+        o[1] = f2h_rne(a.y * inv);
+        o[2] = f2h_rne(a.z * inv);
+        o[3] = f2h_rne(a.w * inv);
+    }
 }
 
 // Grid: (chunk, kv_head, seq).  `positions` (device, per sequence) or the
 // scalar `position` gives the last cached position of each sequence.
-template <int HD, int GP>
+// kFused: the last chunk of each (sequence, kv head) merges; otherwise the
+// partials are left for attn_merge_kernel.
+template <int HD, int GP, bool kFused>
 __global__ __launch_bounds__(kBlock) void attn_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     long long seq_stride, const int32_t* __restrict__ positions, int position, int heads, int kv_heads,
-    int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits, uint16_t* __restrict__ out) {
+    int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits, int* __restrict__ counters,
+    uint16_t* __restrict__ out) {
     using C = Cfg<HD, GP>;
     extern __shared__ __align__(16) uint8_t smem[];
 
@@ -127,11 +190,10 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
     auto load_tile = [&](int t0) {
 #pragma unroll
         for (int i = 0; i < C::kLoads; ++i) {
-            const int pos = t0 + i * C::kRowsPerLoad + lrow;
-            if (pos < w1) {
-                kr[i] = *reinterpret_cast<const u32x4*>(kbase + (size_t)pos * row_step + lc * 8);
-                vr[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pos * row_step + lc * 8);
-            }
+            // branch-free: rows past the range re-read the last one (never used)
+            const int pos = min(t0 + i * C::kRowsPerLoad + lrow, w1 - 1);
+            kr[i] = *reinterpret_cast<const u32x4*>(kbase + (size_t)pos * row_step + lc * 8);
+            vr[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pos * row_step + lc * 8);
         }
     };
 
@@ -164,16 +226,12 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
             }
             s2 = (a0 + a1) * scale_log2;
         }
-        float mt = s2;
-#pragma unroll
-        for (int off = GP; off < kWave; off <<= 1) mt = fmaxf(mt, __shfl_xor(mt, off, kWave));
+        const float mt = column_max<GP>(s2);
         const float m_new = fmaxf(m_run, mt);
         const bool live = m_new != -INFINITY;
         const float alpha = live ? exp2f(m_run - m_new) : 1.f;
         float pw = live ? exp2f(s2 - m_new) : 0.f;
-        float ps = pw;
-#pragma unroll
-        for (int off = GP; off < kWave; off <<= 1) ps += __shfl_xor(ps, off, kWave);
+        const float ps = column_sum<GP>(pw);
         l_run = l_run * alpha + ps;
         m_run = m_new;
         if (s_lane_ok) pt[sh * C::kTP + sp] = pw;
@@ -203,10 +261,15 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
 
     // combine the position-parallel partial sums of the value phase
     if constexpr (C::kPPar > 1) {
+        // lanes (pp, head, slice) with pp stride GP * kChunks in {8, 16, 32}
 #pragma unroll
-        for (int off = GP * C::kChunks; off < kWave; off <<= 1)
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc[0][k] += __shfl_xor(acc[0][k], off, kWave);
+        for (int k = 0; k < 8; ++k) {
+            float a = acc[0][k];
+            if constexpr (GP * C::kChunks <= 8) a += dpp<DppRor<8>::value>(a);
+            if constexpr (GP * C::kChunks <= 16) a += xor16(a);
+            a += xor32(a);
+            acc[0][k] = a;
+        }
     }
 
     // ---- merge the four waves of the workgroup ----
@@ -244,49 +307,80 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
         if (n_valid == 1) {
             out[((size_t)seq * heads + hq) * HD + d] = f2h_rne(A / Ls);
         } else {
-            float* pe = part + (((size_t)seq * heads + hq) * n_splits + split) * (HD + 2);
-            pe[d] = A;
-            if (d == 0) {
-                pe[HD] = M;
-                pe[HD + 1] = Ls;
+            float* pe = part + (((size_t)seq * heads + hq) * n_splits + split) * (HD + 4);
+            if constexpr (kFused) {
+                // write-through (agent-coherent) stores: the merging workgroup
+                // may run on another XCD, whose L2 does not see this one's
+                __hip_atomic_store(pe + d, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (d == 0) {
+                    __hip_atomic_store(pe + HD, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store(pe + HD + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+            } else {
+                pe[d] = A;
+                if (d == 0) {
+                    pe[HD] = M;
+                    pe[HD + 1] = Ls;
+                }
             }
         }
     }
+    if constexpr (kFused) {
+        if (n_valid == 1) return;
+        // Count finished chunks without a cache-wide write-back: each wave
+        // waits for its write-through stores, then one relaxed agent-scope
+        // increment.  The last chunk invalidates its L2 view once (agent
+        // acquire) and reads the partials with ordinary 16-byte loads.
+        __shared__ int last;
+        wait_vm_all();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int* c = counters + (size_t)seq * kv_heads + kvh;
+            const int done = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last = (done == n_valid - 1);
+            if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        const size_t h0 = (size_t)seq * heads + (size_t)kvh * group;
+        merge_heads<HD, GP>(smem, part + h0 * n_splits * (HD + 4), group, n_splits, n_valid, out + h0 * HD);
+    }
 }
 
-// Grid: (head, seq); block: HD threads.  Log-sum-exp merge of the chunks.
+// Grid: (query head, seq).  Merges one head's chunks (separate-kernel mode).
 template <int HD>
-__global__ __launch_bounds__(HD) void attn_merge_kernel(const float* __restrict__ part,
-                                                        const int32_t* __restrict__ positions, int position,
-                                                        int heads, int chunk, int n_splits,
-                                                        uint16_t* __restrict__ out) {
-    const int hq = blockIdx.x, seq = blockIdx.y, d = threadIdx.x;
+__global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restrict__ part,
+                                                            const int32_t* __restrict__ positions, int position,
+                                                            int heads, int chunk, int n_splits,
+                                                            uint16_t* __restrict__ out) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int hq = blockIdx.x, seq = blockIdx.y;
     const int L = (positions ? positions[seq] : position) + 1;
     const int n_valid = (L + chunk - 1) / chunk;
-    if (n_valid <= 1) return;   // finished by the split kernel
-    const float* pe = part + ((size_t)seq * heads + hq) * n_splits * (HD + 2);
-    float M = -INFINITY;
-    for (int s = 0; s < n_valid; ++s) M = fmaxf(M, pe[(size_t)s * (HD + 2) + HD]);
-    float Ls = 0.f, A = 0.f;
-    for (int s = 0; s < n_valid; ++s) {
-        const float* e = pe + (size_t)s * (HD + 2);
-        const float f = exp2f(e[HD] - M);
-        Ls += e[HD + 1] * f;
-        A += e[d] * f;
-    }
-    out[((size_t)seq * heads + hq) * HD + d] = f2h_rne(A / Ls);
+    if (n_valid <= 1) return;   // written by the split kernel
+    const size_t h0 = (size_t)seq * heads + hq;
+    merge_heads<HD, 1>(smem, part + h0 * n_splits * (HD + 4), 1, n_splits, n_valid, out + h0 * HD);
 }
 
 template <int HD, int GP>
 hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
     const size_t lds = split_lds_bytes<HD, GP>();
     const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)HD));
-    hipLaunchKernelGGL((attn_split_kernel<HD, GP>), dim3(p.n_splits, a.kv_heads, a.nseq), dim3(kBlock), lds,
-                       stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions, a.position, a.heads,
-                       a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2, a.workspace, p.n_splits, a.out);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.n_splits <= 1) return e;
-    hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.heads, a.nseq), dim3(HD), 0, stream, a.workspace,
+    const dim3 grid(p.n_splits, a.kv_heads, a.nseq);
+    if (p.fused || p.n_splits <= 1) {
+        hipLaunchKernelGGL((attn_split_kernel<HD, GP, true>), grid, dim3(kBlock), lds, stream, a.q, a.k_cache,
+                           a.v_cache, a.seq_stride, a.positions, a.position, a.heads, a.kv_heads,
+                           a.heads / a.kv_heads, p.chunk, scale_log2, a.workspace, p.n_splits, a.counters, a.out);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((attn_split_kernel<HD, GP, false>), grid, dim3(kBlock), lds, stream, a.q, a.k_cache,
+                       a.v_cache, a.seq_stride, a.positions, a.position, a.heads, a.kv_heads,
+                       a.heads / a.kv_heads, p.chunk, scale_log2, a.workspace, p.n_splits, a.counters, a.out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t mlds = (size_t)(kMaxSplits + 4) * sizeof(float) + (size_t)kBlock * 16;
+    hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.heads, a.nseq), dim3(kBlock), mlds, stream, a.workspace,
                        a.positions, a.position, a.heads, p.chunk, p.n_splits, a.out);
     return hipGetLastError();
 }
@@ -308,8 +402,12 @@ bool attention_supported(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 8;
 }
 
-// Work split: about `target_blocks` workgroups over all (sequence, kv head)
-// units, whole tiles per wave, chunk a multiple of 4 tiles.
+// Work split: enough chunks for about `target_blocks` workgroups over all
+// (sequence, kv head) units, but 256..512 positions per chunk (64..128 per
+// wave) so the per-workgroup set-up and the partial write stay amortised;
+// chunk a multiple of 4 tiles.  The merge runs as a second kernel: faster on
+// gfx950 than a last-workgroup merge, whose cross-XCD hand-off needs
+// write-through stores and an L2 invalidate.
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
     AttnPlan p{};
     const int group = heads / kv_heads;
@@ -317,20 +415,21 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     const int tp = (64 / p.gp) < 32 ? 64 / p.gp : 32;
     const int quantum = tp * kWaves;
     const long long units = (long long)nseq * kv_heads;
-    long long per_unit = (target_blocks + units - 1) / units;
-    if (per_unit < 1) per_unit = 1;
-    long long chunk = (max_len + per_unit - 1) / per_unit;
+    long long chunk = ((long long)max_len * units + target_blocks - 1) / target_blocks;
+    chunk = chunk < 256 ? 256 : chunk > 512 ? 512 : chunk;
+    const long long min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;   // merge LDS bound
+    if (chunk < min_chunk) chunk = min_chunk;
     chunk = ((chunk + quantum - 1) / quantum) * quantum;
-    if (chunk < quantum) chunk = quantum;
     p.chunk = (int)chunk;
     p.n_splits = (int)((max_len + chunk - 1) / chunk);
+    p.fused = false;
     (void)head_dim;
     return p;
 }
 
 size_t attention_workspace_bytes(const AttnPlan& p, int nseq, int heads, int head_dim) {
     if (p.n_splits <= 1) return 0;
-    return (size_t)nseq * heads * p.n_splits * (head_dim + 2) * sizeof(float);
+    return (size_t)nseq * heads * p.n_splits * (head_dim + 4) * sizeof(float);
 }
 
 hipError_t launch_attention(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {

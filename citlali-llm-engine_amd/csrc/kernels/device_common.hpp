@@ -63,20 +63,77 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
-// Butterfly reductions over the 64 lanes of a wave (every lane gets the
-// result).  `Width` limits the butterfly to groups of that many lanes.
-template <int Width = kWave>
+// ---- cross-lane moves on the VALU (DPP and permlane swaps, no LDS) ----
+// DPP controls (GFX9 encoding)
+constexpr int kDppXor1 = 0xB1;     // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;     // quad_perm [2,3,0,1]
+template <int N>
+struct DppRor { static constexpr int value = 0x120 + N; };   // row_ror:N (N = 1..15)
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), Ctrl, 0xF, 0xF, false));
+}
+// value of lane ^ 16 (ds_swizzle SWAP16, no LDS memory access)
+__device__ __forceinline__ float xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+// value of lane ^ 32
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, kWave); }
+
+// Sum over all 64 lanes; every lane gets the same (wave-uniform) result.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = Width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-    return v;
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<DppRor<4>::value>(v);
+    v += dpp<DppRor<8>::value>(v);
+    v += xor16(v);
+    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    return lo + hi;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<DppRor<4>::value>(v));
+    v = fmaxf(v, dpp<DppRor<8>::value>(v));
+    v = fmaxf(v, xor16(v));
+    const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    return fmaxf(lo, hi);
 }
 
-template <int Width = kWave>
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = Width / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
-    return v;
+// Reductions over the lanes that share lane % G (G = 1, 2, 4, 8, 16): the
+// 64 / G lanes of one "column"; every lane gets its column's result.
+template <int G>
+__device__ __forceinline__ float column_sum(float v) {
+    if constexpr (G < 2) v += dpp<kDppXor1>(v);
+    if constexpr (G < 4) v += dpp<kDppXor2>(v);
+    if constexpr (G < 8) v += dpp<DppRor<4>::value>(v);
+    if constexpr (G < 16) v += dpp<DppRor<8>::value>(v);
+    v += xor16(v);
+    return v + xor32(v);
+}
+template <int G>
+__device__ __forceinline__ float column_max(float v) {
+    if constexpr (G < 2) v = fmaxf(v, dpp<kDppXor1>(v));
+    if constexpr (G < 4) v = fmaxf(v, dpp<kDppXor2>(v));
+    if constexpr (G < 8) v = fmaxf(v, dpp<DppRor<4>::value>(v));
+    if constexpr (G < 16) v = fmaxf(v, dpp<DppRor<8>::value>(v));
+    v = fmaxf(v, xor16(v));
+    return fmaxf(v, xor32(v));
+}
+
+// Waits until every earlier vector memory operation of this wave has
+// completed (s_waitcnt vmcnt(0)), e.g. write-through stores before a flag.
+__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Workgroup barrier that orders LDS only: earlier global loads stay in
+// flight across it (a full __syncthreads would wait for them).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Orders LDS traffic between lanes of one wave (no workgroup barrier): the

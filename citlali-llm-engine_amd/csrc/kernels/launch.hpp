@@ -25,12 +25,14 @@ struct AttnArgs {
     int position;
     int nseq, heads, kv_heads, head_dim;
     float* workspace;          // chunk partials, attention_workspace_bytes()
+    int* counters;             // [nseq][kv_heads] ints, zero between launches
     uint16_t* out;             // [nseq][heads][head_dim]
 };
 struct AttnPlan {
     int gp;        // padded GQA group (1, 2, 4, 8)
     int chunk;     // positions per workgroup
     int n_splits;  // chunks of the longest sequence
+    bool fused;    // chunk merge by the last workgroup (else a second kernel)
 };
 bool attention_supported(int head_dim, int group);
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks);

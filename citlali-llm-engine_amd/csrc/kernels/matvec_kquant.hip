@@ -36,6 +36,54 @@ constexpr int kBatch = 4;        // wave steps whose loads are issued together
 // x staging: permuted fp16 pairs + per-group sums.
 // ---------------------------------------------------------------------------
 
+// Permutes one run of eight x values into LDS and writes its share of the
+// group sums (see stage_x).
+template <bool kQ6>
+__device__ __forceinline__ void stage_x8(const u32x4 raw, int v8, uint32_t* xp, float* sx) {
+    u32x4 perm;
+    perm.x = __builtin_amdgcn_perm(raw.y, raw.x, 0x05040100u);
+    perm.y = __builtin_amdgcn_perm(raw.y, raw.x, 0x07060302u);
+    perm.z = __builtin_amdgcn_perm(raw.w, raw.z, 0x05040100u);
+    perm.w = __builtin_amdgcn_perm(raw.w, raw.z, 0x07060302u);
+    *reinterpret_cast<u32x4*>(xp + (size_t)v8 * 4) = perm;
+    float s = 0.f;
+    s += h2f(raw.x & 0xffffu) + h2f(raw.x >> 16);
+    s += h2f(raw.y & 0xffffu) + h2f(raw.y >> 16);
+    s += h2f(raw.z & 0xffffu) + h2f(raw.z >> 16);
+    s += h2f(raw.w & 0xffffu) + h2f(raw.w >> 16);
+    if constexpr (!kQ6) {
+        s += dpp<kDppXor1>(s);
+        s += dpp<kDppXor2>(s);
+        if ((v8 & 3) == 0) sx[v8 >> 2] = s;
+    } else {
+        s += dpp<kDppXor1>(s);
+        if ((v8 & 1) == 0) {
+            const int v = v8 * 8;
+            const int b = v >> 8, in = v & 255;
+            const int h = in >> 7, k = (in & 127) >> 5, ih = (in & 31) >> 4;
+            sx[b * 16 + h * 8 + ih * 4 + k] = s;
+        }
+    }
+}
+
+// x staging split in two so its global loads can be issued before the weight
+// loads: vmcnt retires loads in order, so x issued last would wait for every
+// weight load.  kIter = K / (8 * kBlock) runs of eight values per thread.
+template <bool kQ6, int kIter>
+struct XStage {
+    u32x4 raw[kIter];
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ x) {
+#pragma unroll
+        for (int i = 0; i < kIter; ++i)
+            raw[i] = *reinterpret_cast<const u32x4*>(x + ((size_t)i * kBlock + threadIdx.x) * 8);
+    }
+    __device__ __forceinline__ void store(uint32_t* xp, float* sx) const {
+#pragma unroll
+        for (int i = 0; i < kIter; ++i) stage_x8<kQ6>(raw[i], i * kBlock + threadIdx.x, xp, sx);
+        lds_barrier();
+    }
+};
+
 // Q4_K lanes need sum(x) over each 32-value group (index b*8 + g).
 // Q6_K lanes need sum(x) over 16-value slices, stored in the order
 // [b][h][ih][k] so one lane's four slices are contiguous.
@@ -57,11 +105,11 @@ __device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int K, u
         s += h2f(raw.w & 0xffffu) + h2f(raw.w >> 16);
         if constexpr (!kQ6) {
             // four consecutive threads hold one 32-value group (256 % 4 == 0)
-            s += __shfl_xor(s, 1, kWave);
-            s += __shfl_xor(s, 2, kWave);
+            s += dpp<kDppXor1>(s);
+            s += dpp<kDppXor2>(s);
             if ((v8 & 3) == 0) sx[v8 >> 2] = s;
         } else {
-            s += __shfl_xor(s, 1, kWave);
+            s += dpp<kDppXor1>(s);
             if ((v8 & 1) == 0) {
                 const int v = v8 * 8;
                 const int b = v >> 8, in = v & 255;
@@ -70,7 +118,7 @@ __device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int K, u
             }
         }
     }
-    __syncthreads();
+    lds_barrier();
 }
 
 // ---------------------------------------------------------------------------
@@ -171,14 +219,16 @@ struct Q6K {
         load16(sb + 64 * h + 16 * ih, s, f.wa);
         load16(sb + 64 * h + 32 + 16 * ih, s, f.wb);
         load16(sb + 128 + 32 * h + 16 * ih, s, f.u);
-        // scales[8h .. 8h+8): dword window starting 4 - s bytes before them
-        // (ends at most at byte 210 of the block)
-        const uint8_t* sw = sb + 192 + 8 * h - (4 - s);
+        // scales[8h .. 8h+8) from the dword window [188 + 8h + s, +12) of the
+        // block (inside its 210 bytes for s = 0 and s = 2); they start
+        // o = 4 - s bytes into it.  Branch-free, so loads stay countable.
+        const uint8_t* sw = sb + 188 + 8 * h + s;
         const uint32_t w0 = *reinterpret_cast<const uint32_t*>(sw);
         const uint32_t w1 = *reinterpret_cast<const uint32_t*>(sw + 4);
         const uint32_t w2 = *reinterpret_cast<const uint32_t*>(sw + 8);
-        f.s0 = s ? align_bytes(w0, w1, 2u) : w1;
-        f.s1 = s ? align_bytes(w1, w2, 2u) : w2;
+        const uint32_t o = 8u * (4u - s);
+        f.s0 = (uint32_t)((((uint64_t)w1 << 32) | w0) >> o);
+        f.s1 = (uint32_t)((((uint64_t)w2 << 32) | w1) >> o);
         f.dbits = *reinterpret_cast<const uint16_t*>(sb + 208);
         return f;
     }
@@ -239,54 +289,56 @@ __device__ __forceinline__ void store_y(void* y, int row, float v) {
     }
 }
 
-// Rows whose super-block count is a multiple of 16: every wave step stays
-// inside one row, so the row of a step is wave-uniform.
-template <class QT, bool kF32>
-__global__ __launch_bounds__(kBlock) void matvec_rows16_kernel(const uint8_t* __restrict__ w,
+// Rows of 16*S super-blocks, streamed: each wave walks rows gw, gw + W, ...
+// (W = waves in the grid), a row being S steps of 16 super-blocks, and keeps
+// the next D = S*M steps' fragments in flight while it computes the current
+// one (a ring of D register slots, indices fixed at compile time by
+// unrolling M rows).  x is loaded before the first fragments and staged in
+// LDS behind them.  Loads are branch-free (rows past N re-read row N-1).
+template <class QT, bool kF32, int S, int M>
+__global__ __launch_bounds__(kBlock) void matvec_stream_kernel(const uint8_t* __restrict__ w,
                                                                const uint16_t* __restrict__ x,
-                                                               void* __restrict__ y, int K, int N,
-                                                               int rows_per_wave) {
+                                                               void* __restrict__ y, int K, int N) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
-    stage_x<QT::kSxPerBlock == 16>(x, K, xp, sx);
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
     const int l4 = lane & 3;
     const int sub = lane >> 2;
-    const int nb = K >> 8;
-    const int steps_per_row = nb / kSbPerStep;
-    const int row0 = (blockIdx.x * kWavesPerBlock + wave) * rows_per_wave;
-    const int rows = min(rows_per_wave, N - row0);
-    const int total = rows * steps_per_row;
+    constexpr int nb = S * kSbPerStep;
+    constexpr int D = S * M;
+    const int W = gridDim.x * kWavesPerBlock;
+    const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
 
-    float acc = 0.f;
-    for (int t0 = 0; t0 < total; t0 += kBatch) {
-        typename QT::Frag fr[kBatch];
+    auto frag_at = [&](int row, int t) {
+        const size_t f = (size_t)min(row, N - 1) * nb + t * kSbPerStep + sub;
+        return QT::load(w + f * QT::kBytes, l4);
+    };
+
+    XStage<QT::kSxPerBlock == 16, 2 * S> xs;   // K = 4096 * S
+    xs.load(x);
+    __builtin_amdgcn_sched_barrier(0);   // issue order: x, first fragments, staging
+    typename QT::Frag fr[D];
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int t = t0 + u;
-            if (t < total) {
-                const int r = t / steps_per_row;
-                const int i = t - r * steps_per_row;
-                const size_t f = (size_t)(row0 + r) * nb + (size_t)i * kSbPerStep + sub;
-                fr[u] = QT::load(w + f * QT::kBytes, l4);
-            }
-        }
+    for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-            const int t = t0 + u;
-            if (t < total) {
-                const int r = t / steps_per_row;
-                const int i = t - r * steps_per_row;
-                acc += QT::dot(fr[u], l4, xp, sx, i * kSbPerStep + sub);
-                if (i == steps_per_row - 1) {
-                    const float s = wave_sum(acc);
-                    if (lane == 0) store_y<kF32>(y, row0 + r, s);
-                    acc = 0.f;
-                }
+        for (int t = 0; t < S; ++t) fr[m * S + t] = frag_at(gw + m * W, t);
+    __builtin_amdgcn_sched_barrier(0);
+    xs.store(xp, sx);
+
+    for (int row = gw; row < N; row += M * W) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const int r = row + m * W;
+            float acc = 0.f;
+#pragma unroll
+            for (int t = 0; t < S; ++t) {
+                acc += QT::dot(fr[m * S + t], l4, xp, sx, t * kSbPerStep + sub);
+                fr[m * S + t] = frag_at(r + M * W, t);   // refill the slot
             }
+            acc = wave_sum(acc);
+            if (lane == 0 && r < N) store_y<kF32>(y, r, acc);
         }
     }
 }
@@ -343,27 +395,45 @@ __global__ __launch_bounds__(kBlock) void matvec_flat_kernel(const uint8_t* __re
     }
 }
 
+int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+// Two workgroups per CU, never more waves than rows.
+template <class QT, bool kF32, int S, int M>
+void launch_stream(const uint8_t* w, const uint16_t* x, void* y, int K, int N, size_t lds, hipStream_t stream) {
+    int grid = 2 * device_cus();
+    const int need = (N + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (grid > need) grid = need;
+    hipLaunchKernelGGL((matvec_stream_kernel<QT, kF32, S, M>), dim3(grid), dim3(kBlock), lds, stream, w, x, y, K, N);
+}
+
 template <class QT, bool kF32>
 hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, int N, hipStream_t stream) {
     const int nb = K / kQK;
     const size_t lds = (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float);
-    if (nb % kSbPerStep == 0) {
-        // aim for >= 512 blocks, up to 8 rows per wave
-        int rpw = N / (kWavesPerBlock * 512);
-        rpw = rpw < 1 ? 1 : (rpw > 8 ? 8 : rpw);
-        const int rows_per_block = rpw * kWavesPerBlock;
-        const int grid = (N + rows_per_block - 1) / rows_per_block;
-        hipLaunchKernelGGL((matvec_rows16_kernel<QT, kF32>), dim3(grid), dim3(kBlock), lds, stream, w, x, y, K,
-                           N, rpw);
-    } else {
-        // smallest row count per wave that keeps whole 16-block steps busy
-        constexpr int kRows = 4;
-        // floor(f / nb) == (f * magic) >> 32 for every f < 2^20 (nb <= 112)
-        const uint64_t magic = ((uint64_t)1 << 32) / (uint64_t)nb + 1u;
-        const int rows_per_block = kRows * kWavesPerBlock;
-        const int grid = (N + rows_per_block - 1) / rows_per_block;
-        hipLaunchKernelGGL((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x, y,
-                           K, N, magic);
+    switch (nb) {
+        case 16: launch_stream<QT, kF32, 1, 2>(w, x, y, K, N, lds, stream); break;
+        case 32: launch_stream<QT, kF32, 2, 1>(w, x, y, K, N, lds, stream); break;
+        case 48: launch_stream<QT, kF32, 3, 1>(w, x, y, K, N, lds, stream); break;
+        case 64: launch_stream<QT, kF32, 4, 1>(w, x, y, K, N, lds, stream); break;
+        default: {
+            // any other length: flat walk over the super-blocks of 4 rows
+            constexpr int kRows = 4;
+            // floor(f / nb) == (f * magic) >> 32 for every f < 2^20 (nb <= 112)
+            const uint64_t magic = ((uint64_t)1 << 32) / (uint64_t)nb + 1u;
+            const int rows_per_block = kRows * kWavesPerBlock;
+            const int grid = (N + rows_per_block - 1) / rows_per_block;
+            hipLaunchKernelGGL((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x,
+                               y, K, N, magic);
+        }
     }
     return hipGetLastError();
 }
