@@ -12,9 +12,11 @@ quant blocks with d, dmin in [1e-3, 1e-2]; N(0,1) fp16 activations/caches)
 and are resident in HBM before timing starts.
 
 value = algorithmic bytes per step / time per step (GB/s, all kernels of the
-step).  roofline: the kernel with the largest share of step time, its
-algorithmic bytes per launch over its average launch duration measured with
-HIP events on the launch stream inside the timed steps.  cpu_baseline: the
+step; HIP events on the launch stream around the K timed steps).  roofline:
+the kernel with the largest share of step time, its algorithmic bytes per
+launch over its average launch duration over a second pass of the same K
+steps, from HIP events that the kernel's own dispatches stamp
+(hipExtLaunchKernel; for attention, split start to merge end).  cpu_baseline: the
 oracle's restatement of the reference's host arithmetic (dequant to fp16 with
 the host rule, fp32 dot; fp32 attention) on a bounded sample of the same
 layer, on this machine's host cores.
@@ -34,6 +36,7 @@ sys.path.insert(0, os.path.join(ROOT, "citlali-llm-engine_amd"))
 
 HBM_PEAK_GBPS = 8000.0
 LAYERS = 4
+COPY_HALVES = 1 << 29   # 1 GiB read + 1 GiB written by the calibration copy
 HIDDEN, FFN, HEADS, KV_HEADS, HEAD_DIM, CTX = 4096, 12288, 32, 8, 128, 8192
 
 # (name, kind, rows=out_features, cols=in_features, input, output)
@@ -102,13 +105,14 @@ def run_gpu(args):
             k, r, c, i, o = spec[name]
             hip.device.matvec(k, layer.w[name], act[i], act[o], c, r)
 
-    def step(s, timed_kernel=None, evs=None):
+    def step(s, timed=None):
+        """One layer; `timed` maps kernel names to KernelTimers (HIP events
+        stamped by the kernels' own dispatches on the launch stream)."""
         layer = layers[s % LAYERS]
         for name in ORDER:
-            if name == timed_kernel:
-                evs[0].record()
-                launch(name, layer)
-                evs[1].record()
+            if timed and name in timed:
+                with timed[name]:
+                    launch(name, layer)
             else:
                 launch(name, layer)
 
@@ -116,32 +120,32 @@ def run_gpu(args):
     for s in range(args.warmup):
         step(s)
     hip.synchronize()
-    per = {n: 0.0 for n in ORDER}
-    ev = [hip.Event() for _ in range(len(ORDER) + 1)]
-    cal = max(4, LAYERS)
+    cal = max(8, 2 * LAYERS)
+    cal_timers = [{n: hip.device.KernelTimer() for n in ORDER} for _ in range(cal)]
     for s in range(cal):
-        layer = layers[s % LAYERS]
-        ev[0].record()
-        for j, name in enumerate(ORDER):
-            launch(name, layer)
-            ev[j + 1].record()
-        ev[-1].synchronize()
-        for j, name in enumerate(ORDER):
-            per[name] += ev[j].elapsed_ms(ev[j + 1]) / cal
+        step(s, cal_timers[s])
+    hip.synchronize()
+    per = {n: sum(t[n].ms() for t in cal_timers) / cal for n in ORDER}
     dominant = max(per, key=per.get)
 
-    # timed region: K steps, events around the dominant kernel's launches
+    # timed region: K steps, nothing armed (value, ms_per_step)
     hip.synchronize()
     t0, t1 = hip.Event(), hip.Event()
-    kev = [(hip.Event(), hip.Event()) for _ in range(args.steps)]
     t0.record()
     for s in range(args.steps):
-        step(s, dominant, kev[s])
+        step(s)
     t1.record()
     t1.synchronize()
     hip.synchronize()
     total_ms = t0.elapsed_ms(t1)
-    dom_ms = sum(a.elapsed_ms(b) for a, b in kev) / args.steps
+    # the same K steps again with the dominant kernel's launches timed (a
+    # dispatch that stamps events is scheduled slightly differently, so this
+    # pass is kept out of `value`)
+    dom_timers = [hip.device.KernelTimer() for _ in range(args.steps)]
+    for s in range(args.steps):
+        step(s, {dominant: dom_timers[s]})
+    hip.synchronize()
+    dom_ms = sum(t.ms() for t in dom_timers) / args.steps
 
     # measured HBM read ceiling: 2 GiB streamed once per launch
     big = hip.DeviceArray(2 << 30)
@@ -154,8 +158,18 @@ def run_gpu(args):
     e1.record()
     e1.synchronize()
     stream_gbps = 5 * big.nbytes / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    # plain copy kernel of known size (COPY_HALVES fp16 read + written): the
+    # calibration launch for rocprofv3 FETCH_SIZE / WRITE_SIZE counters
+    dst = hip.DeviceArray(COPY_HALVES * 2)
+    hip.check(lib.citlali_hip_copy(big.vp, dst.vp, COPY_HALVES))
+    e0.record()
+    hip.check(lib.citlali_hip_copy(big.vp, dst.vp, COPY_HALVES))
+    e1.record()
+    e1.synchronize()
+    copy_gbps = 2 * COPY_HALVES * 2 / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    dst.close()
     big.close()
-    return total_ms, dominant, dom_ms, per, stream_gbps, host
+    return total_ms, dominant, dom_ms, per, (stream_gbps, copy_gbps), host
 
 
 def cpu_baseline(host, budget_s):
@@ -185,14 +199,18 @@ def cpu_baseline(host, budget_s):
                       f"at L={CTX}) in {el:.1f} s"}
 
 
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "cfg3_layer_hbm_traffic_pmc.md")
+
+
 def read_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary (profiles/<kernel>_pmc.txt, line 'traffic_bytes_per_launch: N')."""
-    path = os.path.join(ROOT, "profiles", f"{kernel}_pmc.txt")
-    if not os.path.exists(path):
+    """HBM bytes per launch of `kernel` (a step-kernel name) from the
+    committed rocprofv3 PMC summary: the line 'traffic_bytes_per_launch
+    <kernel>: N' (FETCH_SIZE + WRITE_SIZE, scaled by the copy calibration)."""
+    if not os.path.exists(PMC_SUMMARY):
         return None
-    for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
+    key = f"traffic_bytes_per_launch {kernel}:"
+    for line in open(PMC_SUMMARY):
+        if line.startswith(key):
             return int(float(line.split(":", 1)[1]))
     return None
 
@@ -210,7 +228,7 @@ def main():
               "(multi-GPU sharding is a design note, not a measured mode)", file=sys.stderr)
         sys.exit(2)
 
-    total_ms, dominant, dom_ms, per, stream_gbps, host = run_gpu(args)
+    total_ms, dominant, dom_ms, per, (stream_gbps, copy_gbps), host = run_gpu(args)
     kb = kernel_bytes()
     step_bytes = sum(kb.values())
     ms_step = total_ms / args.steps
@@ -240,6 +258,7 @@ def main():
         "kernels_us": {n: round(per[n] * 1e3, 2) for n in ORDER},
         "kernels_GBps": {n: round(kb[n] / (per[n] * 1e-3) / 1e9, 1) for n in ORDER},
         "stream_read_GBps": round(stream_gbps, 1),
+        "copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": None,
     }
     if not args.no_cpu:

@@ -58,58 +58,47 @@ int check_matvec(const char* who, const void* w, const void* x, const void* y, i
     return CITLALI_OK;
 }
 
-// Per-device attention buffers kept by the library: the split-KV partials
-// when the caller's `scores` buffer is too small, and the chunk counters of
-// the fused merge (zeroed when allocated; every launch leaves them at zero).
-// Both grow on demand; launches that overlap on one device would share them.
+// Per-device attention workspace kept by the library for the split-KV
+// partials when the caller's `scores` buffer is too small.  It grows on
+// demand; launches that overlap on one device would share it.
 struct Workspace {
     void* ptr = nullptr;
     size_t bytes = 0;
 };
 constexpr int kMaxDevices = 64;
 Workspace g_ws[kMaxDevices];
-Workspace g_counters[kMaxDevices];
 std::mutex g_ws_mu;
 
-int grow(Workspace* table, size_t bytes, bool zero, void** out) {
+int workspace_for(size_t bytes, float** out) {
     int dev = 0;
     HIP_TRY(hipGetDevice(&dev));
     REQUIRE(dev >= 0 && dev < kMaxDevices, "device index %d out of range", dev);
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = table[dev];
+    Workspace& w = g_ws[dev];
     if (w.bytes < bytes) {
         if (w.ptr) {
-            HIP_TRY(hipStreamSynchronize(g_stream));
+            HIP_TRY(hipStreamSynchronize(g_stream));   // a queued launch may still use it
             HIP_TRY(hipFree(w.ptr));
         }
         w.ptr = nullptr;
         w.bytes = 0;
         HIP_TRY(hipMalloc(&w.ptr, bytes));
-        if (zero) HIP_TRY(hipMemset(w.ptr, 0, bytes));
         w.bytes = bytes;
     }
-    *out = w.ptr;
+    *out = static_cast<float*>(w.ptr);
     return CITLALI_OK;
-}
-
-int workspace_for(size_t bytes, float** out) {
-    void* p = nullptr;
-    const int st = grow(g_ws, bytes, false, &p);
-    *out = static_cast<float*>(p);
-    return st;
-}
-
-int counters_for(int n, int** out) {
-    void* p = nullptr;
-    const size_t bytes = ((size_t)n * sizeof(int) + 255) & ~(size_t)255;
-    const int st = grow(g_counters, bytes, true, &p);
-    *out = static_cast<int*>(p);
-    return st;
 }
 
 constexpr int kAttnTargetBlocks = 512;
 
 }  // namespace
+
+namespace citlali::hip {
+KernelTiming& kernel_timing() {
+    thread_local KernelTiming t;
+    return t;
+}
+}  // namespace citlali::hip
 
 using namespace citlali::hip;
 
@@ -251,6 +240,7 @@ CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_ca
     a.seq_stride = 0;
     a.positions = nullptr;
     a.position = position;
+    a.max_len = position + 1;
     a.nseq = 1;
     a.heads = heads;
     a.kv_heads = kv_heads;
@@ -259,17 +249,12 @@ CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_ca
     const AttnPlan p = plan_attention(position + 1, 1, kv_heads, heads, head_dim, kAttnTargetBlocks);
     const size_t need = attention_workspace_bytes(p, 1, heads, head_dim);
     const size_t have = scores ? (size_t)heads * (size_t)max_context * sizeof(float) : 0;
-    a.counters = nullptr;
     if (need == 0) {
         a.workspace = nullptr;
+    } else if (need <= have && aligned(scores, 16)) {
+        a.workspace = scores;
     } else {
-        if (need <= have && aligned(scores, 16)) {
-            a.workspace = scores;
-        } else {
-            st = workspace_for(need, &a.workspace);
-            if (st) return st;
-        }
-        st = counters_for(kv_heads, &a.counters);
+        st = workspace_for(need, &a.workspace);
         if (st) return st;
     }
     HIP_TRY(launch_attention(a, p, g_stream));
@@ -307,16 +292,12 @@ CITLALI_EXPORT int citlali_hip_attention_batched(const uint16_t* q, const uint16
     a.seq_stride = seq_stride;
     a.positions = positions;
     a.position = 0;
+    a.max_len = max_positions_bound;
     a.nseq = nseq;
     a.heads = heads;
     a.kv_heads = kv_heads;
     a.head_dim = head_dim;
     a.workspace = static_cast<float*>(workspace);
-    a.counters = nullptr;
-    if (need > 0) {
-        const int cst = counters_for(nseq * kv_heads, &a.counters);
-        if (cst) return cst;
-    }
     a.out = out;
     HIP_TRY(launch_attention(a, p, g_stream));
     return CITLALI_OK;
@@ -326,18 +307,20 @@ CITLALI_EXPORT int citlali_hip_release_workspace(void) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
     int cur = 0;
     HIP_TRY(hipGetDevice(&cur));
-    for (Workspace* table : {g_ws, g_counters}) {
-        for (int d = 0; d < kMaxDevices; ++d) {
-            if (!table[d].ptr) continue;
-            HIP_TRY(hipSetDevice(d));
-            HIP_TRY(hipDeviceSynchronize());
-            HIP_TRY(hipFree(table[d].ptr));
-            table[d].ptr = nullptr;
-            table[d].bytes = 0;
+    int st = CITLALI_OK;
+    for (int d = 0; d < kMaxDevices && st == CITLALI_OK; ++d) {
+        Workspace& w = g_ws[d];
+        if (!w.ptr) continue;
+        st = hip_status(hipSetDevice(d), "hipSetDevice(d)", __FILE__, __LINE__);
+        if (st == CITLALI_OK) st = hip_status(hipDeviceSynchronize(), "hipDeviceSynchronize()", __FILE__, __LINE__);
+        if (st == CITLALI_OK) st = hip_status(hipFree(w.ptr), "hipFree(w.ptr)", __FILE__, __LINE__);
+        if (st == CITLALI_OK) {
+            w.ptr = nullptr;
+            w.bytes = 0;
         }
     }
-    HIP_TRY(hipSetDevice(cur));
-    return CITLALI_OK;
+    const int st2 = hip_status(hipSetDevice(cur), "hipSetDevice(cur)", __FILE__, __LINE__);
+    return st != CITLALI_OK ? st : st2;
 }
 
 CITLALI_EXPORT int citlali_hip_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
@@ -442,6 +425,14 @@ CITLALI_EXPORT int citlali_hip_stream_read(const void* buf, size_t bytes, void* 
 }
 
 // ---------------------------------------------------------------- events
+CITLALI_EXPORT int citlali_hip_set_kernel_timing(void* start, void* stop) {
+    REQUIRE((start == nullptr) == (stop == nullptr), "set_kernel_timing: give both events or neither");
+    KernelTiming& t = kernel_timing();
+    t.start = static_cast<hipEvent_t>(start);
+    t.stop = static_cast<hipEvent_t>(stop);
+    return CITLALI_OK;
+}
+
 CITLALI_EXPORT int citlali_hip_event_create(void** ev) {
     REQUIRE(ev, "null output pointer");
     hipEvent_t e = nullptr;

@@ -1,0 +1,87 @@
+// kernels.cpp -- the compute:: launchers over the C ABI.  Each forwards its
+// arguments unchanged (reference kernels.cu:659-876 launchers) and turns a
+// non-zero status into citlali::Error.
+#include "citlali/compute/hip/kernels.h"
+
+#include "citlali/compute/hip/hip_check.h"
+
+namespace citlali::compute {
+
+void device_zero(void* data, std::size_t bytes) { CITLALI_HIP_CHECK(citlali_hip_zero(data, bytes)); }
+
+void launch_embed(const uint16_t* embedding, int32_t token_id, uint16_t* out, int hidden) {
+    CITLALI_HIP_CHECK(citlali_hip_embed(embedding, token_id, out, hidden));
+}
+
+void launch_copy(const uint16_t* input, uint16_t* output, int n) {
+    CITLALI_HIP_CHECK(citlali_hip_copy(input, output, n));
+}
+
+void launch_add_inplace(uint16_t* target, const uint16_t* delta, int n) {
+    CITLALI_HIP_CHECK(citlali_hip_add_inplace(target, delta, n));
+}
+
+void launch_add_bias_inplace(uint16_t* target, const uint16_t* bias, int n) {
+    CITLALI_HIP_CHECK(citlali_hip_add_bias_inplace(target, bias, n));
+}
+
+void launch_rms_norm(const uint16_t* input, const uint16_t* weight, uint16_t* output, int n, float eps) {
+    CITLALI_HIP_CHECK(citlali_hip_rms_norm(input, weight, output, n, eps));
+}
+
+void launch_rms_norm_heads(const uint16_t* input, const uint16_t* weight, uint16_t* output, int heads,
+                           int head_dim, float eps) {
+    CITLALI_HIP_CHECK(citlali_hip_rms_norm_heads(input, weight, output, heads, head_dim, eps));
+}
+
+void launch_matvec_fp16(const uint16_t* weight, const uint16_t* input, uint16_t* output, int in_features,
+                        int out_features) {
+    CITLALI_HIP_CHECK(citlali_hip_matvec_fp16(weight, input, output, in_features, out_features));
+}
+
+void launch_matvec_fp16_to_float(const uint16_t* weight, const uint16_t* input, float* output, int in_features,
+                                 int out_features) {
+    CITLALI_HIP_CHECK(citlali_hip_matvec_fp16_to_float(weight, input, output, in_features, out_features));
+}
+
+void launch_matvec_q4k(const uint8_t* weight, const uint16_t* input, uint16_t* output, int in_features,
+                       int out_features) {
+    CITLALI_HIP_CHECK(citlali_hip_matvec_q4k(weight, input, output, in_features, out_features));
+}
+
+void launch_matvec_q6k(const uint8_t* weight, const uint16_t* input, uint16_t* output, int in_features,
+                       int out_features) {
+    CITLALI_HIP_CHECK(citlali_hip_matvec_q6k(weight, input, output, in_features, out_features));
+}
+
+void launch_matvec_q6k_to_float(const uint8_t* weight, const uint16_t* input, float* output, int in_features,
+                                int out_features) {
+    CITLALI_HIP_CHECK(citlali_hip_matvec_q6k_to_float(weight, input, output, in_features, out_features));
+}
+
+void launch_embed_q6k(const uint8_t* embedding, int32_t token_id, uint16_t* output, int hidden) {
+    CITLALI_HIP_CHECK(citlali_hip_embed_q6k(embedding, token_id, output, hidden));
+}
+
+void launch_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* output, int n) {
+    CITLALI_HIP_CHECK(citlali_hip_swiglu(gate, up, output, n));
+}
+
+void launch_rope(uint16_t* data, int heads, int head_dim, int position, float theta) {
+    CITLALI_HIP_CHECK(citlali_hip_rope(data, heads, head_dim, position, theta));
+}
+
+void launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* k_cache, uint16_t* v_cache, int position,
+                     int kv_size) {
+    CITLALI_HIP_CHECK(citlali_hip_store_kv(k, v, k_cache, v_cache, position, kv_size));
+}
+
+void launch_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* scores,
+                      uint16_t* output, int position, int max_context, int heads, int kv_heads, int head_dim) {
+    CITLALI_HIP_CHECK(citlali_hip_attention(q, k_cache, v_cache, scores, output, position, max_context, heads,
+                                            kv_heads, head_dim));
+}
+
+void synchronize() { CITLALI_HIP_CHECK(citlali_hip_synchronize()); }
+
+}  // namespace citlali::compute

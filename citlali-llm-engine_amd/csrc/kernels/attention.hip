@@ -21,10 +21,10 @@
 //  * Values: lane = (head, 8-dim slice); p * V accumulates in fp32.
 //  * The four waves merge in LDS; a chunk writes (max, sum, acc[head_dim])
 //    per head and a second kernel merges the chunks of each query head by
-//    log-sum-exp.  A sequence that fits one chunk is written directly.  A
-//    fused variant (kFused) lets the last workgroup of a (sequence, kv head)
-//    -- found with an agent-scope counter it resets -- do that merge in the
-//    same launch; it is kept for callers that want one launch.
+//    log-sum-exp.  A sequence that fits one chunk is written directly.
+//    (Merging in the last workgroup of the same launch measured slower on
+//    gfx950: the hand-off across XCDs needs write-through stores and an L2
+//    invalidate.)
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -61,84 +61,42 @@ size_t split_lds_bytes() {
     using C = Cfg<HD, GP>;
     const size_t tiles = C::kWaveLds * kWaves;
     const size_t merge = (size_t)kWaves * GP * (HD + 2) * sizeof(float);
-    // tail merge: weights [GP][kMaxSplits], lsum[GP] (padded to 16 B), red[kBlock] float4
-    const size_t tail = ((size_t)GP * (kMaxSplits + 4)) * sizeof(float) + (size_t)kBlock * 16;
-    const size_t m2 = merge > tail ? merge : tail;
-    return tiles > m2 ? tiles : m2;
+    return tiles > merge ? tiles : merge;
 }
 
-// Log-sum-exp merge of the chunk partials of `nh` (<= NH) consecutive query
-// heads by one workgroup.  hp: first head's entries ([head][chunk][HD + 4]:
-// acc[HD], max, sum), out: first head's output row.  Phase 1: one wave per
-// head finds the max and keeps the chunk weights exp2(m - max) in LDS;
-// phase 2: thread = (head, 4 dims, chunk subset) with 16-byte loads.
-template <int HD, int NH>
-__device__ __forceinline__ void merge_heads(uint8_t* smem, const float* __restrict__ hp, int nh, int n_splits,
-                                            int n_valid, uint16_t* __restrict__ out) {
-    const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    float* wts = reinterpret_cast<float*>(smem);                  // [NH][kMaxSplits]
-    float* lsum = wts + NH * kMaxSplits;                           // [NH], 4 NH floats reserved
-    const size_t ent = HD + 4;
-    for (int h = wave; h < nh; h += kWaves) {
-        const float* e = hp + (size_t)h * n_splits * ent;
-        float M = -INFINITY;
-        for (int s = lane; s < n_valid; s += kWave) M = fmaxf(M, e[(size_t)s * ent + HD]);
-        M = wave_max(M);
-        float Ls = 0.f;
-        for (int s = lane; s < n_valid; s += kWave) {
-            const float w = exp2f(e[(size_t)s * ent + HD] - M);
-            wts[h * kMaxSplits + s] = w;
-            Ls += e[(size_t)s * ent + HD + 1] * w;
-        }
-        Ls = wave_sum(Ls);
-        if (lane == 0) lsum[h] = Ls;
-    }
-    __syncthreads();
-    constexpr int kQuads = NH * HD / 4;          // <= kBlock
-    constexpr int kGroups = kBlock / kQuads;
-    f32x4* red = reinterpret_cast<f32x4*>(lsum + 4 * NH);
-    const int qd = threadIdx.x % kQuads, g = threadIdx.x / kQuads;
-    const int h = qd / (HD / 4), d4 = qd % (HD / 4);
-    const bool ok = h < nh;
-    f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    if (ok) {
-        const float* e = hp + (size_t)h * n_splits * ent + 4 * d4;
-#pragma unroll 8
-        for (int s = g; s < n_valid; s += kGroups)
-            a += *reinterpret_cast<const f32x4*>(e + (size_t)s * ent) * wts[h * kMaxSplits + s];
-    }
-    red[threadIdx.x] = a;
-    __syncthreads();
-    if (ok && g == 0) {
-        for (int gg = 1; gg < kGroups; ++gg) a += red[gg * kQuads + qd];
-        const float inv = 1.f / lsum[h];
-        uint16_t* o = out + (size_t)h * HD + 4 * d4;
-        o[0] = f2h_rne(a.x * inv);
-        o[1] = f2h_rne(a.y * inv);
-        o[2] = f2h_rne(a.z * inv);
-        o[3] = f2h_rne(a.w * inv);
-    }
+// merge kernel: weights [kMaxSplits], lsum (padded to 16 B), red[kBlock] float4
+constexpr size_t kMergeLds = (size_t)(kMaxSplits + 4) * sizeof(float) + (size_t)kBlock * 16;
+
+// Positions a sequence covers and its chunk count.  A position at or beyond
+// the caller's bound `max_len` is cut there, so neither the cache reads nor
+// the chunk index leave their buffers.
+struct SeqSpan {
+    int len, n_valid;
+};
+__device__ __forceinline__ SeqSpan seq_span(const int32_t* positions, int position, int seq, int chunk,
+                                            int max_len) {
+    int L = (positions ? positions[seq] : position) + 1;
+    L = min(L, max_len);
+    return {L, L > 0 ? (L + chunk - 1) / chunk : 0};
 }
 
 // Grid: (chunk, kv_head, seq).  `positions` (device, per sequence) or the
 // scalar `position` gives the last cached position of each sequence.
-// kFused: the last chunk of each (sequence, kv head) merges; otherwise the
-// partials are left for attn_merge_kernel.
-template <int HD, int GP, bool kFused>
+template <int HD, int GP>
 __global__ __launch_bounds__(kBlock) void attn_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
-    long long seq_stride, const int32_t* __restrict__ positions, int position, int heads, int kv_heads,
-    int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits, int* __restrict__ counters,
+    long long seq_stride, const int32_t* __restrict__ positions, int position, int max_len, int heads,
+    int kv_heads, int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits,
     uint16_t* __restrict__ out) {
     using C = Cfg<HD, GP>;
     extern __shared__ __align__(16) uint8_t smem[];
 
     const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
-    const int L = (positions ? positions[seq] : position) + 1;
+    const SeqSpan span = seq_span(positions, position, seq, chunk, max_len);
+    const int L = span.len, n_valid = span.n_valid;
     const int b0 = split * chunk;
     if (b0 >= L) return;
     const int b1 = min(L, b0 + chunk);
-    const int n_valid = (L + chunk - 1) / chunk;
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
@@ -308,80 +266,81 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
             out[((size_t)seq * heads + hq) * HD + d] = f2h_rne(A / Ls);
         } else {
             float* pe = part + (((size_t)seq * heads + hq) * n_splits + split) * (HD + 4);
-            if constexpr (kFused) {
-                // write-through (agent-coherent) stores: the merging workgroup
-                // may run on another XCD, whose L2 does not see this one's
-                __hip_atomic_store(pe + d, A, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (d == 0) {
-                    __hip_atomic_store(pe + HD, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(pe + HD + 1, Ls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            } else {
-                pe[d] = A;
-                if (d == 0) {
-                    pe[HD] = M;
-                    pe[HD + 1] = Ls;
-                }
+            pe[d] = A;
+            if (d == 0) {
+                pe[HD] = M;
+                pe[HD + 1] = Ls;
             }
         }
     }
-    if constexpr (kFused) {
-        if (n_valid == 1) return;
-        // Count finished chunks without a cache-wide write-back: each wave
-        // waits for its write-through stores, then one relaxed agent-scope
-        // increment.  The last chunk invalidates its L2 view once (agent
-        // acquire) and reads the partials with ordinary 16-byte loads.
-        __shared__ int last;
-        wait_vm_all();
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            int* c = counters + (size_t)seq * kv_heads + kvh;
-            const int done = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            last = (done == n_valid - 1);
-            if (last) __hip_atomic_store(c, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!last) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-        const size_t h0 = (size_t)seq * heads + (size_t)kvh * group;
-        merge_heads<HD, GP>(smem, part + h0 * n_splits * (HD + 4), group, n_splits, n_valid, out + h0 * HD);
-    }
 }
 
-// Grid: (query head, seq).  Merges one head's chunks (separate-kernel mode).
+// Grid: (query head, seq).  Log-sum-exp merge of one head's chunk partials
+// ([chunk][HD + 4]: acc[HD], max, sum).  Phase 1: wave 0 finds the max and
+// keeps the chunk weights exp2(m - max) in LDS; phase 2: thread = (4 dims,
+// chunk subset) with 16-byte loads, reduced through LDS.
 template <int HD>
 __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restrict__ part,
                                                             const int32_t* __restrict__ positions, int position,
-                                                            int heads, int chunk, int n_splits,
+                                                            int max_len, int heads, int chunk, int n_splits,
                                                             uint16_t* __restrict__ out) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int hq = blockIdx.x, seq = blockIdx.y;
-    const int L = (positions ? positions[seq] : position) + 1;
-    const int n_valid = (L + chunk - 1) / chunk;
+    const int n_valid = seq_span(positions, position, seq, chunk, max_len).n_valid;
     if (n_valid <= 1) return;   // written by the split kernel
     const size_t h0 = (size_t)seq * heads + hq;
-    merge_heads<HD, 1>(smem, part + h0 * n_splits * (HD + 4), 1, n_splits, n_valid, out + h0 * HD);
+    const float* hp = part + h0 * n_splits * (HD + 4);
+    constexpr size_t ent = HD + 4;
+    float* wts = reinterpret_cast<float*>(smem);   // [kMaxSplits]
+    float* lsum = wts + kMaxSplits;                // 4 floats reserved
+    if (threadIdx.x < kWave) {
+        const int lane = threadIdx.x;
+        float M = -INFINITY;
+        for (int s = lane; s < n_valid; s += kWave) M = fmaxf(M, hp[(size_t)s * ent + HD]);
+        M = wave_max(M);
+        float Ls = 0.f;
+        for (int s = lane; s < n_valid; s += kWave) {
+            const float w = exp2f(hp[(size_t)s * ent + HD] - M);
+            wts[s] = w;
+            Ls += hp[(size_t)s * ent + HD + 1] * w;
+        }
+        Ls = wave_sum(Ls);
+        if (lane == 0) lsum[0] = Ls;
+    }
+    __syncthreads();
+    constexpr int kQuads = HD / 4;
+    constexpr int kGroups = kBlock / kQuads;
+    f32x4* red = reinterpret_cast<f32x4*>(lsum + 4);
+    const int d4 = threadIdx.x % kQuads, g = threadIdx.x / kQuads;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    const float* e = hp + 4 * d4;
+#pragma unroll 8
+    for (int s = g; s < n_valid; s += kGroups) a += *reinterpret_cast<const f32x4*>(e + (size_t)s * ent) * wts[s];
+    red[threadIdx.x] = a;
+    __syncthreads();
+    if (g == 0) {
+        for (int gg = 1; gg < kGroups; ++gg) a += red[gg * kQuads + d4];
+        const float inv = 1.f / lsum[0];
+        uint16_t* o = out + h0 * HD + 4 * d4;
+        o[0] = f2h_rne(a.x * inv);
+        o[1] = f2h_rne(a.y * inv);
+        o[2] = f2h_rne(a.z * inv);
+        o[3] = f2h_rne(a.w * inv);
+    }
 }
 
 template <int HD, int GP>
 hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
     const size_t lds = split_lds_bytes<HD, GP>();
     const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)HD));
-    const dim3 grid(p.n_splits, a.kv_heads, a.nseq);
-    if (p.fused || p.n_splits <= 1) {
-        hipLaunchKernelGGL((attn_split_kernel<HD, GP, true>), grid, dim3(kBlock), lds, stream, a.q, a.k_cache,
-                           a.v_cache, a.seq_stride, a.positions, a.position, a.heads, a.kv_heads,
-                           a.heads / a.kv_heads, p.chunk, scale_log2, a.workspace, p.n_splits, a.counters, a.out);
-        return hipGetLastError();
-    }
-    hipLaunchKernelGGL((attn_split_kernel<HD, GP, false>), grid, dim3(kBlock), lds, stream, a.q, a.k_cache,
-                       a.v_cache, a.seq_stride, a.positions, a.position, a.heads, a.kv_heads,
-                       a.heads / a.kv_heads, p.chunk, scale_log2, a.workspace, p.n_splits, a.counters, a.out);
+    launch_kernel_in_call(p.n_splits <= 1, (attn_split_kernel<HD, GP>), dim3(p.n_splits, a.kv_heads, a.nseq),
+                          dim3(kBlock), lds, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
+                          a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
+                          a.workspace, p.n_splits, a.out);
     const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    const size_t mlds = (size_t)(kMaxSplits + 4) * sizeof(float) + (size_t)kBlock * 16;
-    hipLaunchKernelGGL((attn_merge_kernel<HD>), dim3(a.heads, a.nseq), dim3(kBlock), mlds, stream, a.workspace,
-                       a.positions, a.position, a.heads, p.chunk, p.n_splits, a.out);
+    if (e != hipSuccess || p.n_splits <= 1) return e;
+    launch_kernel((attn_merge_kernel<HD>), dim3(a.heads, a.nseq), dim3(kBlock), kMergeLds, stream, a.workspace,
+                  a.positions, a.position, a.max_len, a.heads, p.chunk, p.n_splits, a.out);
     return hipGetLastError();
 }
 
@@ -405,9 +364,8 @@ bool attention_supported(int head_dim, int group) {
 // Work split: enough chunks for about `target_blocks` workgroups over all
 // (sequence, kv head) units, but 256..512 positions per chunk (64..128 per
 // wave) so the per-workgroup set-up and the partial write stay amortised;
-// chunk a multiple of 4 tiles.  The merge runs as a second kernel: faster on
-// gfx950 than a last-workgroup merge, whose cross-XCD hand-off needs
-// write-through stores and an L2 invalidate.
+// chunk a multiple of 4 tiles, and at most kMaxSplits chunks (the merge's
+// LDS weight table).
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
     AttnPlan p{};
     const int group = heads / kv_heads;
@@ -422,7 +380,6 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     chunk = ((chunk + quantum - 1) / quantum) * quantum;
     p.chunk = (int)chunk;
     p.n_splits = (int)((max_len + chunk - 1) / chunk);
-    p.fused = false;
     (void)head_dim;
     return p;
 }

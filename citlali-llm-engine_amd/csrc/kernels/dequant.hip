@@ -96,7 +96,7 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, uint64_t count, ui
 
 hipError_t launch_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden, hipStream_t s) {
     const int block = 256;
-    hipLaunchKernelGGL(embed_q6k_kernel, dim3((hidden + block - 1) / block), dim3(block), 0, s, table, token_id,
+    launch_kernel(embed_q6k_kernel, dim3((hidden + block - 1) / block), dim3(block), 0, s, table, token_id,
                        out, hidden);
     return hipGetLastError();
 }
@@ -110,13 +110,13 @@ static dim3 dequant_grid(uint64_t count) {
 
 hipError_t launch_dequant_q4k_f16(const uint8_t* w, uint64_t count, uint16_t* out, hipStream_t s) {
     const dim3 g = dequant_grid(count);
-    hipLaunchKernelGGL(dequant_kernel<4>, g, dim3(256), 0, s, w, count, out);
+    launch_kernel(dequant_kernel<4>, g, dim3(256), 0, s, w, count, out);
     return hipGetLastError();
 }
 
 hipError_t launch_dequant_q6k_f16(const uint8_t* w, uint64_t count, uint16_t* out, hipStream_t s) {
     const dim3 g = dequant_grid(count);
-    hipLaunchKernelGGL(dequant_kernel<6>, g, dim3(256), 0, s, w, count, out);
+    launch_kernel(dequant_kernel<6>, g, dim3(256), 0, s, w, count, out);
     return hipGetLastError();
 }
 

@@ -199,57 +199,57 @@ inline dim3 grid_for(int n) { return dim3((unsigned)((n + kBlk - 1) / kBlk)); }
 
 hipError_t launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc, int position,
                            int kv_size, hipStream_t s) {
-    hipLaunchKernelGGL(store_kv_kernel, grid_for(kv_size), dim3(kBlk), 0, s, k, v, kc, vc, position, kv_size);
+    launch_kernel(store_kv_kernel, grid_for(kv_size), dim3(kBlk), 0, s, k, v, kc, vc, position, kv_size);
     return hipGetLastError();
 }
 
 hipError_t launch_embed_f16(const uint16_t* t, int32_t token_id, uint16_t* out, int hidden, hipStream_t s) {
-    hipLaunchKernelGGL(embed_f16_kernel, grid_for(hidden), dim3(kBlk), 0, s, t, token_id, out, hidden);
+    launch_kernel(embed_f16_kernel, grid_for(hidden), dim3(kBlk), 0, s, t, token_id, out, hidden);
     return hipGetLastError();
 }
 
 hipError_t launch_copy(const uint16_t* in, uint16_t* out, int n, hipStream_t s) {
-    hipLaunchKernelGGL(copy_kernel, grid_for(n), dim3(kBlk), 0, s, in, out, n);
+    launch_kernel(copy_kernel, grid_for(n), dim3(kBlk), 0, s, in, out, n);
     return hipGetLastError();
 }
 
 hipError_t launch_add_inplace(uint16_t* t, const uint16_t* d, int n, hipStream_t s) {
-    hipLaunchKernelGGL(add_inplace_kernel, grid_for(n), dim3(kBlk), 0, s, t, d, n);
+    launch_kernel(add_inplace_kernel, grid_for(n), dim3(kBlk), 0, s, t, d, n);
     return hipGetLastError();
 }
 
 hipError_t launch_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, int n, float eps, hipStream_t s) {
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(1), dim3(1024), 0, s, in, w, out, n, eps);
+    launch_kernel(rms_norm_kernel, dim3(1), dim3(1024), 0, s, in, w, out, n, eps);
     return hipGetLastError();
 }
 
 hipError_t launch_rms_norm_heads(const uint16_t* in, const uint16_t* w, uint16_t* out, int heads, int head_dim,
                                  float eps, hipStream_t s) {
-    hipLaunchKernelGGL(rms_norm_kernel, dim3(heads), dim3(kWave * 2), 0, s, in, w, out, head_dim, eps);
+    launch_kernel(rms_norm_kernel, dim3(heads), dim3(kWave * 2), 0, s, in, w, out, head_dim, eps);
     return hipGetLastError();
 }
 
 hipError_t launch_rope(uint16_t* data, int heads, int head_dim, int position, float theta, hipStream_t s) {
     const int threads = ((head_dim / 2 + kWave - 1) / kWave) * kWave;
-    hipLaunchKernelGGL(rope_kernel, dim3(heads), dim3(threads), 0, s, data, head_dim, position, theta);
+    launch_kernel(rope_kernel, dim3(heads), dim3(threads), 0, s, data, head_dim, position, theta);
     return hipGetLastError();
 }
 
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, int n, hipStream_t s) {
-    hipLaunchKernelGGL(swiglu_kernel, grid_for(n), dim3(kBlk), 0, s, g, u, out, n);
+    launch_kernel(swiglu_kernel, grid_for(n), dim3(kBlk), 0, s, g, u, out, n);
     return hipGetLastError();
 }
 
 hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
                              hipStream_t s) {
     const dim3 g((unsigned)((N + (kBlk / kWave) - 1) / (kBlk / kWave)));
-    if (f32_out) hipLaunchKernelGGL(matvec_f16_kernel<true>, g, dim3(kBlk), 0, s, w, x, y, K, N);
-    else hipLaunchKernelGGL(matvec_f16_kernel<false>, g, dim3(kBlk), 0, s, w, x, y, K, N);
+    if (f32_out) launch_kernel(matvec_f16_kernel<true>, g, dim3(kBlk), 0, s, w, x, y, K, N);
+    else launch_kernel(matvec_f16_kernel<false>, g, dim3(kBlk), 0, s, w, x, y, K, N);
     return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s) {
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, out_index);
+    launch_kernel(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, out_index);
     return hipGetLastError();
 }
 
@@ -258,7 +258,7 @@ hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hip
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const size_t n16 = bytes / 16;
-    hipLaunchKernelGGL(stream_read_kernel, dim3((unsigned)(cus * 8)), dim3(kBlk), 0, s,
+    launch_kernel(stream_read_kernel, dim3((unsigned)(cus * 8)), dim3(kBlk), 0, s,
                        static_cast<const u32x4*>(buf), n16, sink);
     return hipGetLastError();
 }
@@ -269,10 +269,10 @@ hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
         const size_t words = bytes / 4;
         size_t blocks = (words + kBlk - 1) / kBlk;
         if (blocks > 65536) blocks = 65536;
-        hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(kBlk), 0, s, (uint32_t*)p, words);
+        launch_kernel(fill_zero_kernel, dim3((unsigned)blocks), dim3(kBlk), 0, s, (uint32_t*)p, words);
     } else {
         size_t blocks = (bytes + kBlk - 1) / kBlk;
-        hipLaunchKernelGGL(fill_zero_bytes_kernel, dim3((unsigned)blocks), dim3(kBlk), 0, s, (uint8_t*)p, bytes);
+        launch_kernel(fill_zero_bytes_kernel, dim3((unsigned)blocks), dim3(kBlk), 0, s, (uint8_t*)p, bytes);
     }
     return hipGetLastError();
 }

@@ -2,11 +2,44 @@
 // C-ABI layer (csrc/abi/citlali_hip.hip) after it has validated arguments.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
 
 namespace citlali::hip {
+
+// ---- kernel timing (citlali_hip_set_kernel_timing) ----
+// While armed on a thread, the first kernel that thread launches records
+// `start` when it begins and the last kernel of each call records `stop`
+// when it ends (hipExtLaunchKernel stamps the events from the dispatch
+// itself), so the elapsed time is the kernels' own time, without the
+// queueing gap an event recorded on the stream would add.
+struct KernelTiming {
+    hipEvent_t start = nullptr;
+    hipEvent_t stop = nullptr;
+};
+KernelTiming& kernel_timing();   // thread-local state, defined by the ABI unit
+
+// Every launch of the library goes through here; `last` is false for a
+// kernel that another kernel of the same call follows.
+template <typename Kernel, typename... Args>
+inline void launch_kernel_in_call(bool last, Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                                  Args... args) {
+    KernelTiming& t = kernel_timing();
+    if (t.start == nullptr && (t.stop == nullptr || !last)) {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+        return;
+    }
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, t.start, last ? t.stop : nullptr, 0u,
+                          args...);
+    t.start = nullptr;
+}
+
+template <typename Kernel, typename... Args>
+inline void launch_kernel(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+    launch_kernel_in_call(true, kernel, grid, block, lds, stream, args...);
+}
 
 // ---- fused dequant GEMV (matvec_kquant.hip) ----
 size_t matvec_lds_bytes(int kind, int K);
@@ -23,16 +56,15 @@ struct AttnArgs {
     long long seq_stride;      // elements
     const int32_t* positions;  // device [nseq] or null (then `position`)
     int position;
+    int max_len;               // positions past max_len - 1 are ignored (the plan's bound)
     int nseq, heads, kv_heads, head_dim;
     float* workspace;          // chunk partials, attention_workspace_bytes()
-    int* counters;             // [nseq][kv_heads] ints, zero between launches
     uint16_t* out;             // [nseq][heads][head_dim]
 };
 struct AttnPlan {
     int gp;        // padded GQA group (1, 2, 4, 8)
     int chunk;     // positions per workgroup
     int n_splits;  // chunks of the longest sequence
-    bool fused;    // chunk merge by the last workgroup (else a second kernel)
 };
 bool attention_supported(int head_dim, int group);
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks);

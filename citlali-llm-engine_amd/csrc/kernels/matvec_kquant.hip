@@ -412,7 +412,7 @@ void launch_stream(const uint8_t* w, const uint16_t* x, void* y, int K, int N, s
     int grid = 2 * device_cus();
     const int need = (N + kWavesPerBlock - 1) / kWavesPerBlock;
     if (grid > need) grid = need;
-    hipLaunchKernelGGL((matvec_stream_kernel<QT, kF32, S, M>), dim3(grid), dim3(kBlock), lds, stream, w, x, y, K, N);
+    launch_kernel((matvec_stream_kernel<QT, kF32, S, M>), dim3(grid), dim3(kBlock), lds, stream, w, x, y, K, N);
 }
 
 template <class QT, bool kF32>
@@ -431,7 +431,7 @@ hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, in
             const uint64_t magic = ((uint64_t)1 << 32) / (uint64_t)nb + 1u;
             const int rows_per_block = kRows * kWavesPerBlock;
             const int grid = (N + rows_per_block - 1) / rows_per_block;
-            hipLaunchKernelGGL((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x,
+            launch_kernel((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x,
                                y, K, N, magic);
         }
     }

@@ -67,6 +67,7 @@ SIGNATURES = [
     ("citlali_hip_rope", c_int, [_P, c_int, c_int, c_int, c_float]),
     ("citlali_hip_argmax", c_int, [_P, c_int, _P]),
     ("citlali_hip_stream_read", c_int, [_P, c_size_t, _P]),
+    ("citlali_hip_set_kernel_timing", c_int, [_P, _P]),
     ("citlali_hip_event_create", c_int, [POINTER(c_void_p)]),
     ("citlali_hip_event_record", c_int, [_P]),
     ("citlali_hip_event_synchronize", c_int, [_P]),

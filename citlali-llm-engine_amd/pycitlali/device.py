@@ -95,6 +95,27 @@ class Event:
             pass
 
 
+class KernelTimer:
+    """Kernel-own time of the library calls made inside `with timer:` (the
+    first kernel's start to the last kernel's end, stamped by the dispatch).
+    Use `ms()` after the stream has passed the calls."""
+
+    def __init__(self):
+        self.start, self.stop = Event(), Event()
+
+    def __enter__(self):
+        _lib.call("citlali_hip_set_kernel_timing", self.start.h, self.stop.h)
+        return self
+
+    def __exit__(self, *exc):
+        _lib.call("citlali_hip_set_kernel_timing", ctypes.c_void_p(0), ctypes.c_void_p(0))
+        return False
+
+    def ms(self) -> float:
+        self.stop.synchronize()
+        return self.start.elapsed_ms(self.stop)
+
+
 def _vp(x) -> ctypes.c_void_p:
     if isinstance(x, DeviceArray):
         return x.vp
@@ -139,3 +160,47 @@ def embed_q6k(table, token_id: int, out, hidden: int) -> None:
 def dequant_f16(kind: str, w, count: int, out) -> None:
     name = "citlali_hip_dequant_q4k_f16" if kind == "q4k" else "citlali_hip_dequant_q6k_f16"
     _lib.call(name, _vp(w), ctypes.c_uint64(count), _vp(out))
+
+
+# ---- the rest of forward_token (kernels.h:8-37 launchers) ----------------
+def rms_norm(x, w, out, n: int, eps: float) -> None:
+    _lib.call("citlali_hip_rms_norm", _vp(x), _vp(w), _vp(out), int(n), ctypes.c_float(eps))
+
+
+def rms_norm_heads(x, w, out, heads: int, head_dim: int, eps: float) -> None:
+    _lib.call("citlali_hip_rms_norm_heads", _vp(x), _vp(w), _vp(out), int(heads), int(head_dim),
+              ctypes.c_float(eps))
+
+
+def rope(data, heads: int, head_dim: int, position: int, theta: float) -> None:
+    _lib.call("citlali_hip_rope", _vp(data), int(heads), int(head_dim), int(position), ctypes.c_float(theta))
+
+
+def swiglu(gate, up, out, n: int) -> None:
+    _lib.call("citlali_hip_swiglu", _vp(gate), _vp(up), _vp(out), int(n))
+
+
+def add_inplace(target, delta, n: int) -> None:
+    _lib.call("citlali_hip_add_inplace", _vp(target), _vp(delta), int(n))
+
+
+def add_bias_inplace(target, bias, n: int) -> None:
+    _lib.call("citlali_hip_add_bias_inplace", _vp(target), _vp(bias), int(n))
+
+
+def store_kv(k, v, k_cache, v_cache, position: int, kv_size: int) -> None:
+    _lib.call("citlali_hip_store_kv", _vp(k), _vp(v), _vp(k_cache), _vp(v_cache), int(position), int(kv_size))
+
+
+def embed(table, token_id: int, out, hidden: int) -> None:
+    _lib.call("citlali_hip_embed", _vp(table), ctypes.c_int32(token_id), _vp(out), int(hidden))
+
+
+def copy(src, dst, n: int) -> None:
+    _lib.call("citlali_hip_copy", _vp(src), _vp(dst), int(n))
+
+
+def argmax(logits, n: int, out_index) -> None:
+    """Index of the first largest finite value of `n` fp32 logits, written to
+    the device int32 `out_index` (0 when none is finite)."""
+    _lib.call("citlali_hip_argmax", _vp(logits), int(n), _vp(out_index))

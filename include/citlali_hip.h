@@ -110,7 +110,8 @@ int citlali_hip_attention(const uint16_t* q, const uint16_t* k_cache, const uint
  * reference decodes one sequence; per sequence the result equals
  * launch_attention).  q/out [nseq][heads][head_dim]; sequence s uses the
  * caches at k_cache + s*seq_stride (elements); positions: device int32
- * [nseq], each < max_positions_bound; workspace of
+ * [nseq], each < max_positions_bound (a larger one is treated as
+ * max_positions_bound - 1, so no read leaves the caches); workspace of
  * citlali_hip_attention_workspace_bytes() bytes (may be NULL if that is 0). */
 int citlali_hip_attention_batched(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                   long long seq_stride, const int32_t* positions, int max_positions_bound,
@@ -155,6 +156,13 @@ int citlali_hip_argmax(const float* logits, int n, int32_t* out_index);
 /* Reads `bytes` (16-byte multiple) of a device buffer once, as fast as the
  * memory system allows: the measured HBM read ceiling.  `sink`: 4 bytes. */
 int citlali_hip_stream_read(const void* buf, size_t bytes, void* sink);
+/* Kernel timing (no reference counterpart; for benchmarks): while armed with
+ * two events of citlali_hip_event_create, the first kernel the calling thread
+ * launches records `start` when it begins and every kernel records `stop`
+ * when it ends, stamped from the dispatch itself (hipExtLaunchKernel), so
+ * citlali_hip_event_elapsed_ms(start, stop) is the kernels' own time.  Arm
+ * before a call, disarm with (NULL, NULL) after it. */
+int citlali_hip_set_kernel_timing(void* start, void* stop);
 int citlali_hip_event_create(void** event);
 int citlali_hip_event_record(void* event);                  /* on the current stream */
 int citlali_hip_event_synchronize(void* event);

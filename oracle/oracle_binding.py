@@ -120,6 +120,47 @@ class Oracle:
         return out
 
 
+    # the rest of forward_token (all fp16 bit patterns in and out)
+    def rms_norm(self, x, w, eps) -> np.ndarray:
+        x, w = np.ascontiguousarray(x, np.uint16), np.ascontiguousarray(w, np.uint16)
+        out = np.empty_like(x)
+        self.lib.orc_rms_norm(_p(x), _p(w), _p(out), x.size, eps)
+        return out
+
+    def rms_norm_heads(self, x, w, heads, head_dim, eps) -> np.ndarray:
+        x, w = np.ascontiguousarray(x, np.uint16), np.ascontiguousarray(w, np.uint16)
+        out = np.empty_like(x)
+        self.lib.orc_rms_norm_heads(_p(x), _p(w), _p(out), heads, head_dim, eps)
+        return out
+
+    def rope(self, x, heads, head_dim, position, theta) -> np.ndarray:
+        out = np.array(x, np.uint16, copy=True)
+        self.lib.orc_rope(_p(out), heads, head_dim, position, theta)
+        return out
+
+    def swiglu(self, g, u) -> np.ndarray:
+        g, u = np.ascontiguousarray(g, np.uint16), np.ascontiguousarray(u, np.uint16)
+        out = np.empty_like(g)
+        self.lib.orc_swiglu(_p(g), _p(u), _p(out), g.size)
+        return out
+
+    def add(self, t, d) -> np.ndarray:
+        out = np.array(t, np.uint16, copy=True)
+        d = np.ascontiguousarray(d, np.uint16)
+        self.lib.orc_add_inplace(_p(out), _p(d), out.size)
+        return out
+
+    def store_kv(self, k, v, kc, vc, position) -> tuple:
+        k, v = np.ascontiguousarray(k, np.uint16), np.ascontiguousarray(v, np.uint16)
+        kc, vc = np.array(kc, np.uint16, copy=True), np.array(vc, np.uint16, copy=True)
+        self.lib.orc_store_kv(_p(k), _p(v), _p(kc), _p(vc), position, k.size)
+        return kc, vc
+
+    def argmax(self, logits) -> int:
+        logits = np.ascontiguousarray(logits, np.float32)
+        return int(self.lib.orc_argmax(_p(logits), logits.size))
+
+
 class RefLib:
     """The reference's own host fp16 and dequant routines (oracle/_ref)."""
 

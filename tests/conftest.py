@@ -38,6 +38,13 @@ def ref() -> RefLib:
 
 
 @pytest.fixture(scope="session")
+def synth():
+    """Seeded synthetic inputs (host only, no GPU)."""
+    from pycitlali import synth as s
+    return s
+
+
+@pytest.fixture(scope="session")
 def hip():
     """The product library on a GPU; fails loudly if the build is missing."""
     import pycitlali

@@ -123,3 +123,13 @@ def test_synth_is_deterministic_and_shaped():
     assert np.all((d >= 1e-3 * 0.999) & (d <= 1e-2 * 1.001))
     z = synth.Rng(1).normal(200000)
     assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
+
+
+def test_kernel_timing_needs_both_events():
+    import ctypes
+    import pycitlali
+    lib = pycitlali.load()
+    st = lib.citlali_hip_set_kernel_timing(ctypes.c_void_p(0x1000), ctypes.c_void_p(0))
+    assert st == pycitlali._lib.ERR_INVALID
+    assert "both events" in pycitlali.last_error()
+    assert lib.citlali_hip_set_kernel_timing(ctypes.c_void_p(0), ctypes.c_void_p(0)) == 0

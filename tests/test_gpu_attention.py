@@ -137,3 +137,24 @@ def test_batched_rejects_small_workspace(hip):
     pos = hip.DeviceArray.from_numpy(np.full(nseq, max_ctx - 1, np.int32))
     with pytest.raises(hip.CitlaliError, match="workspace"):
         hip.device.attention_batched(d, d, d, 0, pos, max_ctx, nseq, heads, kv, hd, d, need - 16, d)
+
+
+def test_batched_position_past_bound_is_cut_at_bound(hip):
+    """A device position >= max_positions_bound attends over positions
+    0..bound-1 (the caches end there), exactly like position = bound - 1."""
+    nseq, heads, kv, hd, bound = 3, 32, 8, 128, 1000
+    rng = hip.synth.Rng(77)
+    stride = bound * kv * hd
+    k = hip.synth.normal_f16(rng, nseq * stride)
+    v = hip.synth.normal_f16(rng, nseq * stride)
+    q = hip.synth.normal_f16(rng, nseq * heads * hd)
+    ws_bytes = hip.device.attention_workspace_bytes(bound, nseq, heads, kv, hd)
+    dws = hip.DeviceArray(max(ws_bytes, 16))
+    dq, dk, dv = (hip.DeviceArray.from_numpy(a) for a in (q, k, v))
+    outs = []
+    for last in (bound - 1, bound + 500):
+        dpos = hip.DeviceArray.from_numpy(np.array([10, last, 999], np.int32))
+        do = hip.DeviceArray(nseq * heads * hd * 2)
+        hip.device.attention_batched(dq, dk, dv, stride, dpos, bound, nseq, heads, kv, hd, dws, ws_bytes, do)
+        outs.append(do.download(np.uint16))
+    assert np.array_equal(outs[0], outs[1])

@@ -1,0 +1,182 @@
+"""GPU parity of the forward_token helpers (kernels.cu:27-124, 474-533 and
+the host argmax of qwen_model.cpp:455-463) through the C ABI, against the
+oracle.  Bit-exact where the arithmetic is one fp32 operation and a
+nearest-even store (add, copy, embed, store_kv, argmax); within the
+north-star bar, and mostly within one fp16 step, elsewhere."""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import tol_ok
+
+pytestmark = pytest.mark.gpu
+H = np.float16
+
+
+def vals(b):
+    return np.asarray(b, np.uint16).view(H).astype(np.float64)
+
+
+def up(hip, a):
+    return hip.DeviceArray.from_numpy(np.ascontiguousarray(a))
+
+
+def ulps(got_bits, ref_bits):
+    """Distance in fp16 steps (same-sign values)."""
+    g = np.asarray(got_bits, np.int64)
+    r = np.asarray(ref_bits, np.int64)
+    g = np.where(g & 0x8000, -(g & 0x7fff), g)
+    r = np.where(r & 0x8000, -(r & 0x7fff), r)
+    return np.abs(g - r)
+
+
+@pytest.mark.parametrize("n", [1024, 4096, 5120])
+def test_rms_norm(hip, orc, n):
+    rng = hip.synth.Rng(100 + n)
+    x, w = hip.synth.normal_f16(rng, n), hip.synth.normal_f16(rng, n)
+    dx, dw, do = up(hip, x), up(hip, w), hip.DeviceArray(n * 2)
+    hip.device.rms_norm(dx, dw, do, n, 1e-6)
+    got = do.download(np.uint16, n)
+    ref = orc.rms_norm(x, w, 1e-6)
+    assert np.all(tol_ok(vals(got), vals(ref)))
+    assert ulps(got, ref).max() <= 1
+
+
+@pytest.mark.parametrize("heads,hd", [(32, 128), (8, 128), (16, 64)])
+def test_rms_norm_heads(hip, orc, heads, hd):
+    rng = hip.synth.Rng(7 * heads + hd)
+    x, w = hip.synth.normal_f16(rng, heads * hd), hip.synth.normal_f16(rng, hd)
+    dx, dw, do = up(hip, x), up(hip, w), hip.DeviceArray(heads * hd * 2)
+    hip.device.rms_norm_heads(dx, dw, do, heads, hd, 1e-6)
+    got = do.download(np.uint16, heads * hd)
+    ref = orc.rms_norm_heads(x, w, heads, hd, 1e-6)
+    assert ulps(got, ref).max() <= 1
+
+
+@pytest.mark.parametrize("position", [0, 1, 37, 1000, 8191])
+@pytest.mark.parametrize("heads,hd", [(32, 128), (8, 128), (16, 64)])
+def test_rope(hip, orc, heads, hd, position):
+    theta = 1e6
+    rng = hip.synth.Rng(position * 31 + heads)
+    x = hip.synth.normal_f16(rng, heads * hd)
+    d = up(hip, x)
+    hip.device.rope(d, heads, hd, position, theta)
+    got = vals(d.download(np.uint16, heads * hd))
+    ref = vals(orc.rope(x, heads, hd, position, theta))
+    if position == 0:
+        assert np.array_equal(got, vals(x))
+        return
+    # The fp32 inverse frequency theta^(-2i/hd) is within ~2 ulp of exact in
+    # any powf, so the angle is known to ~angle * 2^-22; the pair norm bounds
+    # what that moves.
+    half = hd // 2
+    xs = vals(x).reshape(heads, 2, half)
+    norm = np.hypot(xs[:, 0], xs[:, 1])
+    ang = position * theta ** (-2 * np.arange(half) / hd)
+    slack = (norm * ang * 2.0 ** -22)[:, None, :].repeat(2, 1).reshape(-1)
+    assert np.all(np.abs(got - ref) <= 2e-3 + 1e-2 * np.abs(ref) + slack)
+
+
+def test_swiglu(hip, orc):
+    n = 12288
+    rng = hip.synth.Rng(9)
+    g, u = hip.synth.normal_f16(rng, n), hip.synth.normal_f16(rng, n)
+    g[:4] = np.array([0.0, 20.0, -20.0, 11.0], H).view(np.uint16)
+    dg, du, do = up(hip, g), up(hip, u), hip.DeviceArray(n * 2)
+    hip.device.swiglu(dg, du, do, n)
+    got = do.download(np.uint16, n)
+    ref = orc.swiglu(g, u)
+    assert np.all(tol_ok(vals(got), vals(ref)))
+    assert ulps(got, ref).max() <= 1
+
+
+@pytest.mark.parametrize("fn", ["add_inplace", "add_bias_inplace"])
+def test_add_is_bit_exact(hip, orc, fn):
+    n = 4096 + 5
+    rng = hip.synth.Rng(11)
+    t, dlt = hip.synth.normal_f16(rng, n), hip.synth.normal_f16(rng, n)
+    dt, dd = up(hip, t), up(hip, dlt)
+    getattr(hip.device, fn)(dt, dd, n)
+    assert np.array_equal(dt.download(np.uint16, n), orc.add(t, dlt))
+
+
+def test_store_kv_copy_and_embed_are_exact(hip, orc):
+    rng = hip.synth.Rng(12)
+    kv, ctx, pos = 1024, 32, 17
+    kc, vc = hip.synth.normal_f16(rng, ctx * kv), hip.synth.normal_f16(rng, ctx * kv)
+    k, v = hip.synth.normal_f16(rng, kv), hip.synth.normal_f16(rng, kv)
+    dkc, dvc = up(hip, kc), up(hip, vc)
+    hip.device.store_kv(up(hip, k), up(hip, v), dkc, dvc, pos, kv)
+    rk, rv = orc.store_kv(k, v, kc, vc, pos)
+    assert np.array_equal(dkc.download(np.uint16, ctx * kv), rk)
+    assert np.array_equal(dvc.download(np.uint16, ctx * kv), rv)
+    # fp16 embedding row and plain copy
+    hidden, vocab = 1024, 40
+    table = hip.synth.normal_f16(rng, vocab * hidden)
+    out = hip.DeviceArray(hidden * 2)
+    hip.device.embed(up(hip, table), 33, out, hidden)
+    assert np.array_equal(out.download(np.uint16, hidden), table[33 * hidden:34 * hidden])
+    src = up(hip, table)
+    dst = hip.DeviceArray(table.nbytes)
+    hip.device.copy(src, dst, table.size)
+    assert np.array_equal(dst.download(np.uint16, table.size), table)
+
+
+def _argmax(hip, logits):
+    d = up(hip, logits.astype(np.float32))
+    o = hip.DeviceArray(4)
+    hip.device.argmax(d, logits.size, o)
+    return int(o.download(np.int32, 1)[0])
+
+
+def test_argmax_matches_host_rule(hip, orc):
+    r = np.random.default_rng(5)
+    for n in (1, 7, 1000, 151936):
+        x = r.standard_normal(n).astype(np.float32)
+        if n > 10:
+            top = np.float32(x.max() + 1)
+            idx = np.sort(r.choice(n, 3, replace=False))
+            x[idx] = top                                     # ties: the first wins
+            x[r.choice(n, 5)] = np.nan
+            x[r.choice(n, 2)] = np.inf
+        assert _argmax(hip, x) == orc.argmax(x), n
+    assert _argmax(hip, np.array([np.nan, np.inf, -np.inf], np.float32)) == 0
+    assert _argmax(hip, np.full(5000, np.float32(-3e38))) == 0
+
+
+@pytest.mark.parametrize("f32", [False, True])
+@pytest.mark.parametrize("k,n", [(1024, 3072), (4096, 1024), (1000, 64)])
+def test_matvec_fp16(hip, orc, k, n, f32):
+    rng = hip.synth.Rng(k + n)
+    w = hip.synth.normal_f16(rng, n * k)
+    x = hip.synth.normal_f16(rng, k)
+    ref = vals(w).reshape(n, k) @ vals(x) / 1.0
+    dw, dx = up(hip, w), up(hip, x)
+    dy = hip.DeviceArray(n * (4 if f32 else 2))
+    hip.device.matvec("fp16", dw, dx, dy, k, n, f32_out=f32)
+    got = dy.download(np.float32, n).astype(np.float64) if f32 else vals(dy.download(np.uint16, n))
+    bound = 1e-3 * math.sqrt(k / 4096) * np.sqrt((vals(w).reshape(n, k) ** 2) @ (vals(x) ** 2)) + 1e-5
+    if not f32:
+        bound = bound + 2.0 ** -11 * np.abs(ref)
+    assert np.all(tol_ok(got, ref))
+    assert np.all(np.abs(got - ref) <= bound)
+
+
+def test_kernel_timer_brackets_the_calls_kernels(hip):
+    """KernelTimer spans the first kernel's start to the last kernel's end of
+    the calls made while armed, and disarms afterwards."""
+    n, k = 12288, 4096
+    w = hip.synth.quant_matrix("q4k", hip.synth.Rng(1), n, k)
+    dw, dx, dy = up(hip, w), up(hip, hip.synth.normal_f16(hip.synth.Rng(2), k)), hip.DeviceArray(n * 2)
+    hip.device.matvec("q4k", dw, dx, dy, k, n)
+    one, two = hip.device.KernelTimer(), hip.device.KernelTimer()
+    with one:
+        hip.device.matvec("q4k", dw, dx, dy, k, n)
+    with two:
+        hip.device.matvec("q4k", dw, dx, dy, k, n)
+        hip.device.matvec("q4k", dw, dx, dy, k, n)
+    hip.device.matvec("q4k", dw, dx, dy, k, n)   # not timed
+    hip.synchronize()
+    t1, t2 = one.ms(), two.ms()
+    assert 0 < t1 < 5 and t2 > 1.5 * t1, (t1, t2)

@@ -1,0 +1,31 @@
+"""The C++ host API (libcitlali.so: citlali::Error, dtype, DeviceBuffer,
+compute::launch_*, WeightHandle, LinearBackend) through its C++ test program
+tests/cpp/test_host_layer (built by __graft_entry__.build())."""
+import os
+import subprocess
+
+import pytest
+
+BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "test_host_layer")
+
+
+def _run(mode, timeout):
+    assert os.path.exists(BIN), "tests/cpp/test_host_layer is not built: run __graft_entry__.build()"
+    p = subprocess.run([BIN, mode], capture_output=True, text=True, timeout=timeout)
+    print(p.stdout)
+    assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
+    assert f"{mode}: " in p.stdout and "checks passed" in p.stdout
+
+
+def test_host_layer_cpu():
+    """dtype tables, float_to_half_bits over all 2^32 floats and
+    half_bits_to_float / bfloat16_to_half_bits over all 2^16 patterns against
+    the oracle, LinearBackend dispatch errors -- no GPU."""
+    _run("cpu", 600)
+
+
+@pytest.mark.gpu
+def test_host_layer_gpu():
+    """LinearBackend::forward for Q4_K, Q6_K and fp16 weights, launch_attention
+    and launch_embed_q6k through the C++ API, against the oracle."""
+    _run("gpu", 300)
