@@ -18,7 +18,9 @@
 //    fp16 pairs and v_dot2_f32_f16 accumulates in fp32.  The running max and
 //    sum of the online softmax are butterflies over the lanes of one head.
 //    Exponentials are taken in base 2 with log2(e) folded into the scale.
-//  * Values: lane = (head, 8-dim slice); p * V accumulates in fp32.
+//  * Values: lane = (position group, 8-dim slice) accumulating every head of
+//    the group, so each staged V row is read from LDS once per lane group;
+//    p * V accumulates in fp32 and the groups are summed in the final merge.
 //  * The four waves merge in LDS; a chunk writes (max, sum, acc[head_dim])
 //    per head and a second kernel merges the chunks of each query head by
 //    log-sum-exp.  A sequence that fits one chunk is written directly.
@@ -46,22 +48,24 @@ struct Cfg {
     static constexpr int kStride = HD + 8;                 // padded LDS row (halves)
     static constexpr int kRowsPerLoad = kWave / kChunks;
     static constexpr int kLoads = kTP / kRowsPerLoad;      // per tile, for K and for V
-    static constexpr int kSlots = kWave / kChunks;         // head slots in the V phase
-    static constexpr int kHPL = GP > kSlots ? GP / kSlots : 1;
-    static constexpr int kPPar = GP < kSlots ? kSlots / GP : 1;
+    // value phase: lane = (position group, 8-dim slice), every head of the group
+    static constexpr int kVGroups = kWave / kChunks;
+    static constexpr int kVPerLane = kTP / kVGroups;       // positions per lane per tile
     static constexpr int kTileHalves = kTP * kStride;
-    // wave-private region: K tile, V tile, p[GP][kTP], alpha[GP]; 16-byte multiple
+    // wave-private region: K tile, V tile, p[kTP][GP], alpha[GP]; 16-byte multiple
     static constexpr size_t kWaveLds =
         (((size_t)kTileHalves * 2 * 2 + (size_t)GP * kTP * 4 + (size_t)GP * 4) + 15) & ~(size_t)15;
-    static_assert(kLoads >= 1, "tile");
+    // workgroup merge: (max, sum)[kWaves][GP], then acc[kWaves * kVGroups][GP][HD]
+    static constexpr size_t kMlFloats = ((size_t)kWaves * GP * 2 + 3) & ~(size_t)3;
+    static constexpr size_t kMergeLds = (kMlFloats + (size_t)kWaves * kVGroups * GP * HD) * sizeof(float);
+    static_assert(kLoads >= 1 && kVPerLane >= 1 && kTP % kVGroups == 0, "tile");
 };
 
 template <int HD, int GP>
 size_t split_lds_bytes() {
     using C = Cfg<HD, GP>;
     const size_t tiles = C::kWaveLds * kWaves;
-    const size_t merge = (size_t)kWaves * GP * (HD + 2) * sizeof(float);
-    return tiles > merge ? tiles : merge;
+    return tiles > C::kMergeLds ? tiles : C::kMergeLds;
 }
 
 // merge kernel: weights [kMaxSplits], lsum (padded to 16 B), red[kBlock] float4
@@ -82,7 +86,7 @@ __device__ __forceinline__ SeqSpan seq_span(const int32_t* positions, int positi
 
 // Grid: (chunk, kv_head, seq).  `positions` (device, per sequence) or the
 // scalar `position` gives the last cached position of each sequence.
-template <int HD, int GP>
+template <int HD, int GP, int kDepth>
 __global__ __launch_bounds__(kBlock) void attn_split_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     long long seq_stride, const int32_t* __restrict__ positions, int position, int max_len, int heads,
@@ -107,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
     uint8_t* wl = smem + (size_t)wave * C::kWaveLds;
     uint16_t* kt = reinterpret_cast<uint16_t*>(wl);
     uint16_t* vt = kt + C::kTileHalves;
-    float* pt = reinterpret_cast<float*>(vt + C::kTileHalves);   // [GP][kTP]
+    float* pt = reinterpret_cast<float*>(vt + C::kTileHalves);   // [kTP][GP]
     float* at = pt + GP * C::kTP;                                 // [GP]
 
     const uint16_t* kbase = k_cache + (size_t)seq * seq_stride + (size_t)kvh * HD;
@@ -118,56 +122,48 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
     const int sh = lane % GP, sp = lane / GP;
     const bool s_head_ok = sh < group;
     const bool s_lane_ok = sp < C::kTP;
+    // q of the lane's head in VGPRs.  Unconditional loads (a padding head
+    // reads the group's last head and is zeroed) keep every global load
+    // outside branches, so the compiler's load counting stays exact and the
+    // waits below never cover the tiles still in flight.
     uint32_t qv[HD / 2];
     {
-        const uint16_t* qh = q + ((size_t)seq * heads + (size_t)kvh * group + sh) * HD;
+        const int hq = kvh * group + (s_head_ok ? sh : group - 1);
+        const uint16_t* qh = q + ((size_t)seq * heads + hq) * HD;
+        const uint32_t keep = s_head_ok ? 0xffffffffu : 0u;
 #pragma unroll
         for (int c = 0; c < C::kChunks; ++c) {
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (s_head_ok) v = *reinterpret_cast<const u32x4*>(qh + c * 8);
-            qv[4 * c + 0] = v.x; qv[4 * c + 1] = v.y; qv[4 * c + 2] = v.z; qv[4 * c + 3] = v.w;
+            const u32x4 v = *reinterpret_cast<const u32x4*>(qh + c * 8);
+            qv[4 * c + 0] = v.x & keep; qv[4 * c + 1] = v.y & keep;
+            qv[4 * c + 2] = v.z & keep; qv[4 * c + 3] = v.w & keep;
         }
     }
-    // value-phase identity
-    const int vc = lane % C::kChunks, slot = lane / C::kChunks;
-    int vh[C::kHPL];
+    // value-phase identity: lane = (position group vg, 8-dim slice vc)
+    const int vc = lane % C::kChunks, vg = lane / C::kChunks;
+    float acc[GP][8];
 #pragma unroll
-    for (int i = 0; i < C::kHPL; ++i) vh[i] = (C::kHPL == 1) ? (slot % GP) : (slot + C::kSlots * i);
-    const int vpp = (C::kHPL == 1) ? (slot / GP) : 0;
-    float acc[C::kHPL][8];
+    for (int h = 0; h < GP; ++h)
 #pragma unroll
-    for (int i = 0; i < C::kHPL; ++i)
-#pragma unroll
-        for (int k = 0; k < 8; ++k) acc[i][k] = 0.f;
+        for (int k = 0; k < 8; ++k) acc[h][k] = 0.f;
 
     float m_run = -INFINITY, l_run = 0.f;   // per scores lane (head sh)
 
-    // load identity
+    // load identity; kDepth tiles of K and V rows in flight per wave
     const int lrow = lane / C::kChunks, lc = lane % C::kChunks;
-    u32x4 kr[C::kLoads], vr[C::kLoads];
-    auto load_tile = [&](int t0) {
+    u32x4 kr[kDepth][C::kLoads], vr[kDepth][C::kLoads];
+    auto load_tile = [&](u32x4 (&kd)[C::kLoads], u32x4 (&vd)[C::kLoads], int t0) {
 #pragma unroll
         for (int i = 0; i < C::kLoads; ++i) {
             // branch-free: rows past the range re-read the last one (never used)
             const int pos = min(t0 + i * C::kRowsPerLoad + lrow, w1 - 1);
-            kr[i] = *reinterpret_cast<const u32x4*>(kbase + (size_t)pos * row_step + lc * 8);
-            vr[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pos * row_step + lc * 8);
+            kd[i] = *reinterpret_cast<const u32x4*>(kbase + (size_t)pos * row_step + lc * 8);
+            vd[i] = *reinterpret_cast<const u32x4*>(vbase + (size_t)pos * row_step + lc * 8);
         }
     };
 
-    if (w0 < w1) load_tile(w0);
-    for (int t0 = w0; t0 < w1; t0 += C::kTP) {
+    // One staged tile; with nv <= 0 it changes nothing (scores -inf, weights 0).
+    auto process_tile = [&](int t0) {
         const int nv = min(C::kTP, w1 - t0);
-#pragma unroll
-        for (int i = 0; i < C::kLoads; ++i) {
-            const int r = i * C::kRowsPerLoad + lrow;
-            if (r < nv) {
-                *reinterpret_cast<u32x4*>(kt + r * C::kStride + lc * 8) = kr[i];
-                *reinterpret_cast<u32x4*>(vt + r * C::kStride + lc * 8) = vr[i];
-            }
-        }
-        wave_lds_sync();
-        if (t0 + C::kTP < w1) load_tile(t0 + C::kTP);
 
         // ---- scores + online softmax (lane = position sp, head sh) ----
         float s2 = -INFINITY;
@@ -187,64 +183,86 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
         const float mt = column_max<GP>(s2);
         const float m_new = fmaxf(m_run, mt);
         const bool live = m_new != -INFINITY;
-        const float alpha = live ? exp2f(m_run - m_new) : 1.f;
-        float pw = live ? exp2f(s2 - m_new) : 0.f;
+        const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+        const float pw = live ? __builtin_amdgcn_exp2f(s2 - m_new) : 0.f;
         const float ps = column_sum<GP>(pw);
         l_run = l_run * alpha + ps;
         m_run = m_new;
-        if (s_lane_ok) pt[sh * C::kTP + sp] = pw;
+        if (s_lane_ok) pt[lane] = pw;   // lane = sp * GP + sh
         if (sp == 0) at[sh] = alpha;
         wave_lds_sync();
 
-        // ---- values (lane = head slot, 8-dim slice vc) ----
+        // ---- values: every head for kVPerLane positions of this lane ----
+        float al[GP];
+        load_floats<GP>(at, al);
 #pragma unroll
-        for (int i = 0; i < C::kHPL; ++i) {
-            const float al = at[vh[i]];
+        for (int h = 0; h < GP; ++h)
 #pragma unroll
-            for (int k = 0; k < 8; ++k) acc[i][k] *= al;
-        }
-        for (int p = vpp; p < nv; p += C::kPPar) {
+            for (int k = 0; k < 8; ++k) acc[h][k] *= al[h];
+        // rows past nv hold finite copies of a valid row and weight 0
+#pragma unroll
+        for (int j = 0; j < C::kVPerLane; ++j) {
+            const int p = vg + j * C::kVGroups;
             const u32x4 vv = *reinterpret_cast<const u32x4*>(vt + p * C::kStride + vc * 8);
+            float pp[GP];
+            load_floats<GP>(pt + p * GP, pp);
             const float v8[8] = {h2f(vv.x & 0xffffu), h2f(vv.x >> 16), h2f(vv.y & 0xffffu), h2f(vv.y >> 16),
                                  h2f(vv.z & 0xffffu), h2f(vv.z >> 16), h2f(vv.w & 0xffffu), h2f(vv.w >> 16)};
 #pragma unroll
-            for (int i = 0; i < C::kHPL; ++i) {
-                const float pp = pt[vh[i] * C::kTP + p];
+            for (int h = 0; h < GP; ++h)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[i][k] = fmaf(pp, v8[k], acc[i][k]);
-            }
+                for (int k = 0; k < 8; ++k) acc[h][k] = fmaf(pp[h], v8[k], acc[h][k]);
         }
         wave_lds_sync();
-    }
+    };
 
-    // combine the position-parallel partial sums of the value phase
-    if constexpr (C::kPPar > 1) {
-        // lanes (pp, head, slice) with pp stride GP * kChunks in {8, 16, 32}
+    // kDepth tiles in flight: tile t is consumed while tiles t+1 .. t+kDepth-1
+    // load, and its slot is refilled with tile t+kDepth right away.  Loads
+    // are unconditional (past the range they re-read row w1 - 1, in bounds
+    // even for an empty range since w1 = b1 >= 1 there) and a tile past the
+    // range is a no-op, so no load sits in a branch.
+    // The issue order is pinned (sched_barrier): the slots must be issued in
+    // the same order as the loop refills them, or the wait before a slot's
+    // first use covers the later slots too.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            float a = acc[0][k];
-            if constexpr (GP * C::kChunks <= 8) a += dpp<DppRor<8>::value>(a);
-            if constexpr (GP * C::kChunks <= 16) a += xor16(a);
-            a += xor32(a);
-            acc[0][k] = a;
+    for (int d = 0; d < kDepth; ++d) {
+        load_tile(kr[d], vr[d], w0 + d * C::kTP);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int t0 = w0; t0 < w1; t0 += kDepth * C::kTP) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            const int tt = t0 + d * C::kTP;
+            // every row is stored: rows past the range hold a copy of row
+            // w1 - 1 (finite) and get weight 0
+#pragma unroll
+            for (int i = 0; i < C::kLoads; ++i) {
+                const int r = i * C::kRowsPerLoad + lrow;
+                *reinterpret_cast<u32x4*>(kt + r * C::kStride + lc * 8) = kr[d][i];
+                *reinterpret_cast<u32x4*>(vt + r * C::kStride + lc * 8) = vr[d][i];
+            }
+            wave_lds_sync();
+            __builtin_amdgcn_sched_barrier(0);
+            load_tile(kr[d], vr[d], tt + kDepth * C::kTP);
+            __builtin_amdgcn_sched_barrier(0);
+            process_tile(tt);
         }
     }
 
-    // ---- merge the four waves of the workgroup ----
+    // ---- merge the position groups and the four waves in LDS ----
     __syncthreads();   // every wave is done with its tiles
-    float* ms = reinterpret_cast<float*>(smem);               // [kWaves][GP][HD + 2]
+    float* ml = reinterpret_cast<float*>(smem);   // [kWaves][GP] (max, sum)
+    float* ms = ml + C::kMlFloats;                // [kWaves * kVGroups][GP][HD]
     if (sp == 0) {
-        float* e = ms + ((size_t)wave * GP + sh) * (HD + 2);
-        e[HD] = m_run;
-        e[HD + 1] = l_run;
+        ml[(wave * GP + sh) * 2] = m_run;
+        ml[(wave * GP + sh) * 2 + 1] = l_run;
     }
-    if (vpp == 0) {
 #pragma unroll
-        for (int i = 0; i < C::kHPL; ++i) {
-            float* e = ms + ((size_t)wave * GP + vh[i]) * (HD + 2) + vc * 8;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) e[k] = acc[i][k];
-        }
+    for (int h = 0; h < GP; ++h) {
+        f32x4* e = reinterpret_cast<f32x4*>(ms + ((size_t)(wave * C::kVGroups + vg) * GP + h) * HD + vc * 8);
+        e[0] = f32x4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
+        e[1] = f32x4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
     }
     __syncthreads();
 
@@ -252,14 +270,17 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
         const int h = idx / HD, d = idx - h * HD;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ms[((size_t)w * GP + h) * (HD + 2) + HD]);
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[(w * GP + h) * 2]);
         float Ls = 0.f, A = 0.f;
 #pragma unroll
         for (int w = 0; w < kWaves; ++w) {
-            const float* e = ms + ((size_t)w * GP + h) * (HD + 2);
-            const float f = e[HD] == -INFINITY ? 0.f : exp2f(e[HD] - M);
-            Ls += e[HD + 1] * f;
-            A += e[d] * f;
+            const float mw = ml[(w * GP + h) * 2];
+            const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+            Ls += ml[(w * GP + h) * 2 + 1] * f;
+            float a = 0.f;
+#pragma unroll
+            for (int g = 0; g < C::kVGroups; ++g) a += ms[((size_t)(w * C::kVGroups + g) * GP + h) * HD + d];
+            A += a * f;
         }
         const int hq = kvh * group + h;
         if (n_valid == 1) {
@@ -329,11 +350,11 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restr
     }
 }
 
-template <int HD, int GP>
+template <int HD, int GP, int kDepth>
 hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
     const size_t lds = split_lds_bytes<HD, GP>();
     const float scale_log2 = (float)(1.4426950408889634 / sqrt((double)HD));
-    launch_kernel_in_call(p.n_splits <= 1, (attn_split_kernel<HD, GP>), dim3(p.n_splits, a.kv_heads, a.nseq),
+    launch_kernel_in_call(p.n_splits <= 1, (attn_split_kernel<HD, GP, kDepth>), dim3(p.n_splits, a.kv_heads, a.nseq),
                           dim3(kBlock), lds, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
                           a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
                           a.workspace, p.n_splits, a.out);
@@ -344,13 +365,22 @@ hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream
     return hipGetLastError();
 }
 
+template <int HD, int GP>
+hipError_t launch_depth(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
+    switch (p.depth) {
+        case 1: return launch_split<HD, GP, 1>(a, p, s);
+        case 2: return launch_split<HD, GP, 2>(a, p, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 template <int HD>
 hipError_t launch_hd(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
     switch (p.gp) {
-        case 1: return launch_split<HD, 1>(a, p, s);
-        case 2: return launch_split<HD, 2>(a, p, s);
-        case 4: return launch_split<HD, 4>(a, p, s);
-        case 8: return launch_split<HD, 8>(a, p, s);
+        case 1: return launch_depth<HD, 1>(a, p, s);
+        case 2: return launch_depth<HD, 2>(a, p, s);
+        case 4: return launch_depth<HD, 4>(a, p, s);
+        case 8: return launch_depth<HD, 8>(a, p, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -380,6 +410,9 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     chunk = ((chunk + quantum - 1) / quantum) * quantum;
     p.chunk = (int)chunk;
     p.n_splits = (int)((max_len + chunk - 1) / chunk);
+    // one tile in flight per wave: deeper rings measured no faster on
+    // gfx950 (the per-tile work, not the load latency, bounds a wave)
+    p.depth = 1;
     (void)head_dim;
     return p;
 }

@@ -151,4 +151,27 @@ __device__ __forceinline__ uint32_t align_bytes(uint32_t lo, uint32_t hi, uint32
     return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
 }
 
+// N consecutive floats from LDS (16-byte aligned for N >= 4, 8-byte for 2)
+// with the widest reads.
+template <int N>
+__device__ __forceinline__ void load_floats(const float* p, float (&out)[N]) {
+    if constexpr (N == 1) {
+        out[0] = p[0];
+    } else if constexpr (N == 2) {
+        const f32x2 v = *reinterpret_cast<const f32x2*>(p);
+        out[0] = v.x;
+        out[1] = v.y;
+    } else {
+        static_assert(N % 4 == 0, "load_floats");
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const f32x4 v = reinterpret_cast<const f32x4*>(p)[i];
+            out[4 * i + 0] = v.x;
+            out[4 * i + 1] = v.y;
+            out[4 * i + 2] = v.z;
+            out[4 * i + 3] = v.w;
+        }
+    }
+}
+
 }  // namespace citlali::hip

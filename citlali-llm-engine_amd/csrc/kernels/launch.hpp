@@ -65,6 +65,7 @@ struct AttnPlan {
     int gp;        // padded GQA group (1, 2, 4, 8)
     int chunk;     // positions per workgroup
     int n_splits;  // chunks of the longest sequence
+    int depth;     // K/V tiles in flight per wave (1 or 2)
 };
 bool attention_supported(int head_dim, int group);
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks);
