@@ -39,6 +39,10 @@ void launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* k_cache, ui
 // workspace when large enough; it does not receive the raw scores.
 void launch_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* scores,
                       uint16_t* output, int position, int max_context, int heads, int kv_heads, int head_dim);
+// Greedy pick on the device (no reference counterpart: the reference copies
+// the logits to the host, qwen_model.cpp:448-465): the first largest finite
+// value of logits[0..n) is written to *out_index (0 when none is finite).
+void launch_argmax(const float* logits, int n, int32_t* out_index);
 // Waits for every launch queued on the library stream.
 void synchronize();
 

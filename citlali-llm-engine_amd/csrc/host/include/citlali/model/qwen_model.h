@@ -1,0 +1,80 @@
+// citlali/model/qwen_model.h -- single-token decode of a Qwen-family model.
+//
+// forward_token follows the reference's QwenModel::forward_token
+// (src/model/qwen_model.cpp:239-419) operation by operation, with its fp16
+// store points and output-weight rule, over the gfx950 compute:: launchers.
+// The weights arrive as WeightHandles (QwenWeights) instead of being read
+// from a GGUF file by the reference's load(); remote layer ranges are not
+// part of this build.  Greedy sampling picks the first largest finite logit
+// (qwen_model.cpp:448-465) on the device and copies back one index.
+#pragma once
+
+#include "citlali/compute/hip/tensor.h"
+#include "citlali/model/linear_backend.h"
+#include "citlali/model/qwen_config.h"
+#include "citlali/model/weight_handle.h"
+
+#include <cstdint>
+#include <memory>
+#include <vector>
+
+namespace citlali::model {
+
+// Same fields as the reference (include/citlali/model/qwen_model.h:16-33).
+struct QwenLayerWeights {
+    WeightHandle attn_norm;
+    WeightHandle attn_q, attn_q_bias;
+    WeightHandle attn_k, attn_k_bias;
+    WeightHandle attn_v, attn_v_bias;
+    WeightHandle attn_o, attn_o_bias;
+    WeightHandle attn_q_norm, attn_k_norm;
+    WeightHandle ffn_norm;
+    WeightHandle ffn_gate, ffn_gate_bias;
+    WeightHandle ffn_up, ffn_up_bias;
+    WeightHandle ffn_down, ffn_down_bias;
+    compute::DeviceBufferPtr k_cache;   // allocated by load()
+    compute::DeviceBufferPtr v_cache;
+};
+
+// What the reference's load() reads from GGUF.  An output_weight without a
+// buffer falls back to token_embedding (qwen_model.cpp:73-75).
+struct QwenWeights {
+    WeightHandle token_embedding;
+    WeightHandle output_norm;
+    WeightHandle output_weight;
+    std::vector<QwenLayerWeights> layers;
+};
+
+class QwenModel {
+public:
+    QwenModel() = default;
+
+    // max_context 0 -> min(context_length, 2048), as the reference.
+    void load(const QwenConfig& config, QwenWeights weights, uint32_t max_context = 0);
+    // Runs one token at `position`; returns the greedy next token, or -1
+    // when compute_logits is false.
+    int32_t forward_token(int32_t token_id, uint32_t position, bool compute_logits = true);
+    void synchronize() const;
+
+    const QwenConfig& config() const { return config_; }
+    uint32_t max_context() const { return max_context_; }
+    // fp32 logits [vocab] of the last forward_token that computed them.
+    const compute::DeviceBufferPtr& logits() const { return logits_; }
+
+private:
+    void allocate_runtime_buffers();
+    int32_t sample_greedy_from_logits();
+
+    QwenConfig config_;
+    uint32_t max_context_ = 0;
+    WeightHandle token_embedding_;
+    WeightHandle output_norm_;
+    WeightHandle output_weight_;
+    std::vector<QwenLayerWeights> layers_;
+
+    compute::DeviceBufferPtr x_, norm_, q_, k_, v_, attn_out_, attn_proj_;
+    compute::DeviceBufferPtr gate_, up_, ff_act_, ff_out_, logits_, scores_, next_token_;
+    std::unique_ptr<LinearBackend> linear_backend_;
+};
+
+}  // namespace citlali::model

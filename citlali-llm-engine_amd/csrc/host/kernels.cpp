@@ -82,6 +82,10 @@ void launch_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t
                                             kv_heads, head_dim));
 }
 
+void launch_argmax(const float* logits, int n, int32_t* out_index) {
+    CITLALI_HIP_CHECK(citlali_hip_argmax(logits, n, out_index));
+}
+
 void synchronize() { CITLALI_HIP_CHECK(citlali_hip_synchronize()); }
 
 }  // namespace citlali::compute

@@ -1,0 +1,192 @@
+// qwen_model.cpp -- QwenModel::forward_token over the gfx950 launchers
+// (reference: src/model/qwen_model.cpp:15-33, 39-213, 239-465).
+#include "citlali/model/qwen_model.h"
+
+#include "citlali/common.h"
+#include "citlali/compute/hip/kernels.h"
+
+#include <algorithm>
+#include <limits>
+#include <string>
+
+namespace citlali::model {
+namespace {
+
+int as_int(uint64_t value, const std::string& label) {
+    require(value <= static_cast<uint64_t>(std::numeric_limits<int>::max()),
+            label + " is too large for this minimal kernel path");
+    return static_cast<int>(value);
+}
+
+void require_shape(const WeightHandle& weight, uint64_t cols, uint64_t rows) {
+    require(weight.cols() == cols && weight.rows() == rows,
+            "unexpected tensor shape for " + weight.name + ": got [" + std::to_string(weight.cols()) + ", " +
+                std::to_string(weight.rows()) + "], expected [" + std::to_string(cols) + ", " +
+                std::to_string(rows) + "]");
+}
+
+void add_bias_if_present(const WeightHandle& bias, const compute::DeviceBufferPtr& target, uint64_t elements) {
+    if (!bias.buffer) return;
+    require_shape(bias, elements, 1);
+    compute::launch_add_bias_inplace(target->half_data(), bias.device_half_data(),
+                                     as_int(elements, bias.name + " elements"));
+}
+
+}  // namespace
+
+void QwenModel::load(const QwenConfig& config, QwenWeights weights, uint32_t max_context) {
+    config_ = config;
+    max_context_ = max_context == 0 ? std::min<uint32_t>(config_.context_length, 2048)
+                                    : std::min(max_context, config_.context_length);
+    require(max_context_ > 0, "max_context must be positive");
+    require(config_.head_count_kv > 0 && config_.head_count % config_.head_count_kv == 0,
+            "attention head_count must be divisible by head_count_kv");
+    linear_backend_.reset();   // set again only once everything below succeeded
+
+    token_embedding_ = std::move(weights.token_embedding);
+    output_norm_ = std::move(weights.output_norm);
+    output_weight_ = std::move(weights.output_weight);
+    if (!output_weight_.buffer) output_weight_ = token_embedding_;
+    layers_ = std::move(weights.layers);
+
+    const uint64_t hidden = config_.embedding_length;
+    const uint64_t q_size = static_cast<uint64_t>(config_.head_count) * config_.head_dim;
+    const uint64_t kv_size = static_cast<uint64_t>(config_.head_count_kv) * config_.head_dim;
+    const uint64_t ff = config_.feed_forward_length;
+    require(layers_.size() == config_.block_count, "expected " + std::to_string(config_.block_count) +
+                                                       " layers, got " + std::to_string(layers_.size()));
+    require_shape(token_embedding_, hidden, config_.vocab_size);
+    require_shape(output_norm_, hidden, 1);
+    require_shape(output_weight_, hidden, config_.vocab_size);
+    for (QwenLayerWeights& layer : layers_) {
+        require_shape(layer.attn_norm, hidden, 1);
+        require_shape(layer.attn_q, hidden, q_size);
+        if (layer.attn_q_bias.buffer) require_shape(layer.attn_q_bias, q_size, 1);
+        require_shape(layer.attn_k, hidden, kv_size);
+        if (layer.attn_k_bias.buffer) require_shape(layer.attn_k_bias, kv_size, 1);
+        require_shape(layer.attn_v, hidden, kv_size);
+        if (layer.attn_v_bias.buffer) require_shape(layer.attn_v_bias, kv_size, 1);
+        require_shape(layer.attn_o, q_size, hidden);
+        if (layer.attn_o_bias.buffer) require_shape(layer.attn_o_bias, hidden, 1);
+        if (layer.attn_q_norm.buffer) require_shape(layer.attn_q_norm, config_.head_dim, 1);
+        if (layer.attn_k_norm.buffer) require_shape(layer.attn_k_norm, config_.head_dim, 1);
+        require_shape(layer.ffn_norm, hidden, 1);
+        require_shape(layer.ffn_gate, hidden, ff);
+        if (layer.ffn_gate_bias.buffer) require_shape(layer.ffn_gate_bias, ff, 1);
+        require_shape(layer.ffn_up, hidden, ff);
+        if (layer.ffn_up_bias.buffer) require_shape(layer.ffn_up_bias, ff, 1);
+        require_shape(layer.ffn_down, ff, hidden);
+        if (layer.ffn_down_bias.buffer) require_shape(layer.ffn_down_bias, hidden, 1);
+        layer.k_cache = compute::make_device_half_buffer(static_cast<size_t>(max_context_) * kv_size);
+        layer.v_cache = compute::make_device_half_buffer(static_cast<size_t>(max_context_) * kv_size);
+    }
+    allocate_runtime_buffers();
+    linear_backend_ = make_fp16_linear_backend();
+}
+
+void QwenModel::allocate_runtime_buffers() {
+    const size_t hidden = config_.embedding_length;
+    const size_t q = static_cast<size_t>(config_.head_count) * config_.head_dim;
+    const size_t kv = static_cast<size_t>(config_.head_count_kv) * config_.head_dim;
+    const size_t ff = config_.feed_forward_length;
+    x_ = compute::make_device_half_buffer(hidden);
+    norm_ = compute::make_device_half_buffer(hidden);
+    q_ = compute::make_device_half_buffer(q);
+    k_ = compute::make_device_half_buffer(kv);
+    v_ = compute::make_device_half_buffer(kv);
+    attn_out_ = compute::make_device_half_buffer(q);
+    attn_proj_ = compute::make_device_half_buffer(hidden);
+    gate_ = compute::make_device_half_buffer(ff);
+    up_ = compute::make_device_half_buffer(ff);
+    ff_act_ = compute::make_device_half_buffer(ff);
+    ff_out_ = compute::make_device_half_buffer(hidden);
+    logits_ = compute::make_device_buffer(static_cast<size_t>(config_.vocab_size) * sizeof(float));
+    scores_ = compute::make_device_buffer(static_cast<size_t>(config_.head_count) * max_context_ * sizeof(float));
+    next_token_ = compute::make_device_buffer(sizeof(int32_t));
+}
+
+int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compute_logits) {
+    require(linear_backend_ != nullptr, "model is not loaded");
+    require(position < max_context_, "position exceeds max_context");
+    require(token_id >= 0 && token_id < static_cast<int32_t>(config_.vocab_size), "token id out of vocab range");
+
+    const int hidden = as_int(config_.embedding_length, "hidden size");
+    const int head_dim = as_int(config_.head_dim, "head_dim");
+    const int heads = as_int(config_.head_count, "head_count");
+    const int kv_heads = as_int(config_.head_count_kv, "head_count_kv");
+    const int kv_size = kv_heads * head_dim;
+    const int ff = as_int(config_.feed_forward_length, "feed_forward_length");
+    const int pos = static_cast<int>(position);
+
+    if (token_embedding_.storage_kind == compute::WeightStorageKind::QuantizedDevice) {
+        if (token_embedding_.gguf_type != compute::GgufTensorType::Q6_K)
+            throw Error("unsupported quantized embedding type");
+        compute::launch_embed_q6k(token_embedding_.device_quantized_data(), token_id, x_->half_data(), hidden);
+    } else {
+        compute::launch_embed(token_embedding_.device_half_data(), token_id, x_->half_data(), hidden);
+    }
+
+    for (QwenLayerWeights& layer : layers_) {
+        compute::launch_rms_norm(x_->half_data(), layer.attn_norm.device_half_data(), norm_->half_data(), hidden,
+                                 config_.rms_norm_eps);
+        linear_backend_->forward(layer.attn_q, norm_, q_);
+        add_bias_if_present(layer.attn_q_bias, q_, static_cast<uint64_t>(heads) * head_dim);
+        linear_backend_->forward(layer.attn_k, norm_, k_);
+        add_bias_if_present(layer.attn_k_bias, k_, static_cast<uint64_t>(kv_heads) * head_dim);
+        linear_backend_->forward(layer.attn_v, norm_, v_);
+        add_bias_if_present(layer.attn_v_bias, v_, static_cast<uint64_t>(kv_heads) * head_dim);
+        if (layer.attn_q_norm.buffer)
+            compute::launch_rms_norm_heads(q_->half_data(), layer.attn_q_norm.device_half_data(), q_->half_data(),
+                                           heads, head_dim, config_.rms_norm_eps);
+        if (layer.attn_k_norm.buffer)
+            compute::launch_rms_norm_heads(k_->half_data(), layer.attn_k_norm.device_half_data(), k_->half_data(),
+                                           kv_heads, head_dim, config_.rms_norm_eps);
+        compute::launch_rope(q_->half_data(), heads, head_dim, pos, config_.rope_theta);
+        compute::launch_rope(k_->half_data(), kv_heads, head_dim, pos, config_.rope_theta);
+        compute::launch_store_kv(k_->half_data(), v_->half_data(), layer.k_cache->half_data(),
+                                 layer.v_cache->half_data(), pos, kv_size);
+        compute::launch_attention(q_->half_data(), layer.k_cache->half_data(), layer.v_cache->half_data(),
+                                  static_cast<float*>(scores_->data()), attn_out_->half_data(), pos,
+                                  static_cast<int>(max_context_), heads, kv_heads, head_dim);
+        linear_backend_->forward(layer.attn_o, attn_out_, attn_proj_);
+        add_bias_if_present(layer.attn_o_bias, attn_proj_, hidden);
+        compute::launch_add_inplace(x_->half_data(), attn_proj_->half_data(), hidden);
+        compute::launch_rms_norm(x_->half_data(), layer.ffn_norm.device_half_data(), norm_->half_data(), hidden,
+                                 config_.rms_norm_eps);
+        linear_backend_->forward(layer.ffn_gate, norm_, gate_);
+        add_bias_if_present(layer.ffn_gate_bias, gate_, ff);
+        linear_backend_->forward(layer.ffn_up, norm_, up_);
+        add_bias_if_present(layer.ffn_up_bias, up_, ff);
+        compute::launch_swiglu(gate_->half_data(), up_->half_data(), ff_act_->half_data(), ff);
+        linear_backend_->forward(layer.ffn_down, ff_act_, ff_out_);
+        add_bias_if_present(layer.ffn_down_bias, ff_out_, hidden);
+        compute::launch_add_inplace(x_->half_data(), ff_out_->half_data(), hidden);
+    }
+    if (!compute_logits) return -1;
+
+    compute::launch_rms_norm(x_->half_data(), output_norm_.device_half_data(), norm_->half_data(), hidden,
+                             config_.rms_norm_eps);
+    const int vocab = as_int(config_.vocab_size, "vocab_size");
+    if (output_weight_.storage_kind == compute::WeightStorageKind::QuantizedDevice) {
+        if (output_weight_.gguf_type != compute::GgufTensorType::Q6_K)
+            throw Error("unsupported quantized output weight type: " + compute::to_string(output_weight_.gguf_type));
+        compute::launch_matvec_q6k_to_float(output_weight_.device_quantized_data(), norm_->half_data(),
+                                            static_cast<float*>(logits_->data()), hidden, vocab);
+    } else {
+        compute::launch_matvec_fp16_to_float(output_weight_.device_half_data(), norm_->half_data(),
+                                             static_cast<float*>(logits_->data()), hidden, vocab);
+    }
+    return sample_greedy_from_logits();
+}
+
+void QwenModel::synchronize() const { compute::synchronize(); }
+
+int32_t QwenModel::sample_greedy_from_logits() {
+    compute::launch_argmax(static_cast<const float*>(logits_->data()), static_cast<int>(config_.vocab_size),
+                           static_cast<int32_t*>(next_token_->data()));
+    int32_t next = 0;
+    next_token_->copy_to_host(&next, sizeof(next));   // waits for the stream
+    return next;
+}
+
+}  // namespace citlali::model

@@ -1,13 +1,14 @@
 // dequant.hip -- Q6_K embedding gather and whole-tensor Q4_K / Q6_K -> fp16.
 //
 // Values are the exact fp32 dequantised weights of kernels.cu:134-186
-// (== weight_loader.cpp:147-323 before rounding), rounded to fp16 with the
-// reference's host rule (nearest, ties away from zero; dtype.cpp:136-176), so
-// the output equals the host routines dequant_q4_k / dequant_q6_k bit for bit.
-// The embedding therefore matches what the reference's fp16 path stores for
-// the same table row.  (The reference's own CUDA embed_q6k rounds
-// nearest-even, kernels.cu:377, and so differs from its host dequant on exact
-// ties; this build keeps the host rule on both paths.)
+// (== weight_loader.cpp:147-323 before rounding).  The two entry points round
+// them the way their reference counterparts do, and the reference is not
+// consistent on exact ties:
+//  * embed_q6k follows the reference kernel (kernels.cu:340-378), whose
+//    store_half is __float2half: nearest-even.
+//  * the whole-tensor dequant follows the host loader (dequant_q4_k /
+//    dequant_q6_k with float_to_half_bits, dtype.cpp:136-176): nearest, ties
+//    away from zero, so its output equals the host routines bit for bit.
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -73,7 +74,7 @@ __global__ void embed_q6k_kernel(const uint8_t* __restrict__ table, int32_t toke
     if (idx >= hidden) return;
     const size_t nb = (size_t)hidden / kQK;
     const uint8_t* row = table + (size_t)token_id * nb * kQ6KBytes;
-    out[idx] = f2h_ties_away(q6k_value(row + (size_t)(idx / kQK) * kQ6KBytes, idx % kQK));
+    out[idx] = f2h_rne(q6k_value(row + (size_t)(idx / kQK) * kQ6KBytes, idx % kQK));
 }
 
 template <int kKind>

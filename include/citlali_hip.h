@@ -89,9 +89,9 @@ int citlali_hip_matvec_q6k(const uint8_t* w, const uint16_t* x, uint16_t* y, int
 int citlali_hip_matvec_q6k_to_float(const uint8_t* w, const uint16_t* x, float* y, int in_features,
                                     int out_features);
 
-/* launch_embed_q6k (kernels.h:32, kernels.cu:670-683): row token_id of a
- * Q6_K table -> fp16, rounded with the host rule of dequant_q6_k (ties
- * away from zero), i.e. bit-identical to the reference's fp16 path. */
+/* launch_embed_q6k (kernels.h:32, kernels.cu:340-378, 670-683): row
+ * token_id of a Q6_K table -> fp16, the exact fp32 value rounded
+ * nearest-even as the reference kernel's __float2half store does. */
 int citlali_hip_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden);
 
 /* ---- hot path: decode attention ------------------------------------------ *

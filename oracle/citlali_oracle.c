@@ -340,13 +340,15 @@ void orc_matvec_f16(const uint16_t* w, const uint16_t* x, float* y, int in_f, in
  * embedding
  * ------------------------------------------------------------------------ */
 
-/* kernels.cu:340-378 gathers row token_id of a Q6_K table and dequantises it.
- * This oracle rounds with the host rule of dequant_q6_k
- * (weight_loader.cpp:240-323), which is what the fp16 path of the reference
- * stores for the same row; the HIP kernel is held to that rule bit for bit. */
+/* kernels.cu:340-378 gathers row token_id of a Q6_K table, dequantises each
+ * value in fp32 (dequant_q6k_value) and stores it with __float2half, i.e.
+ * rounded nearest-even (kernels.cu:21-24). */
 void orc_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden) {
     const int nb = hidden / ORC_QK;
-    orc_dequant_q6k_f16(table + (size_t)token_id * nb * ORC_Q6K_BYTES, (uint64_t)hidden, out);
+    float* v = (float*)malloc((size_t)hidden * sizeof(float));
+    orc_dequant_q6k_f32(table + (size_t)token_id * nb * ORC_Q6K_BYTES, (uint64_t)hidden, v);
+    orc_f2h_rne_array(v, (size_t)hidden, out);
+    free(v);
 }
 
 /* ------------------------------------------------------------------------ *
@@ -490,4 +492,94 @@ int32_t orc_argmax(const float* logits, int n) {
         if (isfinite(v) && v > best) { best = v; id = i; }
     }
     return id;
+}
+
+/* ------------------------------------------------------------------------ *
+ * one decode step (qwen_model.cpp:239-419)
+ * ------------------------------------------------------------------------ */
+
+/* y = W x in double for any supported weight type (fp16 weights: the
+ * DequantizeToFp16 path's matvec_fp16, kernels.cu:381-471). */
+static void matvec_any(const OrcMatrix* w, const uint16_t* x, double* y, int in_f, int out_f) {
+    if (w->type == ORC_Q4K) {
+        orc_matvec_q4k((const uint8_t*)w->data, x, y, in_f, out_f, 0);
+    } else if (w->type == ORC_Q6K) {
+        orc_matvec_q6k((const uint8_t*)w->data, x, y, in_f, out_f, 0);
+    } else {
+        const uint16_t* wf = (const uint16_t*)w->data;
+#pragma omp parallel for schedule(static)
+        for (int r = 0; r < out_f; ++r) {
+            double acc = 0.0;
+            for (int k = 0; k < in_f; ++k)
+                acc += (double)orc_h2f(wf[(size_t)r * in_f + k]) * (double)orc_h2f(x[k]);
+            y[r] = acc;
+        }
+    }
+}
+
+/* linear_backend.cpp:19-61 then add_bias_if_present (qwen_model.cpp:28-33):
+ * fp16 output, then an fp32 bias add stored as fp16. */
+static void linear(const OrcMatrix* w, const uint16_t* bias, const uint16_t* x, int in_f, int out_f, uint16_t* y,
+                   double* tmp) {
+    matvec_any(w, x, tmp, in_f, out_f);
+    for (int i = 0; i < out_f; ++i) y[i] = d2h_rne(tmp[i]);
+    if (bias) orc_add_inplace(y, bias, out_f);
+}
+
+int32_t orc_forward_token(const OrcModel* m, uint16_t* const* caches, int32_t token, int position, float* logits) {
+    const int H = m->hidden, hd = m->head_dim, nq = m->heads * hd, nkv = m->kv_heads * hd, ff = m->ff;
+    const size_t big = (size_t)(m->vocab > ff ? m->vocab : ff) + (size_t)nq + H;
+    uint16_t* x = (uint16_t*)malloc((size_t)H * 2);
+    uint16_t* norm = (uint16_t*)malloc((size_t)H * 2);
+    uint16_t* q = (uint16_t*)malloc((size_t)nq * 2);
+    uint16_t* k = (uint16_t*)malloc((size_t)nkv * 2);
+    uint16_t* v = (uint16_t*)malloc((size_t)nkv * 2);
+    uint16_t* att = (uint16_t*)malloc((size_t)nq * 2);
+    uint16_t* proj = (uint16_t*)malloc((size_t)H * 2);
+    uint16_t* gate = (uint16_t*)malloc((size_t)ff * 2);
+    uint16_t* up = (uint16_t*)malloc((size_t)ff * 2);
+    uint16_t* act = (uint16_t*)malloc((size_t)ff * 2);
+    double* tmp = (double*)malloc(big * sizeof(double));
+
+    /* token embedding (qwen_model.cpp:256-268) */
+    if (m->token_embd.type == ORC_Q6K)
+        orc_embed_q6k((const uint8_t*)m->token_embd.data, token, x, H);
+    else
+        memcpy(x, (const uint16_t*)m->token_embd.data + (size_t)token * H, (size_t)H * 2);
+
+    for (int l = 0; l < m->n_layers; ++l) {
+        const OrcLayer* L = &m->layers[l];
+        uint16_t* kc = caches[2 * l];
+        uint16_t* vc = caches[2 * l + 1];
+        orc_rms_norm(x, L->attn_norm, norm, H, m->eps);
+        linear(&L->q, L->q_bias, norm, H, nq, q, tmp);
+        linear(&L->k, L->k_bias, norm, H, nkv, k, tmp);
+        linear(&L->v, L->v_bias, norm, H, nkv, v, tmp);
+        if (L->q_norm) orc_rms_norm_heads(q, L->q_norm, q, m->heads, hd, m->eps);
+        if (L->k_norm) orc_rms_norm_heads(k, L->k_norm, k, m->kv_heads, hd, m->eps);
+        orc_rope(q, m->heads, hd, position, m->theta);
+        orc_rope(k, m->kv_heads, hd, position, m->theta);
+        orc_store_kv(k, v, kc, vc, position, nkv);
+        orc_attention(q, kc, vc, position, m->heads, m->kv_heads, hd, tmp);
+        for (int i = 0; i < nq; ++i) att[i] = d2h_rne(tmp[i]);
+        linear(&L->o, L->o_bias, att, nq, H, proj, tmp);
+        orc_add_inplace(x, proj, H);
+        orc_rms_norm(x, L->ffn_norm, norm, H, m->eps);
+        linear(&L->gate, L->gate_bias, norm, H, ff, gate, tmp);
+        linear(&L->up, L->up_bias, norm, H, ff, up, tmp);
+        orc_swiglu(gate, up, act, ff);
+        linear(&L->down, L->down_bias, act, ff, H, proj, tmp);
+        orc_add_inplace(x, proj, H);
+    }
+
+    /* final norm, fp32 logits, greedy pick (qwen_model.cpp:385-419, 448-465) */
+    orc_rms_norm(x, m->output_norm, norm, H, m->eps);
+    matvec_any(&m->output, norm, tmp, H, m->vocab);
+    float* lg = logits ? logits : (float*)malloc((size_t)m->vocab * sizeof(float));
+    for (int i = 0; i < m->vocab; ++i) lg[i] = (float)tmp[i];
+    const int32_t next = orc_argmax(lg, m->vocab);
+    if (!logits) free(lg);
+    free(x); free(norm); free(q); free(k); free(v); free(att); free(proj);
+    free(gate); free(up); free(act); free(tmp);
+    return next;
 }

@@ -69,7 +69,7 @@ void orc_matvec_q4k_f16dot(const uint8_t* w, const uint16_t* x, float* y, int in
 void orc_matvec_q6k_f16dot(const uint8_t* w, const uint16_t* x, float* y, int in_features, int out_features, int nthreads);
 void orc_matvec_f16(const uint16_t* w, const uint16_t* x, float* y, int in_features, int out_features, int nthreads);
 
-/* ---- embedding (kernels.cu:340-378; host rule weight_loader.cpp:240-323) -- */
+/* ---- embedding (kernels.cu:340-378): the fp32 value, rounded nearest-even - */
 void orc_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden);
 
 /* ---- decode attention (kernels.cu:545-649) ------------------------------- *
@@ -91,6 +91,40 @@ void orc_add_inplace(uint16_t* target, const uint16_t* delta, int n);
 void orc_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc, int position, int kv_size);
 /* greedy argmax with the host tie rule (qwen_model.cpp:455-463) */
 int32_t orc_argmax(const float* logits, int n);
+
+/* ---- one decode step of the model (qwen_model.cpp:239-419) -------------- *
+ * Composes the routines above in the reference's order with its fp16 store
+ * points: every GEMV / norm / rope / attention / swiglu / add result is
+ * stored as fp16 (nearest-even) before the next operation reads it; the
+ * logits stay fp32.  No remote layers.                                     */
+#define ORC_F16 1
+#define ORC_Q4K 12
+#define ORC_Q6K 14
+typedef struct {
+    int type;            /* ORC_F16, ORC_Q4K or ORC_Q6K */
+    const void* data;    /* [rows = out][in] */
+} OrcMatrix;
+typedef struct {
+    const uint16_t* attn_norm;
+    OrcMatrix q, k, v, o;
+    const uint16_t *q_bias, *k_bias, *v_bias, *o_bias;   /* NULL when absent */
+    const uint16_t *q_norm, *k_norm;                      /* NULL when absent */
+    const uint16_t* ffn_norm;
+    OrcMatrix gate, up, down;
+    const uint16_t *gate_bias, *up_bias, *down_bias;      /* NULL when absent */
+} OrcLayer;
+typedef struct {
+    int hidden, heads, kv_heads, head_dim, ff, n_layers, vocab, max_ctx;
+    float eps, theta;
+    OrcMatrix token_embd;   /* ORC_Q6K or ORC_F16, [vocab][hidden] */
+    const uint16_t* output_norm;
+    OrcMatrix output;       /* ORC_Q6K or ORC_F16, [vocab][hidden] */
+    const OrcLayer* layers;
+} OrcModel;
+/* caches: 2 * n_layers caller-owned fp16 arrays [max_ctx][kv_heads*head_dim]
+ * (k0, v0, k1, v1, ...).  logits (vocab floats) may be NULL.  Returns the
+ * greedy token of the fp32 logits (orc_argmax rule). */
+int32_t orc_forward_token(const OrcModel* m, uint16_t* const* caches, int32_t token, int position, float* logits);
 
 /* ---- misc ---------------------------------------------------------------- */
 int orc_num_threads(void);

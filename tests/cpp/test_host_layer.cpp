@@ -12,6 +12,7 @@
 #include "citlali/compute/hip/kernels.h"
 #include "citlali/compute/hip/tensor.h"
 #include "citlali/model/linear_backend.h"
+#include "citlali/model/qwen_model.h"
 #include "citlali_hip.h"
 #include "citlali_oracle.h"
 
@@ -73,15 +74,15 @@ std::vector<uint16_t> normal_f16(Rng& r, size_t n) {
     return v;
 }
 
-// Random quant bytes; d (and dmin) = fp16 of U[1e-3, 1e-2].
-std::vector<uint8_t> quant_blocks(Rng& r, GgufTensorType t, size_t blocks) {
+// Random quant bytes; d (and dmin) = fp16 of U[d_lo, d_hi].
+std::vector<uint8_t> quant_blocks(Rng& r, GgufTensorType t, size_t blocks, double d_lo = 1e-3, double d_hi = 1e-2) {
     const size_t bb = compute::gguf_type_block_bytes(t);
     std::vector<uint8_t> b(blocks * bb);
     for (auto& x : b) x = (uint8_t)r.next();
     for (size_t i = 0; i < blocks; ++i) {
         uint8_t* p = b.data() + i * bb;
         auto put = [&](size_t off) {
-            const uint16_t h = orc_f2h_rne((float)(1e-3 + 9e-3 * r.uniform()));
+            const uint16_t h = orc_f2h_rne((float)(d_lo + (d_hi - d_lo) * r.uniform()));
             std::memcpy(p + off, &h, 2);
         };
         if (t == GgufTensorType::Q4_K) {
@@ -311,6 +312,308 @@ void test_embed() {
     std::printf("embed_q6k ok\n");
 }
 
+// ------------------------------------------------------------ the model
+// A synthetic Qwen3-style model: host bytes for the oracle, WeightHandles for
+// QwenModel.  d is chosen so every matrix has rms ~ gain / sqrt(in), which
+// keeps the fp16 activations in range (random Q4_K codes give rms(w) ~ 300 d,
+// random Q6_K codes ~ 1366 d).
+struct HostMatrix {
+    GgufTensorType type;
+    int rows, cols;
+    std::vector<uint8_t> bytes;
+};
+
+struct SynthModel {
+    model::QwenConfig cfg;
+    HostMatrix embd, output;
+    std::vector<uint16_t> output_norm;
+    struct Layer {
+        std::vector<uint16_t> attn_norm, q_norm, k_norm, ffn_norm;
+        HostMatrix q, k, v, o, gate, up, down;
+    };
+    std::vector<Layer> layers;
+};
+
+HostMatrix make_matrix(Rng& r, GgufTensorType t, int rows, int cols, double gain) {
+    const double per = t == GgufTensorType::Q4_K ? 300.0 : 1366.0;
+    const double d = gain / std::sqrt((double)cols) / per;
+    HostMatrix m{t, rows, cols, quant_blocks(r, t, (size_t)rows * cols / 256, 0.8 * d, 1.2 * d)};
+    return m;
+}
+
+std::vector<uint16_t> make_norm(Rng& r, int n) {
+    std::vector<uint16_t> v(n);
+    for (auto& h : v) h = orc_f2h_rne((float)(1.0 + 0.1 * r.normal()));
+    return v;
+}
+
+SynthModel make_model(uint64_t seed, int hidden, int heads, int kv_heads, int ff, int layers, int vocab) {
+    Rng r{seed};
+    SynthModel m;
+    m.cfg.vocab_size = vocab;
+    m.cfg.context_length = 4096;
+    m.cfg.embedding_length = hidden;
+    m.cfg.block_count = layers;
+    m.cfg.feed_forward_length = ff;
+    m.cfg.head_count = heads;
+    m.cfg.head_count_kv = kv_heads;
+    m.cfg.head_dim = 128;
+    m.embd = make_matrix(r, GgufTensorType::Q6_K, vocab, hidden, std::sqrt((double)hidden));   // rows of rms ~1
+    m.output = make_matrix(r, GgufTensorType::Q6_K, vocab, hidden, 3.0);
+    m.output_norm = make_norm(r, hidden);
+    const int nq = heads * 128, nkv = kv_heads * 128;
+    for (int l = 0; l < layers; ++l) {
+        SynthModel::Layer L;
+        L.attn_norm = make_norm(r, hidden);
+        L.q_norm = make_norm(r, 128);
+        L.k_norm = make_norm(r, 128);
+        L.ffn_norm = make_norm(r, hidden);
+        L.q = make_matrix(r, GgufTensorType::Q4_K, nq, hidden, 1.0);
+        L.k = make_matrix(r, GgufTensorType::Q4_K, nkv, hidden, 1.0);
+        L.v = make_matrix(r, GgufTensorType::Q6_K, nkv, hidden, 1.0);
+        L.o = make_matrix(r, GgufTensorType::Q4_K, hidden, nq, 0.5);
+        L.gate = make_matrix(r, GgufTensorType::Q4_K, ff, hidden, 1.0);
+        L.up = make_matrix(r, GgufTensorType::Q4_K, ff, hidden, 1.0);
+        L.down = make_matrix(r, GgufTensorType::Q6_K, hidden, ff, 0.5);
+        m.layers.push_back(std::move(L));
+    }
+    return m;
+}
+
+OrcMatrix orc_of(const HostMatrix& m) { return {m.type == GgufTensorType::Q4_K ? ORC_Q4K : ORC_Q6K, m.bytes.data()}; }
+
+// The oracle's model view; `drop` zeroes nothing, it only selects layers.
+struct OracleModel {
+    std::vector<OrcLayer> layers;
+    OrcModel m{};
+    std::vector<std::vector<uint16_t>> caches;
+    std::vector<uint16_t*> cache_ptrs;
+    OracleModel(const SynthModel& s, int max_ctx, int n_layers) {
+        for (int l = 0; l < n_layers; ++l) {
+            const auto& L = s.layers[l];
+            OrcLayer o{};
+            o.attn_norm = L.attn_norm.data();
+            o.q = orc_of(L.q); o.k = orc_of(L.k); o.v = orc_of(L.v); o.o = orc_of(L.o);
+            o.q_norm = L.q_norm.data(); o.k_norm = L.k_norm.data();
+            o.ffn_norm = L.ffn_norm.data();
+            o.gate = orc_of(L.gate); o.up = orc_of(L.up); o.down = orc_of(L.down);
+            layers.push_back(o);
+        }
+        m.hidden = (int)s.cfg.embedding_length; m.heads = (int)s.cfg.head_count; m.kv_heads = (int)s.cfg.head_count_kv;
+        m.head_dim = 128; m.ff = (int)s.cfg.feed_forward_length; m.n_layers = n_layers;
+        m.vocab = (int)s.cfg.vocab_size; m.max_ctx = max_ctx; m.eps = s.cfg.rms_norm_eps; m.theta = s.cfg.rope_theta;
+        m.token_embd = orc_of(s.embd); m.output_norm = s.output_norm.data(); m.output = orc_of(s.output);
+        m.layers = layers.data();
+        for (int i = 0; i < 2 * n_layers; ++i) caches.emplace_back((size_t)max_ctx * m.kv_heads * 128, 0);
+        for (auto& c : caches) cache_ptrs.push_back(c.data());
+    }
+    int32_t step(int32_t tok, int pos, float* logits) { return orc_forward_token(&m, cache_ptrs.data(), tok, pos, logits); }
+};
+
+model::WeightHandle handle_of(const HostMatrix& m, const std::string& name) {
+    model::WeightHandle w;
+    w.name = name;
+    w.gguf_type = m.type;
+    w.storage_kind = WeightStorageKind::QuantizedDevice;
+    w.dims = {(uint64_t)m.cols, (uint64_t)m.rows};
+    w.element_count = (uint64_t)m.rows * m.cols;
+    w.buffer = upload(m.bytes);
+    return w;
+}
+
+model::WeightHandle handle_of_norm(const std::vector<uint16_t>& v, const std::string& name) {
+    model::WeightHandle w;
+    w.name = name;
+    w.gguf_type = GgufTensorType::F16;
+    w.storage_kind = WeightStorageKind::Fp16Device;
+    w.dims = {(uint64_t)v.size(), 1};
+    w.element_count = v.size();
+    w.buffer = upload(v);
+    return w;
+}
+
+model::QwenWeights device_weights(const SynthModel& s) {
+    model::QwenWeights w;
+    w.token_embedding = handle_of(s.embd, "token_embd.weight");
+    w.output_norm = handle_of_norm(s.output_norm, "output_norm.weight");
+    w.output_weight = handle_of(s.output, "output.weight");
+    for (size_t l = 0; l < s.layers.size(); ++l) {
+        const auto& L = s.layers[l];
+        const std::string b = "blk." + std::to_string(l) + ".";
+        model::QwenLayerWeights d;
+        d.attn_norm = handle_of_norm(L.attn_norm, b + "attn_norm.weight");
+        d.attn_q = handle_of(L.q, b + "attn_q.weight");
+        d.attn_k = handle_of(L.k, b + "attn_k.weight");
+        d.attn_v = handle_of(L.v, b + "attn_v.weight");
+        d.attn_o = handle_of(L.o, b + "attn_output.weight");
+        d.attn_q_norm = handle_of_norm(L.q_norm, b + "attn_q_norm.weight");
+        d.attn_k_norm = handle_of_norm(L.k_norm, b + "attn_k_norm.weight");
+        d.ffn_norm = handle_of_norm(L.ffn_norm, b + "ffn_norm.weight");
+        d.ffn_gate = handle_of(L.gate, b + "ffn_gate.weight");
+        d.ffn_up = handle_of(L.up, b + "ffn_up.weight");
+        d.ffn_down = handle_of(L.down, b + "ffn_down.weight");
+        w.layers.push_back(std::move(d));
+    }
+    return w;
+}
+
+// CPU: pins of the oracle's forward composition.
+void test_oracle_forward_pins() {
+    SynthModel s = make_model(21, 1024, 8, 4, 2048, 2, 512);
+    const int ctx = 8;
+    // (1) attn_o and ffn_down zero: every layer adds nothing, so the logits
+    // are output(rms_norm(embed(token))) -- residual stream and final norm wiring
+    SynthModel z = s;
+    for (auto& L : z.layers) {
+        std::fill(L.o.bytes.begin(), L.o.bytes.end(), 0);
+        std::fill(L.down.bytes.begin(), L.down.bytes.end(), 0);
+    }
+    OracleModel oz(z, ctx, 2);
+    std::vector<float> lg(512);
+    oz.step(5, 0, lg.data());
+    oz.step(77, 1, lg.data());
+    std::vector<uint16_t> e(1024), n(1024);
+    orc_embed_q6k(z.embd.bytes.data(), 77, e.data(), 1024);
+    orc_rms_norm(e.data(), z.output_norm.data(), n.data(), 1024, z.cfg.rms_norm_eps);
+    std::vector<double> ref(512);
+    orc_matvec_q6k(z.output.bytes.data(), n.data(), ref.data(), 1024, 512, 0);
+    for (int i = 0; i < 512; ++i) check(lg[i] == (float)ref[i], "zero residual branches: logit " + std::to_string(i));
+    // (2) a second layer whose attn_o and ffn_down are zero changes nothing:
+    // the two-layer model equals the one-layer model, step by step
+    SynthModel t = s;
+    std::fill(t.layers[1].o.bytes.begin(), t.layers[1].o.bytes.end(), 0);
+    std::fill(t.layers[1].down.bytes.begin(), t.layers[1].down.bytes.end(), 0);
+    OracleModel two(t, ctx, 2), one(s, ctx, 1);
+    std::vector<float> a(512), b(512);
+    for (int p = 0; p < 4; ++p) {
+        two.step(3 + 11 * p, p, a.data());
+        one.step(3 + 11 * p, p, b.data());
+        check(a == b, "inert second layer, position " + std::to_string(p));
+    }
+    // (3) history matters: the same token at position 1 after different
+    // first tokens gives different logits (attention reads the cache)
+    OracleModel h1(s, ctx, 2), h2(s, ctx, 2);
+    h1.step(1, 0, a.data());
+    h2.step(2, 0, b.data());
+    h1.step(9, 1, a.data());
+    h2.step(9, 1, b.data());
+    check(a != b, "the cache feeds attention");
+    std::printf("oracle forward pins ok\n");
+}
+
+void test_model_load_errors() {
+    SynthModel s = make_model(22, 1024, 8, 4, 2048, 1, 512);
+    model::QwenModel m;
+    expect_error([&] { m.forward_token(0, 0); }, "model is not loaded", "forward before load");
+    // shapes are checked before anything is allocated on the device
+    model::QwenWeights w;
+    w.token_embedding.name = "token_embd.weight";
+    w.token_embedding.dims = {1024, 500};
+    w.layers.resize(1);
+    expect_error([&] { m.load(s.cfg, w); },
+                 "unexpected tensor shape for token_embd.weight: got [1024, 500], expected [1024, 512]",
+                 "embedding shape");
+    model::QwenConfig bad = s.cfg;
+    bad.head_count_kv = 3;
+    expect_error([&] { m.load(bad, model::QwenWeights{}); }, "head_count must be divisible by head_count_kv",
+                 "GQA divisibility");
+    std::printf("model load errors ok\n");
+}
+
+// GPU: greedy decode through QwenModel against the oracle's forward.  Both
+// are fed the oracle's token at every step (teacher forcing), so each step
+// compares the two models on identical inputs.  A step may pick differently
+// only where the oracle's logits of the two picks are a numerical tie (within
+// the measured logit agreement); random weights make such near-ties among
+// thousands of tokens rare but possible, and then any two correct
+// implementations with different summation orders may split.
+//
+// How far the logits may move: the model itself amplifies fp16 rounding
+// differences, so the bound is measured, not assumed.  A third model -- the
+// oracle with half of its embedding values moved by one fp16 ulp -- runs in
+// lockstep, and the GPU must stay within the spread that this 1-ulp input
+// noise produces in the oracle.
+void greedy_run(uint64_t seed, int prompt, int steps, int* identical, int* ties) {
+    SynthModel s = make_model(seed, 2048, 16, 8, 4096, 2, 8192);
+    const int ctx = 128;
+    model::QwenModel gpu;
+    gpu.load(s.cfg, device_weights(s), ctx);
+    OracleModel orc(s, ctx, 2), ctl(s, ctx, 2);
+    std::vector<uint16_t> e16((size_t)8192 * 2048);
+    for (int t = 0; t < 8192; ++t) orc_embed_q6k(s.embd.bytes.data(), t, e16.data() + (size_t)t * 2048, 2048);
+    Rng flip{seed + 100};
+    for (auto& h : e16)
+        if ((h & 0x7fff) && (flip.next() & 1)) h ^= 1;
+    ctl.m.token_embd = {ORC_F16, e16.data()};
+    Rng r{seed * 31 + 1};
+    std::vector<float> lo(8192), lg(8192), lc(8192);
+    int32_t to = 0;
+    double worst = 0, ctl_worst = 0, min_margin = 1e30, rms_sum = 0;
+    std::string profile;
+    *identical = 0;
+    *ties = 0;
+    for (int p = 0; p < prompt + steps; ++p) {
+        const int32_t tok = p < prompt ? (int32_t)(r.next() % 8192) : to;
+        const int32_t tg = gpu.forward_token(tok, (uint32_t)p);
+        to = orc.step(tok, p, lo.data());
+        ctl.step(tok, p, lc.data());
+        gpu.logits()->copy_to_host(lg.data(), lg.size() * 4);
+        double step_err = 0, ctl_err = 0;
+        double ss = 0;
+        for (int i = 0; i < 8192; ++i) {
+            const double d = std::fabs((double)lg[i] - lo[i]);
+            step_err = std::max(step_err, d);
+            ctl_err = std::max(ctl_err, std::fabs((double)lc[i] - lo[i]));
+            ss += (double)lo[i] * lo[i];
+        }
+        const double rms = std::sqrt(ss / 8192);
+        rms_sum += rms;
+        worst = std::max(worst, step_err / rms);
+        ctl_worst = std::max(ctl_worst, ctl_err / rms);
+        if (p == 0 || p == 1 || p == 4 || p == 16 || p == 40 || p == prompt + steps - 1) {
+            char b[64];
+            std::snprintf(b, sizeof b, " p%d:%.1e", p, step_err / rms);
+            profile += b;
+        }
+        // device argmax = host rule on the device's own logits
+        int32_t host_pick = 0;
+        float hb = -INFINITY;
+        for (int i = 0; i < 8192; ++i)
+            if (std::isfinite(lg[i]) && lg[i] > hb) { hb = lg[i]; host_pick = i; }
+        check(tg == host_pick, "device argmax = host rule at position " + std::to_string(p));
+        if (p < prompt) continue;
+        float best = -INFINITY, second = -INFINITY;
+        for (float v : lo) {
+            if (v > best) { second = best; best = v; } else if (v > second) second = v;
+        }
+        min_margin = std::min(min_margin, (double)(best - second));
+        if (tg == to) {
+            ++*identical;
+        } else {
+            ++*ties;
+            const double gap = (double)lo[to] - lo[tg];
+            check(gap <= 2.0 * step_err, "greedy step " + std::to_string(p - prompt) + ": gpu " + std::to_string(tg) +
+                                             " oracle " + std::to_string(to) + ", oracle gap " + std::to_string(gap) +
+                                             " exceeds twice the logit error " + std::to_string(step_err));
+        }
+    }
+    std::printf("greedy decode seed %llu: %d prompt tokens, %d greedy steps: %d identical, %d numerical ties; "
+                "max |logit diff| / rms(logits) = %.2e (rms %.2f; by position%s); oracle under 1-ulp embedding "
+                "noise: %.2e; min oracle top-2 margin %.2e\n",
+                (unsigned long long)seed, prompt, steps, *identical, *ties, worst, rms_sum / (prompt + steps),
+                profile.c_str(), ctl_worst, min_margin);
+    check(worst <= ctl_worst, "GPU logits within the oracle's own 1-ulp sensitivity");
+}
+
+void test_forward_greedy() {
+    int identical = 0, ties = 0, all_ties = 0;
+    for (uint64_t seed : {7ull, 8ull, 9ull}) {
+        greedy_run(seed, 8, 64, &identical, &ties);
+        all_ties += ties;
+    }
+    check(all_ties <= 3, "at most one numerical tie per 64-step run on average");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -320,6 +623,8 @@ int main(int argc, char** argv) {
             test_dtype();
             test_fp16_rules();
             test_dispatch_errors();
+            test_oracle_forward_pins();
+            test_model_load_errors();
         } else if (mode == "gpu") {
             if (citlali_hip_init(0) != CITLALI_OK) {
                 std::printf("FAIL: no GPU: %s\n", citlali_hip_last_error());
@@ -333,6 +638,7 @@ int main(int argc, char** argv) {
             test_linear_errors();
             test_attention();
             test_embed();
+            test_forward_greedy();
             compute::synchronize();
         } else {
             std::printf("usage: %s cpu|gpu\n", argv[0]);

@@ -104,3 +104,14 @@ def test_q6k_closed_forms(orc):
     for e in range(256):
         h, part, i = e // 128, (e % 128) // 32, e % 32
         assert v[e] == -32.0 * (8 * h + i // 16 + 2 * part - 8)
+
+
+def test_embed_is_nearest_even_of_f32_dequant(orc, synth):
+    """orc_embed_q6k = numpy's IEEE (nearest-even) cast of the fp32 dequant
+    row (pinned above) -- the reference kernel's __float2half store."""
+    hidden, vocab = 1024, 7
+    table = synth.q6k_blocks(synth.Rng(9), vocab * hidden // 256)
+    for tok in (0, 3, vocab - 1):
+        row = table[tok * (hidden // 256) * 210:(tok + 1) * (hidden // 256) * 210]
+        f32 = orc.dequant_f32("q6k", row, hidden)
+        np.testing.assert_array_equal(orc.embed_q6k(table, tok, hidden), f32.astype(np.float16).view(np.uint16))
