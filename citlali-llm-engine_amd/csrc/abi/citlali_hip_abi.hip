@@ -425,6 +425,40 @@ CITLALI_EXPORT int citlali_hip_stream_read(const void* buf, size_t bytes, void* 
 }
 
 // ---------------------------------------------------------------- events
+CITLALI_EXPORT int citlali_hip_add_rms_norm(uint16_t* x, const uint16_t* delta, const uint16_t* w, uint16_t* out,
+                                            int n, float eps) {
+    REQUIRE(x && delta && w && out && n > 0, "add_rms_norm: bad arguments");
+    HIP_TRY(launch_add_rms_norm(x, delta, w, out, n, eps, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                                  const uint16_t* q_norm, const uint16_t* k_norm, int heads,
+                                                  int kv_heads, int head_dim, int position, float theta, float eps,
+                                                  uint16_t* k_cache, uint16_t* v_cache) {
+    REQUIRE(q && k && v && k_cache && v_cache, "qk_norm_rope_store received a null buffer");
+    REQUIRE(heads > 0 && kv_heads > 0 && position >= 0, "qk_norm_rope_store: bad heads or position");
+    REQUIRE(head_dim > 0 && head_dim <= 128 && head_dim % 2 == 0, "qk_norm_rope_store: head_dim %d not supported",
+            head_dim);
+    HIP_TRY(launch_qk_norm_rope_store(q, k, v, q_norm, k_norm, heads, kv_heads, head_dim, position, theta, eps,
+                                      k_cache, v_cache, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up,
+                                                     const uint16_t* x, uint16_t* act, int in_f, int out_f) {
+    REQUIRE(gguf_type == 12 || gguf_type == 14, "matvec_gate_up_swiglu: GGUF type %d is not Q4_K or Q6_K",
+            gguf_type);
+    const uintptr_t walign = gguf_type == 12 ? 16 : 4;
+    int st = check_matvec("matvec_gate_up_swiglu", w_gate, x, act, in_f, out_f, walign, 2);
+    if (st) return st;
+    REQUIRE(w_up && aligned(w_up, walign), "matvec_gate_up_swiglu: bad up weight");
+    if (in_f != 4096 && in_f != 8192)
+        return fail(CITLALI_ERR_UNSUPPORTED, "matvec_gate_up_swiglu: in_features %d has no fused kernel", in_f);
+    HIP_TRY(launch_matvec_gate_up_swiglu(gguf_type == 14 ? 6 : 4, w_gate, w_up, x, act, in_f, out_f, g_stream));
+    return CITLALI_OK;
+}
+
 CITLALI_EXPORT int citlali_hip_set_kernel_timing(void* start, void* stop) {
     REQUIRE((start == nullptr) == (stop == nullptr), "set_kernel_timing: give both events or neither");
     KernelTiming& t = kernel_timing();

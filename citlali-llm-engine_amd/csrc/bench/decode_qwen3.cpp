@@ -1,0 +1,220 @@
+// decode_qwen3.cpp -- synthetic Qwen3 greedy decode through QwenModel.
+//
+// BASELINE config 5 by default: Qwen3-8B shapes (36 layers, hidden 4096,
+// FFN 12288, 32/8 heads, head_dim 128, vocab 151936, rope_theta 1e6,
+// rms_eps 1e-6), Q4_K for most matrices, Q6_K for attn_v, ffn_down, the
+// output and the token embedding; a prompt of 512 random token ids fed as
+// the reference's session does (session.cpp:71-74: one forward_token per
+// prompt token, logits only for the last), then 256 greedy steps
+// (session.cpp:92).  Weights are random quant blocks whose d keeps every
+// matrix at rms ~ gain/sqrt(in) (random Q4_K codes give rms ~ 300 d, Q6_K
+// ~ 1366 d); `--distinct N` fills N distinct layer byte sets and gives every
+// one of the 36 layers its own device copy, so each layer reads its own
+// weights from HBM.  Prints one JSON line.
+//
+// usage: decode_qwen3 [--layers 36] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1]
+#include "citlali/common.h"
+#include "citlali/compute/hip/kernels.h"
+#include "citlali/model/qwen_model.h"
+#include "citlali_hip.h"
+
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+using namespace citlali;
+using compute::GgufTensorType;
+
+namespace {
+
+struct SplitMix {
+    uint64_t s;
+    uint64_t next() {
+        uint64_t z = (s += 0x9e3779b97f4a7c15ull);
+        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+        return z ^ (z >> 31);
+    }
+};
+
+uint16_t half_bits(float v) { return compute::float_to_half_bits(v); }
+
+std::vector<uint8_t> quant_bytes(uint64_t seed, GgufTensorType t, int rows, int cols, double gain) {
+    const size_t bb = compute::gguf_type_block_bytes(t);
+    const size_t blocks = (size_t)rows * cols / 256;
+    std::vector<uint8_t> b(blocks * bb);
+    SplitMix r{seed};
+    for (size_t i = 0; i + 8 <= b.size(); i += 8) {
+        const uint64_t v = r.next();
+        std::memcpy(b.data() + i, &v, 8);
+    }
+    const double d = gain / std::sqrt((double)cols) / (t == GgufTensorType::Q4_K ? 300.0 : 1366.0);
+    const uint16_t dh = half_bits((float)d);
+    for (size_t i = 0; i < blocks; ++i) {
+        uint8_t* p = b.data() + i * bb;
+        if (t == GgufTensorType::Q4_K) {
+            std::memcpy(p, &dh, 2);
+            std::memcpy(p + 2, &dh, 2);
+        } else {
+            std::memcpy(p + 208, &dh, 2);
+        }
+    }
+    return b;
+}
+
+model::WeightHandle quant_handle(const std::vector<uint8_t>& bytes, GgufTensorType t, int rows, int cols,
+                                 const std::string& name) {
+    model::WeightHandle w;
+    w.name = name;
+    w.gguf_type = t;
+    w.storage_kind = compute::WeightStorageKind::QuantizedDevice;
+    w.dims = {(uint64_t)cols, (uint64_t)rows};
+    w.element_count = (uint64_t)rows * cols;
+    w.buffer = compute::make_device_buffer(bytes.size());
+    w.buffer->copy_from_host(bytes.data(), bytes.size());
+    return w;
+}
+
+model::WeightHandle norm_handle(int n, const std::string& name) {
+    std::vector<uint16_t> v(n, half_bits(1.0f));
+    model::WeightHandle w;
+    w.name = name;
+    w.gguf_type = GgufTensorType::F16;
+    w.storage_kind = compute::WeightStorageKind::Fp16Device;
+    w.dims = {(uint64_t)n, 1};
+    w.element_count = n;
+    w.buffer = compute::make_device_half_buffer(n);
+    w.buffer->copy_from_host(v.data(), v.size() * 2);
+    return w;
+}
+
+int arg(int argc, char** argv, const char* key, int def) {
+    for (int i = 1; i + 1 < argc; ++i)
+        if (std::strcmp(argv[i], key) == 0) return std::atoi(argv[i + 1]);
+    return def;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+    const int layers = arg(argc, argv, "--layers", 36);
+    const int prompt = arg(argc, argv, "--prompt", 512);
+    const int steps = arg(argc, argv, "--steps", 256);
+    const int distinct = arg(argc, argv, "--distinct", 4);
+    const uint64_t seed = (uint64_t)arg(argc, argv, "--seed", 1);
+    try {
+        if (citlali_hip_init(0) != CITLALI_OK) throw Error(citlali_hip_last_error());
+        model::QwenConfig cfg;
+        cfg.architecture = "qwen3";
+        cfg.vocab_size = 151936;
+        cfg.context_length = 40960;
+        cfg.embedding_length = 4096;
+        cfg.block_count = layers;
+        cfg.feed_forward_length = 12288;
+        cfg.head_count = 32;
+        cfg.head_count_kv = 8;
+        cfg.head_dim = 128;
+        cfg.rms_norm_eps = 1e-6f;
+        cfg.rope_theta = 1e6f;
+        const int H = 4096, F = 12288, NQ = 32 * 128, NKV = 8 * 128, V = 151936;
+
+        const auto t0 = std::chrono::steady_clock::now();
+        struct LayerBytes {
+            std::vector<uint8_t> q, k, v, o, gate, up, down;
+        };
+        std::vector<LayerBytes> sets(distinct);
+        for (int i = 0; i < distinct; ++i) {
+            const uint64_t s = seed * 1000 + (uint64_t)i * 10;
+            sets[i].q = quant_bytes(s + 1, GgufTensorType::Q4_K, NQ, H, 1.0);
+            sets[i].k = quant_bytes(s + 2, GgufTensorType::Q4_K, NKV, H, 1.0);
+            sets[i].v = quant_bytes(s + 3, GgufTensorType::Q6_K, NKV, H, 1.0);
+            sets[i].o = quant_bytes(s + 4, GgufTensorType::Q4_K, H, NQ, 0.5);
+            sets[i].gate = quant_bytes(s + 5, GgufTensorType::Q4_K, F, H, 1.0);
+            sets[i].up = quant_bytes(s + 6, GgufTensorType::Q4_K, F, H, 1.0);
+            sets[i].down = quant_bytes(s + 7, GgufTensorType::Q6_K, H, F, 0.5);
+        }
+        model::QwenWeights w;
+        w.token_embedding = quant_handle(quant_bytes(seed * 7 + 11, GgufTensorType::Q6_K, V, H, std::sqrt(4096.0)),
+                                         GgufTensorType::Q6_K, V, H, "token_embd.weight");
+        w.output_norm = norm_handle(H, "output_norm.weight");
+        w.output_weight = quant_handle(quant_bytes(seed * 7 + 13, GgufTensorType::Q6_K, V, H, 3.0),
+                                       GgufTensorType::Q6_K, V, H, "output.weight");
+        for (int l = 0; l < layers; ++l) {
+            const LayerBytes& b = sets[l % distinct];
+            const std::string n = "blk." + std::to_string(l) + ".";
+            model::QwenLayerWeights L;
+            L.attn_norm = norm_handle(H, n + "attn_norm.weight");
+            L.attn_q = quant_handle(b.q, GgufTensorType::Q4_K, NQ, H, n + "attn_q.weight");
+            L.attn_k = quant_handle(b.k, GgufTensorType::Q4_K, NKV, H, n + "attn_k.weight");
+            L.attn_v = quant_handle(b.v, GgufTensorType::Q6_K, NKV, H, n + "attn_v.weight");
+            L.attn_o = quant_handle(b.o, GgufTensorType::Q4_K, H, NQ, n + "attn_output.weight");
+            L.attn_q_norm = norm_handle(128, n + "attn_q_norm.weight");
+            L.attn_k_norm = norm_handle(128, n + "attn_k_norm.weight");
+            L.ffn_norm = norm_handle(H, n + "ffn_norm.weight");
+            L.ffn_gate = quant_handle(b.gate, GgufTensorType::Q4_K, F, H, n + "ffn_gate.weight");
+            L.ffn_up = quant_handle(b.up, GgufTensorType::Q4_K, F, H, n + "ffn_up.weight");
+            L.ffn_down = quant_handle(b.down, GgufTensorType::Q6_K, H, F, n + "ffn_down.weight");
+            w.layers.push_back(std::move(L));
+        }
+        sets.clear();
+        model::QwenModel m;
+        m.load(cfg, std::move(w), (uint32_t)(prompt + steps));
+        m.synchronize();
+        const double setup_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+
+        // prompt, one token at a time (logits only for the last one)
+        SplitMix r{seed * 31 + 7};
+        std::vector<int32_t> ids(prompt);
+        for (auto& t : ids) t = (int32_t)(r.next() % (uint64_t)V);
+        void *e0 = nullptr, *e1 = nullptr, *e2 = nullptr;
+        citlali_hip_event_create(&e0);
+        citlali_hip_event_create(&e1);
+        citlali_hip_event_create(&e2);
+        uint32_t pos = 0;
+        int32_t next = 0;
+        const auto p0 = std::chrono::steady_clock::now();
+        citlali_hip_event_record(e0);
+        for (int i = 0; i < prompt; ++i) next = m.forward_token(ids[i], pos++, i == prompt - 1);
+        citlali_hip_event_record(e1);
+        const auto p1 = std::chrono::steady_clock::now();
+        // greedy decode
+        uint64_t checksum = 0;
+        for (int i = 0; i < steps; ++i) {
+            next = m.forward_token(next, pos++);
+            checksum = checksum * 1000003ull + (uint64_t)next;
+        }
+        citlali_hip_event_record(e2);
+        citlali_hip_event_synchronize(e2);
+        const auto p2 = std::chrono::steady_clock::now();
+        float prompt_ms = 0, decode_ms = 0;
+        citlali_hip_event_elapsed_ms(e0, e1, &prompt_ms);
+        citlali_hip_event_elapsed_ms(e1, e2, &decode_ms);
+        const double decode_wall = std::chrono::duration<double>(p2 - p1).count();
+        const double prompt_wall = std::chrono::duration<double>(p1 - p0).count();
+        // bytes one decode step must read: every weight once, the KV cache
+        // up to the position, the embedding row and the logits
+        const double layer_bytes = 9437184.0 * 2 + 2359296 + 3440640 + 28311552.0 * 2 + 41287680;
+        const double mean_len = prompt + (steps + 1) / 2.0;
+        const double step_bytes = layer_bytes * layers + 510504960.0 + 3360 + V * 4.0 +
+                                  (double)layers * 2 * 2 * NKV * mean_len;
+        std::printf("{\"workload\": \"BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode\", \"layers\": %d, "
+                    "\"distinct_layer_weight_sets\": %d, \"prompt\": %d, \"steps\": %d, \"decode_tok_per_s\": %.2f, "
+                    "\"decode_ms_per_token\": %.4f, \"decode_ms_per_token_wall\": %.4f, \"prompt_tok_per_s\": %.2f, "
+                    "\"prompt_ms_per_token_wall\": %.4f, \"decode_GBps\": %.1f, \"setup_s\": %.1f, "
+                    "\"token_checksum\": %llu}\n",
+                    layers, distinct, prompt, steps, steps / (decode_ms * 1e-3), decode_ms / steps,
+                    decode_wall * 1e3 / steps, prompt / (prompt_ms * 1e-3), prompt_wall * 1e3 / prompt,
+                    step_bytes / (decode_ms * 1e-3 / steps) / 1e9, setup_s, (unsigned long long)checksum);
+        citlali_hip_event_destroy(e0);
+        citlali_hip_event_destroy(e1);
+        citlali_hip_event_destroy(e2);
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "decode_qwen3: %s\n", e.what());
+        return 1;
+    }
+    return 0;
+}

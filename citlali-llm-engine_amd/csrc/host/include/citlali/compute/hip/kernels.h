@@ -7,6 +7,8 @@
 // `device_zero` here.
 #pragma once
 
+#include "citlali/compute/common/dtype.h"
+
 #include <cstddef>
 #include <cstdint>
 
@@ -39,6 +41,20 @@ void launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* k_cache, ui
 // workspace when large enough; it does not receive the raw scores.
 void launch_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* scores,
                       uint16_t* output, int position, int max_context, int heads, int kv_heads, int head_dim);
+// Fused forward_token steps (no reference counterpart): each gives the
+// results of the launches it names bit for bit, in one launch.
+// launch_add_inplace(x, delta) then launch_rms_norm(x, weight, output).
+void launch_add_rms_norm(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* output, int n,
+                         float eps);
+// launch_rms_norm_heads on q and k (skipped for a null weight), launch_rope
+// on both, launch_store_kv(k, v) into the caches at `position`.
+void launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                               const uint16_t* k_norm, int heads, int kv_heads, int head_dim, int position,
+                               float theta, float eps, uint16_t* k_cache, uint16_t* v_cache);
+// The ffn_gate and ffn_up GEMVs (both of `type`) then launch_swiglu; returns
+// false, launching nothing, when no fused kernel covers the shape.
+bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
+                                  const uint16_t* input, uint16_t* output, int in_features, int out_features);
 // Greedy pick on the device (no reference counterpart: the reference copies
 // the logits to the host, qwen_model.cpp:448-465): the first largest finite
 // value of logits[0..n) is written to *out_index (0 when none is finite).

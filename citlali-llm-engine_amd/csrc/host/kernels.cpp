@@ -82,6 +82,28 @@ void launch_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t
                                             kv_heads, head_dim));
 }
 
+void launch_add_rms_norm(uint16_t* x, const uint16_t* delta, const uint16_t* weight, uint16_t* output, int n,
+                         float eps) {
+    CITLALI_HIP_CHECK(citlali_hip_add_rms_norm(x, delta, weight, output, n, eps));
+}
+
+void launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                               const uint16_t* k_norm, int heads, int kv_heads, int head_dim, int position,
+                               float theta, float eps, uint16_t* k_cache, uint16_t* v_cache) {
+    CITLALI_HIP_CHECK(citlali_hip_qk_norm_rope_store(q, k, v, q_norm, k_norm, heads, kv_heads, head_dim, position,
+                                                     theta, eps, k_cache, v_cache));
+}
+
+bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
+                                  const uint16_t* input, uint16_t* output, int in_features, int out_features) {
+    if (type != GgufTensorType::Q4_K && type != GgufTensorType::Q6_K) return false;
+    const int st = citlali_hip_matvec_gate_up_swiglu(static_cast<int>(type), w_gate, w_up, input, output,
+                                                     in_features, out_features);
+    if (st == CITLALI_ERR_UNSUPPORTED) return false;
+    CITLALI_HIP_CHECK(st);
+    return true;
+}
+
 void launch_argmax(const float* logits, int n, int32_t* out_index) {
     CITLALI_HIP_CHECK(citlali_hip_argmax(logits, n, out_index));
 }

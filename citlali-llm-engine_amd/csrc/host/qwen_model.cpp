@@ -114,7 +114,6 @@ int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compu
     const int head_dim = as_int(config_.head_dim, "head_dim");
     const int heads = as_int(config_.head_count, "head_count");
     const int kv_heads = as_int(config_.head_count_kv, "head_count_kv");
-    const int kv_size = kv_heads * head_dim;
     const int ff = as_int(config_.feed_forward_length, "feed_forward_length");
     const int pos = static_cast<int>(position);
 
@@ -126,46 +125,69 @@ int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compu
         compute::launch_embed(token_embedding_.device_half_data(), token_id, x_->half_data(), hidden);
     }
 
-    for (QwenLayerWeights& layer : layers_) {
-        compute::launch_rms_norm(x_->half_data(), layer.attn_norm.device_half_data(), norm_->half_data(), hidden,
-                                 config_.rms_norm_eps);
+    // The reference's per-layer sequence, with three groups of its launches
+    // done by fused kernels that give the same results bit for bit: the
+    // residual add with the RMSNorm that follows it, the q/k head norms with
+    // RoPE and the KV store, and (when gate and up share a type and have no
+    // bias) the gate/up GEMVs with SwiGLU.
+    bool normed = false;   // norm_ already holds this layer's attn_norm(x)
+    for (size_t li = 0; li < layers_.size(); ++li) {
+        QwenLayerWeights& layer = layers_[li];
+        if (!normed)
+            compute::launch_rms_norm(x_->half_data(), layer.attn_norm.device_half_data(), norm_->half_data(),
+                                     hidden, config_.rms_norm_eps);
         linear_backend_->forward(layer.attn_q, norm_, q_);
         add_bias_if_present(layer.attn_q_bias, q_, static_cast<uint64_t>(heads) * head_dim);
         linear_backend_->forward(layer.attn_k, norm_, k_);
         add_bias_if_present(layer.attn_k_bias, k_, static_cast<uint64_t>(kv_heads) * head_dim);
         linear_backend_->forward(layer.attn_v, norm_, v_);
         add_bias_if_present(layer.attn_v_bias, v_, static_cast<uint64_t>(kv_heads) * head_dim);
-        if (layer.attn_q_norm.buffer)
-            compute::launch_rms_norm_heads(q_->half_data(), layer.attn_q_norm.device_half_data(), q_->half_data(),
-                                           heads, head_dim, config_.rms_norm_eps);
-        if (layer.attn_k_norm.buffer)
-            compute::launch_rms_norm_heads(k_->half_data(), layer.attn_k_norm.device_half_data(), k_->half_data(),
-                                           kv_heads, head_dim, config_.rms_norm_eps);
-        compute::launch_rope(q_->half_data(), heads, head_dim, pos, config_.rope_theta);
-        compute::launch_rope(k_->half_data(), kv_heads, head_dim, pos, config_.rope_theta);
-        compute::launch_store_kv(k_->half_data(), v_->half_data(), layer.k_cache->half_data(),
-                                 layer.v_cache->half_data(), pos, kv_size);
+        compute::launch_qk_norm_rope_store(
+            q_->half_data(), k_->half_data(), v_->half_data(),
+            layer.attn_q_norm.buffer ? layer.attn_q_norm.device_half_data() : nullptr,
+            layer.attn_k_norm.buffer ? layer.attn_k_norm.device_half_data() : nullptr, heads, kv_heads, head_dim, pos,
+            config_.rope_theta, config_.rms_norm_eps, layer.k_cache->half_data(), layer.v_cache->half_data());
         compute::launch_attention(q_->half_data(), layer.k_cache->half_data(), layer.v_cache->half_data(),
                                   static_cast<float*>(scores_->data()), attn_out_->half_data(), pos,
                                   static_cast<int>(max_context_), heads, kv_heads, head_dim);
         linear_backend_->forward(layer.attn_o, attn_out_, attn_proj_);
         add_bias_if_present(layer.attn_o_bias, attn_proj_, hidden);
-        compute::launch_add_inplace(x_->half_data(), attn_proj_->half_data(), hidden);
-        compute::launch_rms_norm(x_->half_data(), layer.ffn_norm.device_half_data(), norm_->half_data(), hidden,
-                                 config_.rms_norm_eps);
-        linear_backend_->forward(layer.ffn_gate, norm_, gate_);
-        add_bias_if_present(layer.ffn_gate_bias, gate_, ff);
-        linear_backend_->forward(layer.ffn_up, norm_, up_);
-        add_bias_if_present(layer.ffn_up_bias, up_, ff);
-        compute::launch_swiglu(gate_->half_data(), up_->half_data(), ff_act_->half_data(), ff);
+        compute::launch_add_rms_norm(x_->half_data(), attn_proj_->half_data(), layer.ffn_norm.device_half_data(),
+                                     norm_->half_data(), hidden, config_.rms_norm_eps);
+        const bool fuse_ffn = layer.ffn_gate.storage_kind == compute::WeightStorageKind::QuantizedDevice &&
+                              layer.ffn_up.storage_kind == compute::WeightStorageKind::QuantizedDevice &&
+                              layer.ffn_gate.gguf_type == layer.ffn_up.gguf_type && !layer.ffn_gate_bias.buffer &&
+                              !layer.ffn_up_bias.buffer;
+        if (!fuse_ffn || !compute::launch_matvec_gate_up_swiglu(layer.ffn_gate.gguf_type,
+                                                                layer.ffn_gate.device_quantized_data(),
+                                                                layer.ffn_up.device_quantized_data(),
+                                                                norm_->half_data(), ff_act_->half_data(), hidden, ff)) {
+            linear_backend_->forward(layer.ffn_gate, norm_, gate_);
+            add_bias_if_present(layer.ffn_gate_bias, gate_, ff);
+            linear_backend_->forward(layer.ffn_up, norm_, up_);
+            add_bias_if_present(layer.ffn_up_bias, up_, ff);
+            compute::launch_swiglu(gate_->half_data(), up_->half_data(), ff_act_->half_data(), ff);
+        }
         linear_backend_->forward(layer.ffn_down, ff_act_, ff_out_);
         add_bias_if_present(layer.ffn_down_bias, ff_out_, hidden);
-        compute::launch_add_inplace(x_->half_data(), ff_out_->half_data(), hidden);
+        // residual add, fused with the norm that reads x next when there is one
+        const WeightHandle* next_norm = li + 1 < layers_.size() ? &layers_[li + 1].attn_norm
+                                        : compute_logits             ? &output_norm_
+                                                                     : nullptr;
+        if (next_norm) {
+            compute::launch_add_rms_norm(x_->half_data(), ff_out_->half_data(), next_norm->device_half_data(),
+                                         norm_->half_data(), hidden, config_.rms_norm_eps);
+            normed = true;
+        } else {
+            compute::launch_add_inplace(x_->half_data(), ff_out_->half_data(), hidden);
+            normed = false;
+        }
     }
     if (!compute_logits) return -1;
 
-    compute::launch_rms_norm(x_->half_data(), output_norm_.device_half_data(), norm_->half_data(), hidden,
-                             config_.rms_norm_eps);
+    if (!normed)
+        compute::launch_rms_norm(x_->half_data(), output_norm_.device_half_data(), norm_->half_data(), hidden,
+                                 config_.rms_norm_eps);
     const int vocab = as_int(config_.vocab_size, "vocab_size");
     if (output_weight_.storage_kind == compute::WeightStorageKind::QuantizedDevice) {
         if (output_weight_.gguf_type != compute::GgufTensorType::Q6_K)

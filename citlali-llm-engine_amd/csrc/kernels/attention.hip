@@ -104,7 +104,9 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int sub = ((chunk / kWaves + C::kTP - 1) / C::kTP) * C::kTP;
+    // the chunk's positions split over the four waves in whole tiles (a
+    // short sequence's only chunk still occupies every wave)
+    const int sub = (((b1 - b0 + kWaves - 1) / kWaves + C::kTP - 1) / C::kTP) * C::kTP;
     const int w0 = min(b1, b0 + wave * sub);
     const int w1 = min(b1, w0 + sub);
 

@@ -68,6 +68,72 @@ __global__ void rms_norm_kernel(const uint16_t* __restrict__ in, const uint16_t*
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[base + i] = f2h_rne(h2f(in[base + i]) * inv * h2f(w[i]));
 }
 
+// Residual add then RMSNorm of the sum, one launch for the reference's
+// launch_add_inplace + launch_rms_norm pair (qwen_model.cpp:340-341, 372 and
+// the next layer's 306 or the final norm at 385): x = fp16(x + d) is stored,
+// then norm = fp16(x * rsqrt(mean(x^2) + eps) * w) over the stored values.
+// Same single 1024-thread block and reduction order as rms_norm_kernel, so
+// the results equal the two separate launches bit for bit.
+__global__ void add_rms_norm_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ d,
+                                    const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int n, float eps) {
+    __shared__ float red[16];
+    float s = 0.f;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) {
+        const uint16_t xi = f2h_rne(h2f(x[i]) + h2f(d[i]));
+        x[i] = xi;
+        const float v = h2f(xi);
+        s += v * v;
+    }
+    s = block_sum(s, red);
+    const float inv = rsqrtf(s / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = f2h_rne(h2f(x[i]) * inv * h2f(w[i]));
+}
+
+// Per-head RMSNorm of q and k (when their weights are given), NeoX RoPE of
+// both, and the store of this position's k and v rows into the caches: the
+// reference's launch_rms_norm_heads x2, launch_rope x2 and launch_store_kv
+// (qwen_model.cpp:326-336) in one launch.  Block h < heads is query head h
+// (rewritten in place); block heads + j is kv head j (k roped into k_cache,
+// v copied into v_cache).  Each stage rounds to fp16 where the separate
+// kernels store, with the same per-head 128-thread reduction, so the
+// results equal the separate launches bit for bit.
+__global__ void qk_norm_rope_store_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                          const uint16_t* __restrict__ v, const uint16_t* __restrict__ qw,
+                                          const uint16_t* __restrict__ kw, int heads, int head_dim, int position,
+                                          float theta, float eps, uint16_t* __restrict__ k_cache,
+                                          uint16_t* __restrict__ v_cache, int kv_size) {
+    __shared__ float red[16];
+    __shared__ uint16_t vals[256];
+    const bool is_q = (int)blockIdx.x < heads;
+    const int head = is_q ? blockIdx.x : blockIdx.x - heads;
+    const uint16_t* src = is_q ? q + (size_t)head * head_dim : k + (size_t)head * head_dim;
+    const uint16_t* w = is_q ? qw : kw;
+    const int i = threadIdx.x;   // blockDim.x == 128 >= head_dim
+    uint16_t xi = i < head_dim ? src[i] : (uint16_t)0;
+    if (w != nullptr) {
+        const float xv = h2f(xi);
+        const float ss = block_sum(i < head_dim ? xv * xv : 0.f, red);
+        const float inv = rsqrtf(ss / (float)head_dim + eps);
+        if (i < head_dim) xi = f2h_rne(xv * inv * h2f(w[i]));
+    }
+    if (i < head_dim) vals[i] = xi;
+    __syncthreads();
+    const int half = head_dim / 2;
+    uint16_t* dst = is_q ? q + (size_t)head * head_dim
+                         : k_cache + (size_t)position * kv_size + (size_t)head * head_dim;
+    if (i < half) {
+        const float inv_freq = powf(theta, -(float)(2 * i) / (float)head_dim);
+        const float angle = (float)position * inv_freq;
+        float sn, cs;
+        sincosf(angle, &sn, &cs);
+        const float x0 = h2f(vals[i]), x1 = h2f(vals[half + i]);
+        dst[i] = f2h_rne(x0 * cs - x1 * sn);
+        dst[half + i] = f2h_rne(x0 * sn + x1 * cs);
+    }
+    if (!is_q && i < head_dim)
+        v_cache[(size_t)position * kv_size + (size_t)head * head_dim + i] = v[(size_t)head * head_dim + i];
+}
+
 // NeoX pairs (i, i + hd/2), angle = position * theta^(-2i/hd) (kernels.cu:485-521)
 __global__ void rope_kernel(uint16_t* __restrict__ data, int head_dim, int position, float theta) {
     const int head = blockIdx.x, i = threadIdx.x, half = head_dim / 2;
@@ -123,45 +189,55 @@ __global__ __launch_bounds__(kBlk) void matvec_f16_kernel(const uint16_t* __rest
 
 // Greedy argmax with the host rule of qwen_model.cpp:455-463: the first
 // (lowest index) strictly greatest finite value wins; all non-finite -> 0.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                      int32_t* __restrict__ out) {
-    __shared__ float bv[16];
-    __shared__ int bi[16];
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = logits[i];
-        if (isfinite(v) && (v > best || (v == best && i < idx))) {
-            best = v;
-            idx = i;
-        }
-    }
+// Two launches: blocks reduce contiguous ranges to a partial, one block
+// reduces the partials.  A candidate is one 64-bit key, (order-preserving
+// bits of the value) << 32 | ~index, so the largest key is the largest value
+// and, among equal values, the lowest index; -0.0 counts as +0.0, as the
+// host's `>` does.  0 means "no finite value".
+constexpr int kArgmaxThreads = 256;
+constexpr int kArgmaxMaxBlocks = 1024;
+__device__ uint64_t g_argmax_partial[kArgmaxMaxBlocks];   // per device; concurrent argmax calls would race
+
+__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
+    if (!isfinite(v)) return 0ull;
+    uint32_t u = __float_as_uint(v == 0.f ? 0.f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)u << 32) | (uint32_t)~(uint32_t)i;
+}
+
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t k, uint64_t* red) {
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off, kWave);
-        const int oi = __shfl_xor(idx, off, kWave);
-        if (ov > best || (ov == best && oi < idx)) {
-            best = ov;
-            idx = oi;
-        }
+        const uint64_t o = __shfl_xor(k, off, kWave);
+        k = o > k ? o : k;
     }
     const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-    if (lane == 0) {
-        bv[wave] = best;
-        bi[wave] = idx;
-    }
+    if (lane == 0) red[wave] = k;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float b = -INFINITY;
-        int id = 0x7fffffff;
-        for (int w = 0; w < (int)(blockDim.x / kWave); ++w) {
-            if (bv[w] > b || (bv[w] == b && bi[w] < id)) {
-                b = bv[w];
-                id = bi[w];
-            }
-        }
-        out[0] = (id == 0x7fffffff) ? 0 : id;
+    uint64_t m = 0;
+    for (int w = 0; w < (int)(blockDim.x / kWave); ++w) m = red[w] > m ? red[w] : m;
+    return m;
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(const float* __restrict__ logits, int n,
+                                                                         int per_block) {
+    __shared__ uint64_t red[kArgmaxThreads / kWave];
+    const int b0 = blockIdx.x * per_block, b1 = min(n, b0 + per_block);
+    uint64_t k = 0;
+    for (int i = b0 + (int)threadIdx.x; i < b1; i += kArgmaxThreads) {
+        const uint64_t c = argmax_key(logits[i], i);
+        k = c > k ? c : k;
     }
+    const uint64_t m = block_max_u64(k, red);
+    if (threadIdx.x == 0) g_argmax_partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(int parts, int32_t* __restrict__ out) {
+    __shared__ uint64_t red[kArgmaxThreads / kWave];
+    uint64_t k = 0;
+    for (int i = threadIdx.x; i < parts; i += kArgmaxThreads) k = g_argmax_partial[i] > k ? g_argmax_partial[i] : k;
+    const uint64_t m = block_max_u64(k, red);
+    if (threadIdx.x == 0) out[0] = m == 0 ? 0 : (int32_t)~(uint32_t)(m & 0xffffffffu);
 }
 
 __global__ void fill_zero_kernel(uint32_t* __restrict__ p, size_t nwords) {
@@ -229,6 +305,20 @@ hipError_t launch_rms_norm_heads(const uint16_t* in, const uint16_t* w, uint16_t
     return hipGetLastError();
 }
 
+hipError_t launch_add_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w, uint16_t* out, int n, float eps,
+                               hipStream_t s) {
+    launch_kernel(add_rms_norm_kernel, dim3(1), dim3(1024), 0, s, x, d, w, out, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* qw,
+                                     const uint16_t* kw, int heads, int kv_heads, int head_dim, int position,
+                                     float theta, float eps, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s) {
+    launch_kernel(qk_norm_rope_store_kernel, dim3(heads + kv_heads), dim3(kWave * 2), 0, s, q, k, v, qw, kw, heads,
+                  head_dim, position, theta, eps, k_cache, v_cache, kv_heads * head_dim);
+    return hipGetLastError();
+}
+
 hipError_t launch_rope(uint16_t* data, int heads, int head_dim, int position, float theta, hipStream_t s) {
     const int threads = ((head_dim / 2 + kWave - 1) / kWave) * kWave;
     launch_kernel(rope_kernel, dim3(heads), dim3(threads), 0, s, data, head_dim, position, theta);
@@ -249,7 +339,15 @@ hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool
 }
 
 hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s) {
-    launch_kernel(argmax_kernel, dim3(1), dim3(1024), 0, s, logits, n, out_index);
+    // about 4 values per thread, at most kArgmaxMaxBlocks partials
+    int parts = (n + 4 * kArgmaxThreads - 1) / (4 * kArgmaxThreads);
+    if (parts > kArgmaxMaxBlocks) parts = kArgmaxMaxBlocks;
+    const int per_block = (n + parts - 1) / parts;
+    parts = (n + per_block - 1) / per_block;
+    launch_kernel_in_call(false, argmax_partial_kernel, dim3(parts), dim3(kArgmaxThreads), 0, s, logits, n, per_block);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_kernel(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, parts, out_index);
     return hipGetLastError();
 }
 

@@ -92,6 +92,15 @@ hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, in
 hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
                              hipStream_t s);
 hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s);
+// fused forward_token steps (no reference counterpart; same results as the
+// separate launches)
+hipError_t launch_add_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w, uint16_t* out, int n, float eps,
+                               hipStream_t s);
+hipError_t launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* qw,
+                                     const uint16_t* kw, int heads, int kv_heads, int head_dim, int position,
+                                     float theta, float eps, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s);
+hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
+                                        uint16_t* act, int K, int N, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hipStream_t s);
 

@@ -343,6 +343,70 @@ __global__ __launch_bounds__(kBlock) void matvec_stream_kernel(const uint8_t* __
     }
 }
 
+// ffn_gate and ffn_up GEMVs plus SwiGLU in one launch (the reference's two
+// LinearBackend::forward calls and launch_swiglu, qwen_model.cpp:364-368).
+// Each wave computes row r of both matrices exactly as matvec_stream_kernel
+// does (same lane mapping and summation order), rounds both to fp16 where
+// the separate GEMVs store, and writes act[r] = fp16(silu(g) * u) with the
+// swiglu_kernel expression -- the separate launches' results bit for bit.
+template <class QT, int S, int M>
+__global__ __launch_bounds__(kBlock) void matvec_gate_up_kernel(const uint8_t* __restrict__ wg,
+                                                                const uint8_t* __restrict__ wu,
+                                                                const uint16_t* __restrict__ x,
+                                                                uint16_t* __restrict__ act, int K, int N) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
+    float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int l4 = lane & 3;
+    const int sub = lane >> 2;
+    constexpr int nb = S * kSbPerStep;
+    constexpr int D = S * M;
+    const int W = gridDim.x * kWavesPerBlock;
+    const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+
+    auto frag_at = [&](const uint8_t* w, int row, int t) {
+        const size_t f = (size_t)min(row, N - 1) * nb + t * kSbPerStep + sub;
+        return QT::load(w + f * QT::kBytes, l4);
+    };
+
+    XStage<QT::kSxPerBlock == 16, 2 * S> xs;   // K = 4096 * S
+    xs.load(x);
+    __builtin_amdgcn_sched_barrier(0);
+    typename QT::Frag fg[D], fu[D];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+        for (int t = 0; t < S; ++t) {
+            fg[m * S + t] = frag_at(wg, gw + m * W, t);
+            fu[m * S + t] = frag_at(wu, gw + m * W, t);
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    xs.store(xp, sx);
+
+    for (int row = gw; row < N; row += M * W) {
+#pragma unroll
+        for (int m = 0; m < M; ++m) {
+            const int r = row + m * W;
+            float ag = 0.f, au = 0.f;
+#pragma unroll
+            for (int t = 0; t < S; ++t) {
+                ag += QT::dot(fg[m * S + t], l4, xp, sx, t * kSbPerStep + sub);
+                au += QT::dot(fu[m * S + t], l4, xp, sx, t * kSbPerStep + sub);
+                fg[m * S + t] = frag_at(wg, r + M * W, t);
+                fu[m * S + t] = frag_at(wu, r + M * W, t);
+            }
+            ag = wave_sum(ag);
+            au = wave_sum(au);
+            if (lane == 0 && r < N) {
+                const float g = h2f(f2h_rne(ag)), u = h2f(f2h_rne(au));
+                act[r] = f2h_rne(g / (1.0f + expf(-g)) * u);
+            }
+        }
+    }
+}
+
 // Any super-block count: a wave owns kRows rows and walks their super-blocks
 // as one flat list; a lane's row is found by multiply-high division.
 template <class QT, bool kF32, int kRows>
@@ -438,6 +502,25 @@ hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, in
     return hipGetLastError();
 }
 
+template <class QT>
+hipError_t launch_gate_up(const uint8_t* wg, const uint8_t* wu, const uint16_t* x, uint16_t* act, int K, int N,
+                          hipStream_t stream) {
+    const size_t lds = (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float);
+    int grid = 2 * device_cus();
+    const int need = (N + kWavesPerBlock - 1) / kWavesPerBlock;
+    if (grid > need) grid = need;
+    switch (K / kQK) {
+        case 16:
+            launch_kernel((matvec_gate_up_kernel<QT, 1, 2>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x, act, K, N);
+            break;
+        case 32:
+            launch_kernel((matvec_gate_up_kernel<QT, 2, 1>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x, act, K, N);
+            break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 }  // namespace
 
 size_t matvec_lds_bytes(int kind, int K) {
@@ -454,4 +537,12 @@ hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool 
     return f32_out ? launch_matvec<Q6K, true>(w, x, y, K, N, s) : launch_matvec<Q6K, false>(w, x, y, K, N, s);
 }
 
+}  // namespace citlali::hip
+
+namespace citlali::hip {
+// kind 4: Q4_K, 6: Q6_K; in_features 4096 or 8192 (16 or 32 super-blocks)
+hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
+                                        uint16_t* act, int K, int N, hipStream_t s) {
+    return kind == 6 ? launch_gate_up<Q6K>(wg, wu, x, act, K, N, s) : launch_gate_up<Q4K>(wg, wu, x, act, K, N, s);
+}
 }  // namespace citlali::hip

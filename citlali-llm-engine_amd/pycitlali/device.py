@@ -204,3 +204,21 @@ def argmax(logits, n: int, out_index) -> None:
     """Index of the first largest finite value of `n` fp32 logits, written to
     the device int32 `out_index` (0 when none is finite)."""
     _lib.call("citlali_hip_argmax", _vp(logits), int(n), _vp(out_index))
+
+
+# ---- fused forward_token steps (same results as the separate launches) ----
+def add_rms_norm(x, delta, w, out, n: int, eps: float) -> None:
+    _lib.call("citlali_hip_add_rms_norm", _vp(x), _vp(delta), _vp(w), _vp(out), int(n), ctypes.c_float(eps))
+
+
+def qk_norm_rope_store(q, k, v, q_norm, k_norm, heads: int, kv_heads: int, head_dim: int, position: int,
+                       theta: float, eps: float, k_cache, v_cache) -> None:
+    null = ctypes.c_void_p(0)
+    _lib.call("citlali_hip_qk_norm_rope_store", _vp(q), _vp(k), _vp(v), _vp(q_norm) if q_norm is not None else null,
+              _vp(k_norm) if k_norm is not None else null, int(heads), int(kv_heads), int(head_dim), int(position),
+              ctypes.c_float(theta), ctypes.c_float(eps), _vp(k_cache), _vp(v_cache))
+
+
+def matvec_gate_up_swiglu(kind: str, w_gate, w_up, x, act, in_features: int, out_features: int) -> None:
+    _lib.call("citlali_hip_matvec_gate_up_swiglu", 12 if kind == "q4k" else 14, _vp(w_gate), _vp(w_up), _vp(x),
+              _vp(act), int(in_features), int(out_features))

@@ -148,14 +148,35 @@ int citlali_hip_swiglu(const uint16_t* gate, const uint16_t* up, uint16_t* out, 
 int citlali_hip_rope(uint16_t* data, int heads, int head_dim, int position, float theta);    /* kernels.h:35 */
 
 /* Greedy sampling on the device: index of the first greatest finite logit
- * (0 if none), written to device int32 *out_index.  Replaces the host loop
- * of sample_greedy_from_logits (qwen_model.cpp:448-465). */
+ * (0 if none; -0.0 equals +0.0), written to device int32 *out_index.
+ * Replaces the host loop of sample_greedy_from_logits (qwen_model.cpp:
+ * 448-465).  Uses a per-device partials table in the library: argmax calls
+ * that overlap on one device (several streams) race. */
 int citlali_hip_argmax(const float* logits, int n, int32_t* out_index);
 
 /* ---- timing (bench and tests) --------------------------------------------- */
 /* Reads `bytes` (16-byte multiple) of a device buffer once, as fast as the
  * memory system allows: the measured HBM read ceiling.  `sink`: 4 bytes. */
 int citlali_hip_stream_read(const void* buf, size_t bytes, void* sink);
+/* ---- fused forward_token steps (no reference counterpart) ---------------- *
+ * Each equals the sequence of reference launches it names, bit for bit (same
+ * fp16 store points and reduction order); QwenModel uses them to cut the
+ * launches per layer.                                                       */
+/* launch_add_inplace(x, delta) then launch_rms_norm(x, w, out) */
+int citlali_hip_add_rms_norm(uint16_t* x, const uint16_t* delta, const uint16_t* w, uint16_t* out, int n, float eps);
+/* launch_rms_norm_heads on q and k (skipped for a NULL weight), launch_rope
+ * on q and k, launch_store_kv(k, v) -- q rewritten in place, k and v written
+ * to the caches at `position`.  head_dim even and <= 128. */
+int citlali_hip_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                                   const uint16_t* k_norm, int heads, int kv_heads, int head_dim, int position,
+                                   float theta, float eps, uint16_t* k_cache, uint16_t* v_cache);
+/* LinearBackend::forward for ffn_gate and ffn_up (both of GGUF type
+ * `gguf_type`, 12 = Q4_K or 14 = Q6_K) then launch_swiglu.  Returns
+ * CITLALI_ERR_UNSUPPORTED, launching nothing, for in_features other than
+ * 4096 or 8192 -- then use the separate launches. */
+int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up, const uint16_t* x,
+                                      uint16_t* act, int in_features, int out_features);
+
 /* Kernel timing (no reference counterpart; for benchmarks): while armed with
  * two events of citlali_hip_event_create, the first kernel the calling thread
  * launches records `start` when it begins and every kernel records `stop`

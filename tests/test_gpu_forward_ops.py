@@ -180,3 +180,81 @@ def test_kernel_timer_brackets_the_calls_kernels(hip):
     hip.synchronize()
     t1, t2 = one.ms(), two.ms()
     assert 0 < t1 < 5 and t2 > 1.5 * t1, (t1, t2)
+
+
+def test_argmax_signed_zero_and_block_edges(hip, orc):
+    """-0.0 and +0.0 are equal for the host's `>`: the first one wins.  The
+    device reduces ranges of about 1024 values per block: maxima placed at
+    range edges and in the last partial range are found."""
+    x = np.full(5000, -1.0, np.float32)
+    x[7], x[9] = -0.0, 0.0
+    assert _argmax(hip, x) == orc.argmax(x) == 7
+    n = 151936
+    for pos in (0, 1023, 1024, 2047, n - 1):
+        y = np.zeros(n, np.float32)
+        y[pos] = 1.0
+        y[min(n - 1, pos + 5)] = 1.0   # a later equal value
+        assert _argmax(hip, y) == orc.argmax(y) == pos
+
+
+# ---- fused forward_token steps: the separate launches' results, bit for bit ----
+@pytest.mark.parametrize("n", [1024, 4096])
+def test_add_rms_norm_equals_add_then_norm(hip, n):
+    rng = hip.synth.Rng(500 + n)
+    x, d, w = (hip.synth.normal_f16(rng, n) for _ in range(3))
+    dx1, dd, dw = up(hip, x), up(hip, d), up(hip, w)
+    o1 = hip.DeviceArray(n * 2)
+    hip.device.add_inplace(dx1, dd, n)
+    hip.device.rms_norm(dx1, dw, o1, n, 1e-6)
+    dx2, o2 = up(hip, x), hip.DeviceArray(n * 2)
+    hip.device.add_rms_norm(dx2, dd, dw, o2, n, 1e-6)
+    assert np.array_equal(dx1.download(np.uint16, n), dx2.download(np.uint16, n))
+    assert np.array_equal(o1.download(np.uint16, n), o2.download(np.uint16, n))
+
+
+@pytest.mark.parametrize("with_norm", [True, False])
+@pytest.mark.parametrize("heads,kv,hd,pos", [(32, 8, 128, 700), (16, 8, 128, 0), (16, 4, 64, 37)])
+def test_qk_norm_rope_store_equals_separate_launches(hip, heads, kv, hd, pos, with_norm):
+    rng = hip.synth.Rng(heads * 1000 + pos)
+    ctx = 1024
+    q, k, v = hip.synth.normal_f16(rng, heads * hd), hip.synth.normal_f16(rng, kv * hd), hip.synth.normal_f16(rng, kv * hd)
+    qw, kw = hip.synth.normal_f16(rng, hd), hip.synth.normal_f16(rng, hd)
+    cache0 = hip.synth.normal_f16(rng, ctx * kv * hd)
+    # separate launches (qwen_model.cpp:326-336)
+    dq, dk, dv = up(hip, q), up(hip, k), up(hip, v)
+    kc1, vc1 = up(hip, cache0), up(hip, cache0)
+    if with_norm:
+        hip.device.rms_norm_heads(dq, up(hip, qw), dq, heads, hd, 1e-6)
+        hip.device.rms_norm_heads(dk, up(hip, kw), dk, kv, hd, 1e-6)
+    hip.device.rope(dq, heads, hd, pos, 1e6)
+    hip.device.rope(dk, kv, hd, pos, 1e6)
+    hip.device.store_kv(dk, dv, kc1, vc1, pos, kv * hd)
+    # fused
+    fq = up(hip, q)
+    kc2, vc2 = up(hip, cache0), up(hip, cache0)
+    hip.device.qk_norm_rope_store(fq, up(hip, k), up(hip, v), up(hip, qw) if with_norm else None,
+                                  up(hip, kw) if with_norm else None, heads, kv, hd, pos, 1e6, 1e-6, kc2, vc2)
+    assert np.array_equal(dq.download(np.uint16, heads * hd), fq.download(np.uint16, heads * hd))
+    assert np.array_equal(kc1.download(np.uint16), kc2.download(np.uint16))
+    assert np.array_equal(vc1.download(np.uint16), vc2.download(np.uint16))
+
+
+@pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q4k", 3000, 8192), ("q6k", 2048, 4096)])
+def test_gate_up_swiglu_equals_two_gemvs_and_swiglu(hip, kind, n, k):
+    rng = hip.synth.Rng(n + k)
+    wg, wu = hip.synth.quant_matrix(kind, rng, n, k), hip.synth.quant_matrix(kind, rng, n, k)
+    x = hip.synth.normal_f16(rng, k)
+    dg, du, dx = up(hip, wg), up(hip, wu), up(hip, x)
+    g, u, a1 = hip.DeviceArray(n * 2), hip.DeviceArray(n * 2), hip.DeviceArray(n * 2)
+    hip.device.matvec(kind, dg, dx, g, k, n)
+    hip.device.matvec(kind, du, dx, u, k, n)
+    hip.device.swiglu(g, u, a1, n)
+    a2 = hip.DeviceArray(n * 2)
+    hip.device.matvec_gate_up_swiglu(kind, dg, du, dx, a2, k, n)
+    assert np.array_equal(a1.download(np.uint16, n), a2.download(np.uint16, n))
+
+
+def test_gate_up_swiglu_declines_other_lengths(hip):
+    d = hip.DeviceArray(1 << 20)
+    with pytest.raises(hip.CitlaliError, match="no fused kernel"):
+        hip.device.matvec_gate_up_swiglu("q4k", d, d, d, d, 2048, 64)
