@@ -19,7 +19,8 @@ steps, from HIP events that the kernel's own dispatches stamp
 (hipExtLaunchKernel; for attention, split start to merge end).  cpu_baseline: the
 oracle's restatement of the reference's host arithmetic (dequant to fp16 with
 the host rule, fp32 dot; fp32 attention) on a bounded sample of the same
-layer, on this machine's host cores.
+layer, on this machine's host cores.  decode_cfg5: BASELINE config 5 (the
+whole synthetic Qwen3-8B, greedy decode tok/s) from bin/decode_qwen3.
 """
 from __future__ import annotations
 
@@ -202,6 +203,22 @@ def cpu_baseline(host, budget_s):
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "cfg3_layer_hbm_traffic_pmc.md")
 
 
+DECODE_BIN = os.path.join(ROOT, "citlali-llm-engine_amd", "bin", "decode_qwen3")
+
+
+def decode_cfg5():
+    """BASELINE config 5 beside the headline: the synthetic Qwen3-8B greedy
+    decode through QwenModel (bin/decode_qwen3, a child process), 512-token
+    prompt then 256 greedy steps; decode tok/s from HIP events."""
+    import subprocess
+    if not os.path.exists(DECODE_BIN):
+        return {"error": "citlali-llm-engine_amd/bin/decode_qwen3 is not built"}
+    p = subprocess.run([DECODE_BIN], capture_output=True, text=True, timeout=600)
+    if p.returncode != 0:
+        return {"error": (p.stderr or p.stdout)[-300:]}
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
 def read_traffic(kernel):
     """HBM bytes per launch of `kernel` (a step-kernel name) from the
     committed rocprofv3 PMC summary: the line 'traffic_bytes_per_launch
@@ -222,6 +239,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-decode", action="store_true", help="skip the config-5 whole-model decode run")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the decode hot path here is a single-GPU build "
@@ -263,6 +281,7 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+    line["decode_cfg5"] = None if args.no_decode else decode_cfg5()
     print(json.dumps(line), flush=True)
 
 

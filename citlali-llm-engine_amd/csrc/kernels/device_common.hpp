@@ -14,9 +14,10 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-// A 16-byte vector that the compiler may only assume 4-byte aligned: used for
-// Q6_K super-blocks, which start on 2-byte boundaries.
-typedef u32x4 u32x4_a4 __attribute__((aligned(4)));
+// Vectors the compiler may only assume 2-byte aligned: Q6_K super-blocks start
+// on 2-byte boundaries and are read with unaligned global loads.
+typedef u32x4 u32x4_a2 __attribute__((aligned(2)));
+typedef u32x2 u32x2_a2 __attribute__((aligned(2)));
 
 constexpr int kWave = 64;
 constexpr int kQK = 256;          // values per K-quant super-block
@@ -143,12 +144,6 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Loads 4 bytes at a 2-byte aligned address as an aligned 8-byte window and
-// funnel-shifts: lo/hi are the dwords covering [a & ~3, (a & ~3) + 8).
-__device__ __forceinline__ uint32_t align_bytes(uint32_t lo, uint32_t hi, uint32_t shift_bytes) {
-    return __builtin_amdgcn_alignbyte(hi, lo, shift_bytes);
 }
 
 // N consecutive floats from LDS (16-byte aligned for N >= 4, 8-byte for 2)

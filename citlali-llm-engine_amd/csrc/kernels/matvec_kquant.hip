@@ -197,38 +197,22 @@ struct Q6K {
     static constexpr int kSxPerBlock = 16;
     struct Frag { uint32_t wa[4], wb[4], u[4]; uint32_t s0, s1, dbits; };
 
-    // 16 bytes at a 2-byte aligned address `p`, through the dword-aligned
-    // window [p - s, p - s + 20), s = p & 3 in {0, 2}.  The window never
-    // leaves the super-block for the ranges used here.
-    __device__ static __forceinline__ void load16(const uint8_t* p, uint32_t s, uint32_t out[4]) {
-        const uint8_t* base = p - s;
-        const u32x4 v = *reinterpret_cast<const u32x4_a4*>(base);
-        const uint32_t e = *reinterpret_cast<const uint32_t*>(base + 16);
-        const uint32_t sb = s;  // bytes
-        out[0] = align_bytes(v.x, v.y, sb);
-        out[1] = align_bytes(v.y, v.z, sb);
-        out[2] = align_bytes(v.z, v.w, sb);
-        out[3] = align_bytes(v.w, e, sb);
-    }
-
-    // lane_in_sb = 2*h + ih
+    // lane_in_sb = 2*h + ih.  A 210-byte block starts on a 2-byte boundary;
+    // gfx950 global loads take unaligned addresses (the ROCm default
+    // unaligned mode, which the compiler targets), so each range is one
+    // 16-byte load.
     __device__ static __forceinline__ Frag load(const uint8_t* sb, int l4) {
         const int h = l4 >> 1, ih = l4 & 1;
-        const uint32_t s = (uint32_t)((uintptr_t)sb & 3u);
         Frag f;
-        load16(sb + 64 * h + 16 * ih, s, f.wa);
-        load16(sb + 64 * h + 32 + 16 * ih, s, f.wb);
-        load16(sb + 128 + 32 * h + 16 * ih, s, f.u);
-        // scales[8h .. 8h+8) from the dword window [188 + 8h + s, +12) of the
-        // block (inside its 210 bytes for s = 0 and s = 2); they start
-        // o = 4 - s bytes into it.  Branch-free, so loads stay countable.
-        const uint8_t* sw = sb + 188 + 8 * h + s;
-        const uint32_t w0 = *reinterpret_cast<const uint32_t*>(sw);
-        const uint32_t w1 = *reinterpret_cast<const uint32_t*>(sw + 4);
-        const uint32_t w2 = *reinterpret_cast<const uint32_t*>(sw + 8);
-        const uint32_t o = 8u * (4u - s);
-        f.s0 = (uint32_t)((((uint64_t)w1 << 32) | w0) >> o);
-        f.s1 = (uint32_t)((((uint64_t)w2 << 32) | w1) >> o);
+        const u32x4 a = *reinterpret_cast<const u32x4_a2*>(sb + 64 * h + 16 * ih);        // ql, low set
+        const u32x4 b = *reinterpret_cast<const u32x4_a2*>(sb + 64 * h + 32 + 16 * ih);   // ql, high set
+        const u32x4 c = *reinterpret_cast<const u32x4_a2*>(sb + 128 + 32 * h + 16 * ih);  // qh
+        const u32x2 sc = *reinterpret_cast<const u32x2_a2*>(sb + 192 + 8 * h);           // scales[8h, 8h+8)
+        f.wa[0] = a.x; f.wa[1] = a.y; f.wa[2] = a.z; f.wa[3] = a.w;
+        f.wb[0] = b.x; f.wb[1] = b.y; f.wb[2] = b.z; f.wb[3] = b.w;
+        f.u[0] = c.x; f.u[1] = c.y; f.u[2] = c.z; f.u[3] = c.w;
+        f.s0 = sc.x;
+        f.s1 = sc.y;
         f.dbits = *reinterpret_cast<const uint16_t*>(sb + 208);
         return f;
     }
