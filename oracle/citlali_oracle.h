@@ -24,8 +24,14 @@
  *   orc_attention            -- L = 1 (out = V[0]), q = 0 (mean of V),
  *                               GQA head equality, numpy softmax on small
  *                               shapes.
- *   orc_rms_norm / orc_rope / orc_swiglu / orc_forward -- see the tests;
- *                               the forward composes the pinned pieces.
+ *   orc_embed_q6k            -- numpy's nearest-even cast of the f32 row.
+ *   orc_rms_norm(_heads), orc_rope, orc_swiglu, orc_add_inplace,
+ *   orc_store_kv, orc_argmax -- known answers, closed forms (unit vectors,
+ *                               one-hot rotations, silu(0)), numpy fp32
+ *                               adds, tie / NaN rules (test_oracle_forward).
+ *   orc_forward_token        -- composition of the pinned pieces; zeroed
+ *                               residual branches, an inert second layer
+ *                               and cache dependence (tests/cpp, cpu mode).
  */
 #ifndef CITLALI_ORACLE_H
 #define CITLALI_ORACLE_H
