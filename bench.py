@@ -5,7 +5,11 @@ Workload: one Qwen3-8B decoder layer of single-token
 decode through the hot path -- attn_q/attn_k Q4_K, attn_v Q6_K, GQA attention
 (32 query / 8 kv heads, head_dim 128) over an fp16 KV cache of 8192
 positions, attn_o Q4_K, ffn_gate/ffn_up Q4_K 12288x4096, ffn_down Q6_K
-4096x12288.  A step is one such layer; steps rotate over LAYERS distinct
+4096x12288.  A step is one such layer, launched as QwenModel::forward_token
+launches it: attn_q/k/v as one grouped GEMV launch, attention (split and
+merge), attn_o, ffn_gate/ffn_up with SwiGLU in one launch, ffn_down (the
+norms, RoPE and residual adds between them are not part of the step).
+Steps rotate over LAYERS distinct
 copies of weights and caches (>= 512 MB in total) so every byte comes from
 HBM, not the 256 MB Infinity Cache.  Inputs are synthetic (seeded random
 quant blocks with d, dmin in [1e-3, 1e-2]; N(0,1) fp16 activations/caches)
@@ -50,13 +54,13 @@ GEMVS = [
     ("ffn_up", "q4k", FFN, HIDDEN, "x", "up"),
     ("ffn_down", "q6k", HIDDEN, FFN, "up", "down"),
 ]
-ORDER = ["attn_q", "attn_k", "attn_v", "attention", "attn_o", "ffn_gate", "ffn_up", "ffn_down"]
+# the step's launches, as QwenModel::forward_token issues them for one layer
+ORDER = ["attn_qkv", "attention", "attn_o", "ffn_gate_up", "ffn_down"]
 SB_BYTES = {"q4k": 144, "q6k": 210}
 
 
-def gemv_bytes(kind, rows, cols):
-    """Algorithmic bytes: weights once, x once, y once (fp16)."""
-    return rows * (cols // 256) * SB_BYTES[kind] + cols * 2 + rows * 2
+def weight_bytes(kind, rows, cols):
+    return rows * (cols // 256) * SB_BYTES[kind]
 
 
 def attention_bytes(L):
@@ -64,9 +68,17 @@ def attention_bytes(L):
 
 
 def kernel_bytes():
-    b = {n: gemv_bytes(k, r, c) for n, k, r, c, _, _ in GEMVS}
-    b["attention"] = attention_bytes(CTX)
-    return b
+    """Algorithmic bytes per launch: every weight byte once, the shared input
+    once, each output once (fp16)."""
+    spec = {n: (k, r, c) for n, k, r, c, _, _ in GEMVS}
+    wb = {n: weight_bytes(*spec[n]) for n in spec}
+    return {
+        "attn_qkv": wb["attn_q"] + wb["attn_k"] + wb["attn_v"] + HIDDEN * 2 + (HEADS + 2 * KV_HEADS) * HEAD_DIM * 2,
+        "attention": attention_bytes(CTX),
+        "attn_o": wb["attn_o"] + HEADS * HEAD_DIM * 2 + HIDDEN * 2,
+        "ffn_gate_up": wb["ffn_gate"] + wb["ffn_up"] + HIDDEN * 2 + FFN * 2,
+        "ffn_down": wb["ffn_down"] + FFN * 2 + HIDDEN * 2,
+    }
 
 
 class Layer:
@@ -93,15 +105,23 @@ def run_gpu(args):
     layers = [Layer(hip, host) for _ in range(LAYERS)]
     act = {"x": hip.DeviceArray.from_numpy(host["x"])}
     for name, size in (("q", HEADS * HEAD_DIM), ("k", KV_HEADS * HEAD_DIM), ("v", KV_HEADS * HEAD_DIM),
-                       ("att", HEADS * HEAD_DIM), ("o", HIDDEN), ("gate", FFN), ("up", FFN), ("down", HIDDEN)):
+                       ("att", HEADS * HEAD_DIM), ("o", HIDDEN), ("up", FFN), ("down", HIDDEN)):
         act[name] = hip.DeviceArray(size * 2)
     scores = hip.DeviceArray(HEADS * CTX * 4)
     spec = {n: (k, r, c, i, o) for n, k, r, c, i, o in GEMVS}
+    qkv = ["attn_q", "attn_k", "attn_v"]
 
     def launch(name, layer):
-        if name == "attention":
+        if name == "attn_qkv":
+            hip.device.matvec_group([spec[n][0] for n in qkv], [layer.w[n] for n in qkv], act["x"],
+                                    [act[spec[n][4]] for n in qkv], [spec[n][1] for n in qkv], HIDDEN)
+        elif name == "attention":
             hip.device.attention(act["q"], layer.kc, layer.vc, scores, act["att"], CTX - 1, CTX, HEADS, KV_HEADS,
                                  HEAD_DIM)
+        elif name == "ffn_gate_up":
+            # gate and up GEMVs with SwiGLU; the activation feeds ffn_down
+            hip.device.matvec_gate_up_swiglu("q4k", layer.w["ffn_gate"], layer.w["ffn_up"], act["x"], act["up"],
+                                             HIDDEN, FFN)
         else:
             k, r, c, i, o = spec[name]
             hip.device.matvec(k, layer.w[name], act[i], act[o], c, r)
@@ -265,8 +285,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {"workload": "BASELINE config 3: Qwen3-8B one-layer decode (7 Q4_K/Q6_K fused GEMVs + "
-                               "32/8-head attention, head_dim 128, L=8192)",
+        "config": {"workload": "BASELINE config 3: Qwen3-8B one-layer decode (7 Q4_K/Q6_K fused-dequant GEMVs in "
+                               "4 launches -- q/k/v grouped, gate/up with SwiGLU -- + 32/8-head attention, "
+                               "head_dim 128, L=8192)",
                    "layers_rotated": LAYERS, "bytes_per_step": step_bytes,
                    "layer_tok_per_s_equiv": round(1000.0 / ms_step, 1)},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,

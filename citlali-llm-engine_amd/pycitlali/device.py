@@ -222,3 +222,13 @@ def qk_norm_rope_store(q, k, v, q_norm, k_norm, heads: int, kv_heads: int, head_
 def matvec_gate_up_swiglu(kind: str, w_gate, w_up, x, act, in_features: int, out_features: int) -> None:
     _lib.call("citlali_hip_matvec_gate_up_swiglu", 12 if kind == "q4k" else 14, _vp(w_gate), _vp(w_up), _vp(x),
               _vp(act), int(in_features), int(out_features))
+
+
+def matvec_group(kinds, weights, x, outputs, out_features, in_features: int) -> None:
+    """One launch of up to three Q4_K/Q6_K GEMVs that read `x`."""
+    n = len(kinds)
+    types = (ctypes.c_int * n)(*[12 if k == "q4k" else 14 for k in kinds])
+    ws = (ctypes.c_void_p * n)(*[w.ptr for w in weights])
+    ys = (ctypes.c_void_p * n)(*[y.ptr for y in outputs])
+    rows = (ctypes.c_int * n)(*[int(r) for r in out_features])
+    _lib.call("citlali_hip_matvec_group", n, types, ws, _vp(x), ys, rows, int(in_features))

@@ -176,6 +176,17 @@ int citlali_hip_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_
  * 4096 or 8192 -- then use the separate launches. */
 int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up, const uint16_t* x,
                                       uint16_t* act, int in_features, int out_features);
+/* LinearBackend::forward (linear_backend.cpp:17-61) for `count` (1..3)
+ * KeepQuantized weights that read the same input -- attn_q, attn_k and
+ * attn_v of one layer (qwen_model.cpp:315-321) -- in one launch.
+ * gguf_types[i] is 12 = Q4_K or 14 = Q6_K, outputs[i] receives
+ * out_features[i] fp16 values: the results of the separate
+ * citlali_hip_matvec_q4k / _q6k calls bit for bit.  Outputs must not overlap
+ * each other or x.  Returns CITLALI_ERR_UNSUPPORTED, launching nothing, for
+ * in_features other than 4096, 8192, 12288 or 16384 -- then use the
+ * separate launches. */
+int citlali_hip_matvec_group(int count, const int* gguf_types, const uint8_t* const* weights, const uint16_t* x,
+                             uint16_t* const* outputs, const int* out_features, int in_features);
 
 /* Kernel timing (no reference counterpart; for benchmarks): while armed with
  * two events of citlali_hip_event_create, the first kernel the calling thread

@@ -73,6 +73,30 @@ def test_matvec_validation(fn):
     assert st == 1 and "aligned" in msg
 
 
+def test_matvec_group_validation():
+    fake = P(0x10000)
+    ints = lambda *v: (ctypes.c_int * len(v))(*v)
+    ptrs = lambda *v: (ctypes.c_void_p * len(v))(*v)
+    g = lambda n, types, ws, ys, rows, k: _status("citlali_hip_matvec_group", n, types, ws, fake, ys, rows, k)
+    st, msg = g(0, ints(12), ptrs(0x10000), ptrs(0x10000), ints(4), 4096)
+    assert st == 1 and "count" in msg
+    st, msg = g(4, ints(12, 12, 12, 12), ptrs(*[0x10000] * 4), ptrs(*[0x10000] * 4), ints(4, 4, 4, 4), 4096)
+    assert st == 1 and "count" in msg
+    st, msg = g(2, ints(12, 10), ptrs(0x10000, 0x10000), ptrs(0x10000, 0x10000), ints(4, 4), 4096)
+    assert st == 1 and "not Q4_K or Q6_K" in msg
+    st, msg = g(2, ints(12, 14), ptrs(0x10000, 0), ptrs(0x10000, 0x10000), ints(4, 4), 4096)
+    assert st == 1 and "null buffer" in msg
+    st, msg = g(1, ints(12), ptrs(0x10004), ptrs(0x10000), ints(4), 4096)
+    assert st == 1 and "aligned" in msg
+    st, msg = g(3, ints(14, 14, 14), ptrs(*[0x10000] * 3), ptrs(*[0x10000] * 3), ints(2 ** 30, 2 ** 30, 2 ** 30),
+                4096)
+    assert st == 1 and "INT_MAX" in msg
+    st, msg = g(1, ints(14), ptrs(0x10000), ptrs(0x10000), ints(4), 2048)
+    assert st == 2 and "no grouped kernel" in msg
+    st, msg = _status("citlali_hip_matvec_group", 1, None, ptrs(0x10000), fake, ptrs(0x10000), ints(4), 4096)
+    assert st == 1 and "null array" in msg
+
+
 def test_attention_validation():
     fake = P(0x10000)
     st, msg = _status("citlali_hip_attention", fake, fake, fake, fake, fake, 5, 5, 16, 8, 128)

@@ -30,6 +30,13 @@ SHAPES = [
     ("q6k", 1, 256),
     ("q4k", 37, 768),        # ragged rows, nb = 3
     ("q6k", 37, 768),
+    # K = 4096 launch shapes: one pass with one / two rows per wave (<= 1024,
+    # <= 4096 rows), streaming with one / two rows in flight (more rows)
+    ("q4k", 7, 4096),
+    ("q6k", 2500, 4096),
+    ("q6k", 5000, 4096),
+    ("q4k", 8192, 4096),
+    ("q4k", 1030, 8192),     # nb = 32
     ("q6k", 3, 28672),       # the largest in_features the ABI takes
     ("q4k", 5, 28672),
 ]

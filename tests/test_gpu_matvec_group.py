@@ -1,0 +1,93 @@
+"""GPU parity of citlali_hip_matvec_group: attn_q, attn_k and attn_v of one
+layer (qwen_model.cpp:315-321, each a LinearBackend::forward of
+linear_backend.cpp:17-61) in one launch.  Every output must equal the
+separate matvec_q4k / matvec_q6k launch bit for bit (same lane mapping and
+summation order), and one case is also held to the north-star bar against
+the oracle's fp32 restatement."""
+import numpy as np
+import pytest
+
+from conftest import tol_ok
+
+pytestmark = pytest.mark.gpu
+H = np.float16
+
+
+def up(hip, a):
+    return hip.DeviceArray.from_numpy(np.ascontiguousarray(a))
+
+
+def run_group(hip, kinds, rows, k, seed):
+    rng = hip.synth.Rng(seed)
+    ws = [hip.synth.quant_matrix(kd, rng, n, k) for kd, n in zip(kinds, rows)]
+    x = hip.synth.normal_f16(rng, k)
+    dws, dx = [up(hip, w) for w in ws], up(hip, x)
+    sep = [hip.DeviceArray(n * 2) for n in rows]
+    for kd, dw, y, n in zip(kinds, dws, sep, rows):
+        hip.device.matvec(kd, dw, dx, y, k, n)
+    grp = [hip.DeviceArray(n * 2) for n in rows]
+    hip.device.matvec_group(kinds, dws, dx, grp, rows, k)
+    got = [g.download(np.uint16, n) for g, n in zip(grp, rows)]
+    ref = [s.download(np.uint16, n) for s, n in zip(sep, rows)]
+    return ws, x, got, ref
+
+
+CASES = [
+    # Qwen3-8B attn_q / attn_k Q4_K, attn_v Q6_K
+    (("q4k", "q4k", "q6k"), (4096, 1024, 1024), 4096),
+    # one type only, three matrices (one row set)
+    (("q4k", "q4k", "q4k"), (2048, 512, 512), 4096),
+    (("q6k", "q6k", "q6k"), (1024, 256, 256), 8192),
+    # Q6_K first, ragged row counts, every streamed length
+    (("q6k", "q4k", "q4k"), (1000, 7, 3), 4096),
+    (("q4k", "q6k", "q4k"), (513, 1, 130), 8192),
+    (("q4k", "q6k", "q6k"), (96, 64, 33), 12288),
+    (("q6k", "q4k", "q6k"), (200, 100, 5), 16384),
+    (("q6k", "q6k"), (300, 2), 16384),
+    # more rows than one pass covers: the streaming split of the workgroups
+    (("q4k", "q4k", "q6k"), (8192, 1024, 1024), 4096),
+    (("q6k", "q6k", "q4k"), (4000, 4000, 4000), 4096),
+    # fewer than three matrices
+    (("q4k",), (4096,), 4096),
+    (("q6k", "q4k"), (1024, 4096), 4096),
+    (("q4k", "q6k"), (1, 1), 4096),
+]
+
+
+@pytest.mark.parametrize("kinds,rows,k", CASES)
+def test_group_equals_separate_launches(hip, kinds, rows, k):
+    _, _, got, ref = run_group(hip, kinds, rows, k, seed=sum(rows) + k)
+    for g, r in zip(got, ref):
+        assert np.array_equal(g, r)
+
+
+def test_group_qwen3_8b_against_oracle(hip, orc):
+    kinds, rows, k = ("q4k", "q4k", "q6k"), (4096, 1024, 1024), 4096
+    ws, x, got, _ = run_group(hip, kinds, rows, k, seed=77)
+    for kd, w, g, n in zip(kinds, ws, got, rows):
+        ref = orc.matvec(kd, w, x, k, n)
+        assert tol_ok(g.view(H).astype(np.float64), ref).all()
+
+
+@pytest.mark.parametrize("k", [2048, 20480])
+def test_group_declines_other_lengths_without_writing(hip, k):
+    n = 64
+    rng = hip.synth.Rng(5)
+    w = up(hip, hip.synth.quant_matrix("q4k", rng, n, k))
+    x = up(hip, hip.synth.normal_f16(rng, k))
+    y = up(hip, np.full(n, 0x3c00, np.uint16))
+    with pytest.raises(hip.CitlaliError, match="no grouped kernel"):
+        hip.device.matvec_group(["q4k"], [w], x, [y], [n], k)
+    assert (y.download(np.uint16, n) == 0x3c00).all()
+
+
+def test_group_rejects_bad_arguments(hip):
+    d = hip.DeviceArray(1 << 20)
+    with pytest.raises(hip.CitlaliError, match="count"):
+        hip.device.matvec_group([], [], d, [], [], 4096)
+    with pytest.raises(hip.CitlaliError, match="count"):
+        hip.device.matvec_group(["q4k"] * 4, [d] * 4, d, [d] * 4, [1] * 4, 4096)
+    with pytest.raises(hip.CitlaliError, match="multiple of the 256"):
+        hip.device.matvec_group(["q4k"], [d], d, [d], [8], 4000)
+    with pytest.raises(hip.CitlaliError, match="must be positive"):
+        hip.device.matvec_group(["q4k", "q6k"], [d, d], d, [d, d], [8, 0], 4096)
