@@ -209,7 +209,7 @@ CITLALI_EXPORT int citlali_hip_embed_q6k(const uint8_t* table, int32_t token_id,
     REQUIRE(table && out, "embed_q6k received a null buffer");
     REQUIRE(token_id >= 0, "token id out of vocab range");
     REQUIRE(hidden > 0 && hidden % 256 == 0, "embed_q6k: hidden (%d) must be a positive multiple of 256", hidden);
-    HIP_TRY(launch_embed_q6k(table, token_id, out, hidden, g_stream));
+    HIP_TRY(launch_embed_q6k(table, token_id, nullptr, 0, out, hidden, g_stream));
     return CITLALI_OK;
 }
 
@@ -246,7 +246,10 @@ CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_ca
     a.kv_heads = kv_heads;
     a.head_dim = head_dim;
     a.out = out;
-    const AttnPlan p = plan_attention(position + 1, 1, kv_heads, heads, head_dim, kAttnTargetBlocks);
+    // planned for the length's bucket, so every step of a bucket launches the
+    // same kernels (as a captured step with the position in device memory)
+    const AttnPlan p = plan_attention(attention_plan_length(position + 1, max_context), 1, kv_heads, heads, head_dim,
+                                      kAttnTargetBlocks);
     const size_t need = attention_workspace_bytes(p, 1, heads, head_dim);
     const size_t have = scores ? (size_t)heads * (size_t)max_context * sizeof(float) : 0;
     if (need == 0) {
@@ -259,6 +262,11 @@ CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_ca
     }
     HIP_TRY(launch_attention(a, p, g_stream));
     return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_attention_plan_length(int length, int max_context) {
+    if (length <= 0 || max_context < length) return 0;
+    return attention_plan_length(length, max_context);
 }
 
 CITLALI_EXPORT size_t citlali_hip_attention_workspace_bytes(int max_positions_bound, int nseq, int heads,
@@ -350,7 +358,7 @@ CITLALI_EXPORT int citlali_hip_dequant_q6k_f16(const uint8_t* w, uint64_t count,
 CITLALI_EXPORT int citlali_hip_embed(const uint16_t* table, int32_t token_id, uint16_t* out, int hidden) {
     REQUIRE(table && out, "embed received a null buffer");
     REQUIRE(token_id >= 0 && hidden > 0, "embed: bad token id or hidden size");
-    HIP_TRY(launch_embed_f16(table, token_id, out, hidden, g_stream));
+    HIP_TRY(launch_embed_f16(table, token_id, nullptr, 0, out, hidden, g_stream));
     return CITLALI_OK;
 }
 
@@ -414,7 +422,33 @@ CITLALI_EXPORT int citlali_hip_rope(uint16_t* data, int heads, int head_dim, int
 
 CITLALI_EXPORT int citlali_hip_argmax(const float* logits, int n, int32_t* out_index) {
     REQUIRE(logits && out_index && n > 0, "argmax: bad arguments");
-    HIP_TRY(launch_argmax(logits, n, out_index, g_stream));
+    HIP_TRY(launch_argmax(logits, n, out_index, nullptr, nullptr, 0, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_argmax_advance(const float* logits, int n, int32_t* state, int32_t* tokens,
+                                              int capacity) {
+    REQUIRE(logits && state && n > 0, "argmax_advance: bad arguments");
+    REQUIRE(capacity >= 0 && (capacity == 0 || tokens), "argmax_advance: bad token array");
+    REQUIRE(aligned(state, 16), "argmax_advance: state must be 16-byte aligned");
+    HIP_TRY(launch_argmax(logits, n, nullptr, state, tokens, capacity, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_embed_q6k_at(const uint8_t* table, const int32_t* token, int vocab, uint16_t* out,
+                                            int hidden) {
+    REQUIRE(table && token && out, "embed_q6k_at received a null buffer");
+    REQUIRE(vocab > 0, "embed_q6k_at: vocab must be positive");
+    REQUIRE(hidden > 0 && hidden % 256 == 0, "embed_q6k_at: hidden (%d) must be a positive multiple of 256", hidden);
+    HIP_TRY(launch_embed_q6k(table, 0, token, vocab, out, hidden, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_embed_at(const uint16_t* table, const int32_t* token, int vocab, uint16_t* out,
+                                        int hidden) {
+    REQUIRE(table && token && out, "embed_at received a null buffer");
+    REQUIRE(vocab > 0 && hidden > 0, "embed_at: bad vocab or hidden size");
+    HIP_TRY(launch_embed_f16(table, 0, token, vocab, out, hidden, g_stream));
     return CITLALI_OK;
 }
 
@@ -440,8 +474,71 @@ CITLALI_EXPORT int citlali_hip_qk_norm_rope_store(uint16_t* q, const uint16_t* k
     REQUIRE(heads > 0 && kv_heads > 0 && position >= 0, "qk_norm_rope_store: bad heads or position");
     REQUIRE(head_dim > 0 && head_dim <= 128 && head_dim % 2 == 0, "qk_norm_rope_store: head_dim %d not supported",
             head_dim);
-    HIP_TRY(launch_qk_norm_rope_store(q, k, v, q_norm, k_norm, heads, kv_heads, head_dim, position, theta, eps,
-                                      k_cache, v_cache, g_stream));
+    HIP_TRY(launch_qk_norm_rope_store(q, k, v, q_norm, k_norm, heads, kv_heads, head_dim, position, nullptr, INT_MAX,
+                                      theta, eps, k_cache, v_cache, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_qk_norm_rope_store_at(uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                                     const uint16_t* q_norm, const uint16_t* k_norm, int heads,
+                                                     int kv_heads, int head_dim, const int32_t* position,
+                                                     int max_positions, float theta, float eps, uint16_t* k_cache,
+                                                     uint16_t* v_cache) {
+    REQUIRE(q && k && v && k_cache && v_cache && position, "qk_norm_rope_store_at received a null buffer");
+    REQUIRE(heads > 0 && kv_heads > 0 && max_positions > 0, "qk_norm_rope_store_at: bad heads or max_positions");
+    REQUIRE(head_dim > 0 && head_dim <= 128 && head_dim % 2 == 0,
+            "qk_norm_rope_store_at: head_dim %d not supported", head_dim);
+    HIP_TRY(launch_qk_norm_rope_store(q, k, v, q_norm, k_norm, heads, kv_heads, head_dim, 0, position,
+                                      max_positions, theta, eps, k_cache, v_cache, g_stream));
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- streams and graphs
+CITLALI_EXPORT int citlali_hip_stream_create(void** stream) {
+    REQUIRE(stream, "null output pointer");
+    hipStream_t st = nullptr;
+    HIP_TRY(hipStreamCreate(&st));
+    *stream = st;
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_stream_destroy(void* stream) {
+    REQUIRE(stream, "stream_destroy: null stream");
+    REQUIRE(stream != g_stream, "stream_destroy: the stream is the library stream");
+    HIP_TRY(hipStreamDestroy(static_cast<hipStream_t>(stream)));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_graph_begin(void) {
+    REQUIRE(g_stream != nullptr, "graph_begin: capture needs a library stream other than the null stream");
+    REQUIRE(kernel_timing().start == nullptr, "graph_begin: kernel timing is armed");
+    HIP_TRY(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_graph_end(void** graph) {
+    REQUIRE(graph, "null output pointer");
+    *graph = nullptr;
+    REQUIRE(g_stream != nullptr, "graph_end: no capture on the null stream");
+    hipGraph_t g = nullptr;
+    HIP_TRY(hipStreamEndCapture(g_stream, &g));   // ends the capture even when it failed
+    hipGraphExec_t exec = nullptr;
+    const hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    HIP_TRY(e);
+    *graph = exec;
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_graph_launch(void* graph) {
+    REQUIRE(graph, "graph_launch: null graph");
+    HIP_TRY(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_graph_destroy(void* graph) {
+    REQUIRE(graph, "graph_destroy: null graph");
+    HIP_TRY(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)));
     return CITLALI_OK;
 }
 

@@ -10,7 +10,10 @@
 // matrix at rms ~ gain/sqrt(in) (random Q4_K codes give rms ~ 300 d, Q6_K
 // ~ 1366 d); `--distinct N` fills N distinct layer byte sets and gives every
 // one of the 36 layers its own device copy, so each layer reads its own
-// weights from HBM.  Prints one JSON line.
+// weights from HBM.  The greedy steps run twice: as the reference's loop of
+// forward_token calls, then through QwenModel::decode_greedy (each step
+// replayed from a captured HIP graph); both must give the same tokens.
+// Prints one JSON line.
 //
 // usage: decode_qwen3 [--layers 36] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1]
 #include "citlali/common.h"
@@ -181,20 +184,35 @@ int main(int argc, char** argv) {
         for (int i = 0; i < prompt; ++i) next = m.forward_token(ids[i], pos++, i == prompt - 1);
         citlali_hip_event_record(e1);
         const auto p1 = std::chrono::steady_clock::now();
-        // greedy decode
-        uint64_t checksum = 0;
+        // greedy decode, one forward_token per step (the reference's loop)
+        const int32_t first = next;
+        const uint32_t first_pos = pos;
+        std::vector<int32_t> eager;
         for (int i = 0; i < steps; ++i) {
             next = m.forward_token(next, pos++);
-            checksum = checksum * 1000003ull + (uint64_t)next;
+            eager.push_back(next);
         }
         citlali_hip_event_record(e2);
         citlali_hip_event_synchronize(e2);
         const auto p2 = std::chrono::steady_clock::now();
-        float prompt_ms = 0, decode_ms = 0;
+        float prompt_ms = 0, eager_ms = 0;
         citlali_hip_event_elapsed_ms(e0, e1, &prompt_ms);
-        citlali_hip_event_elapsed_ms(e1, e2, &decode_ms);
-        const double decode_wall = std::chrono::duration<double>(p2 - p1).count();
+        citlali_hip_event_elapsed_ms(e1, e2, &eager_ms);
+        const double eager_wall = std::chrono::duration<double>(p2 - p1).count();
         const double prompt_wall = std::chrono::duration<double>(p1 - p0).count();
+        // the same steps again through decode_greedy (each step replayed from
+        // a captured graph, no host synchronisation between steps): the first
+        // call captures the graphs, the second is timed, wall clock around
+        // the whole call including the copy of the tokens
+        const std::vector<int32_t> warm = m.decode_greedy(first, first_pos, (uint32_t)steps);
+        const auto g0 = std::chrono::steady_clock::now();
+        const std::vector<int32_t> graph = m.decode_greedy(first, first_pos, (uint32_t)steps);
+        const auto g1 = std::chrono::steady_clock::now();
+        const double graph_wall = std::chrono::duration<double>(g1 - g0).count();
+        const bool match = graph == eager && warm == eager;
+        uint64_t checksum = 0;
+        for (int32_t t : graph) checksum = checksum * 1000003ull + (uint64_t)t;
+        const double decode_ms = graph_wall * 1e3;
         // bytes one decode step must read: every weight once, the KV cache
         // up to the position, the embedding row and the logits
         const double layer_bytes = 9437184.0 * 2 + 2359296 + 3440640 + 28311552.0 * 2 + 41287680;
@@ -203,12 +221,19 @@ int main(int argc, char** argv) {
                                   (double)layers * 2 * 2 * NKV * mean_len;
         std::printf("{\"workload\": \"BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode\", \"layers\": %d, "
                     "\"distinct_layer_weight_sets\": %d, \"prompt\": %d, \"steps\": %d, \"decode_tok_per_s\": %.2f, "
-                    "\"decode_ms_per_token\": %.4f, \"decode_ms_per_token_wall\": %.4f, \"prompt_tok_per_s\": %.2f, "
-                    "\"prompt_ms_per_token_wall\": %.4f, \"decode_GBps\": %.1f, \"setup_s\": %.1f, "
-                    "\"token_checksum\": %llu}\n",
+                    "\"decode_ms_per_token\": %.4f, \"decode_mode\": \"QwenModel::decode_greedy (graph replay), "
+                    "wall clock\", \"decode_GBps\": %.1f, \"decode_tok_per_s_forward_token\": %.2f, "
+                    "\"decode_ms_per_token_forward_token\": %.4f, \"decode_ms_per_token_forward_token_wall\": %.4f, "
+                    "\"graph_tokens_equal_forward_token\": %s, \"prompt_tok_per_s\": %.2f, "
+                    "\"prompt_ms_per_token_wall\": %.4f, \"setup_s\": %.1f, \"token_checksum\": %llu}\n",
                     layers, distinct, prompt, steps, steps / (decode_ms * 1e-3), decode_ms / steps,
-                    decode_wall * 1e3 / steps, prompt / (prompt_ms * 1e-3), prompt_wall * 1e3 / prompt,
-                    step_bytes / (decode_ms * 1e-3 / steps) / 1e9, setup_s, (unsigned long long)checksum);
+                    step_bytes / (decode_ms * 1e-3 / steps) / 1e9, steps / (eager_ms * 1e-3), eager_ms / steps,
+                    eager_wall * 1e3 / steps, match ? "true" : "false", prompt / (prompt_ms * 1e-3),
+                    prompt_wall * 1e3 / prompt, setup_s, (unsigned long long)checksum);
+        if (!match) {
+            std::fprintf(stderr, "decode_qwen3: decode_greedy tokens differ from the forward_token loop\n");
+            return 1;
+        }
         citlali_hip_event_destroy(e0);
         citlali_hip_event_destroy(e1);
         citlali_hip_event_destroy(e2);

@@ -67,4 +67,34 @@ void launch_argmax(const float* logits, int n, int32_t* out_index);
 // Waits for every launch queued on the library stream.
 void synchronize();
 
+// ---- replayable decode steps (no reference counterpart) -------------------
+// The same launches with the token / position read from device memory
+// (decode state int32 {token, position, step, 0}), so one decode step can be
+// captured in a HIP graph and replayed per token; each gives the result of
+// its scalar form at the values it reads.
+void launch_embed_q6k_at(const uint8_t* embedding, const int32_t* token, int vocab, uint16_t* output, int hidden);
+void launch_embed_at(const uint16_t* embedding, const int32_t* token, int vocab, uint16_t* output, int hidden);
+void launch_qk_norm_rope_store_at(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                                  const uint16_t* k_norm, int heads, int kv_heads, int head_dim,
+                                  const int32_t* position, int max_positions, float theta, float eps,
+                                  uint16_t* k_cache, uint16_t* v_cache);
+// launch_attention at the position in device memory, for every position p
+// with attention_plan_length(p + 1, max_context) == plan_length.
+void launch_attention_at(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                         const int32_t* position, int plan_length, float* workspace, std::size_t workspace_bytes,
+                         uint16_t* output, int heads, int kv_heads, int head_dim);
+int attention_plan_length(int length, int max_context);
+// launch_argmax, then tokens[step] = pick, token = pick, position += 1, step += 1
+void launch_argmax_advance(const float* logits, int n, int32_t* state, int32_t* tokens, int capacity);
+
+// Library stream and graphs (see citlali_hip_graph_begin).
+void* create_stream();
+void destroy_stream(void* stream) noexcept;
+void* current_stream();
+void set_stream(void* stream);
+void graph_begin();
+void* graph_end();   // ends the capture; throws when it failed
+void graph_launch(void* graph);
+void graph_destroy(void* graph) noexcept;
+
 }  // namespace citlali::compute

@@ -16,6 +16,7 @@
 
 #include <cstdint>
 #include <memory>
+#include <utility>
 #include <vector>
 
 namespace citlali::model {
@@ -48,12 +49,22 @@ struct QwenWeights {
 class QwenModel {
 public:
     QwenModel() = default;
+    ~QwenModel();
+    QwenModel(const QwenModel&) = delete;
+    QwenModel& operator=(const QwenModel&) = delete;
 
     // max_context 0 -> min(context_length, 2048), as the reference.
     void load(const QwenConfig& config, QwenWeights weights, uint32_t max_context = 0);
     // Runs one token at `position`; returns the greedy next token, or -1
     // when compute_logits is false.
     int32_t forward_token(int32_t token_id, uint32_t position, bool compute_logits = true);
+    // `steps` greedy tokens after token_id at `position`: the tokens that
+    // forward_token would return one call at a time, bit for bit, but with
+    // each step replayed from a HIP graph (one per attention plan length) on
+    // a stream of the model's own and no host synchronisation between steps.
+    // Needs position + steps <= max_context.  No reference counterpart (the
+    // reference's caller loops over forward_token).
+    std::vector<int32_t> decode_greedy(int32_t token_id, uint32_t position, uint32_t steps);
     void synchronize() const;
 
     const QwenConfig& config() const { return config_; }
@@ -64,6 +75,9 @@ public:
 private:
     void allocate_runtime_buffers();
     bool launch_qkv_grouped(const QwenLayerWeights& layer, int hidden);
+    void enqueue_token(int32_t token_id, int position, int32_t* state, int plan_length, bool compute_logits);
+    void* step_graph(int plan_length);
+    void release_graphs() noexcept;
     int32_t sample_greedy_from_logits();
 
     QwenConfig config_;
@@ -75,7 +89,10 @@ private:
 
     compute::DeviceBufferPtr x_, norm_, q_, k_, v_, attn_out_, attn_proj_;
     compute::DeviceBufferPtr gate_, up_, ff_act_, ff_out_, logits_, scores_, next_token_;
+    compute::DeviceBufferPtr state_, tokens_;   // decode_greedy: {token, position, step, 0}, picks
     std::unique_ptr<LinearBackend> linear_backend_;
+    void* stream_ = nullptr;                                  // decode_greedy's stream
+    std::vector<std::pair<int, void*>> graphs_;               // plan length -> captured step
 };
 
 }  // namespace citlali::model

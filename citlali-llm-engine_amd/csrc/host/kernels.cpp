@@ -124,4 +124,65 @@ void launch_argmax(const float* logits, int n, int32_t* out_index) {
 
 void synchronize() { CITLALI_HIP_CHECK(citlali_hip_synchronize()); }
 
+void launch_embed_q6k_at(const uint8_t* embedding, const int32_t* token, int vocab, uint16_t* output, int hidden) {
+    CITLALI_HIP_CHECK(citlali_hip_embed_q6k_at(embedding, token, vocab, output, hidden));
+}
+
+void launch_embed_at(const uint16_t* embedding, const int32_t* token, int vocab, uint16_t* output, int hidden) {
+    CITLALI_HIP_CHECK(citlali_hip_embed_at(embedding, token, vocab, output, hidden));
+}
+
+void launch_qk_norm_rope_store_at(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                                  const uint16_t* k_norm, int heads, int kv_heads, int head_dim,
+                                  const int32_t* position, int max_positions, float theta, float eps,
+                                  uint16_t* k_cache, uint16_t* v_cache) {
+    CITLALI_HIP_CHECK(citlali_hip_qk_norm_rope_store_at(q, k, v, q_norm, k_norm, heads, kv_heads, head_dim, position,
+                                                        max_positions, theta, eps, k_cache, v_cache));
+}
+
+void launch_attention_at(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                         const int32_t* position, int plan_length, float* workspace, std::size_t workspace_bytes,
+                         uint16_t* output, int heads, int kv_heads, int head_dim) {
+    CITLALI_HIP_CHECK(citlali_hip_attention_batched(q, k_cache, v_cache, 0, position, plan_length, 1, heads, kv_heads,
+                                                    head_dim, workspace, workspace_bytes, output));
+}
+
+int attention_plan_length(int length, int max_context) {
+    const int n = citlali_hip_attention_plan_length(length, max_context);
+    require(n > 0, "attention_plan_length: length outside [1, max_context]");
+    return n;
+}
+
+void launch_argmax_advance(const float* logits, int n, int32_t* state, int32_t* tokens, int capacity) {
+    CITLALI_HIP_CHECK(citlali_hip_argmax_advance(logits, n, state, tokens, capacity));
+}
+
+void* create_stream() {
+    void* s = nullptr;
+    CITLALI_HIP_CHECK(citlali_hip_stream_create(&s));
+    return s;
+}
+
+void destroy_stream(void* stream) noexcept {
+    if (stream) (void)citlali_hip_stream_destroy(stream);
+}
+
+void* current_stream() { return citlali_hip_get_stream(); }
+
+void set_stream(void* stream) { CITLALI_HIP_CHECK(citlali_hip_set_stream(stream)); }
+
+void graph_begin() { CITLALI_HIP_CHECK(citlali_hip_graph_begin()); }
+
+void* graph_end() {
+    void* g = nullptr;
+    CITLALI_HIP_CHECK(citlali_hip_graph_end(&g));
+    return g;
+}
+
+void graph_launch(void* graph) { CITLALI_HIP_CHECK(citlali_hip_graph_launch(graph)); }
+
+void graph_destroy(void* graph) noexcept {
+    if (graph) (void)citlali_hip_graph_destroy(graph);
+}
+
 }  // namespace citlali::compute

@@ -42,6 +42,7 @@ void QwenModel::load(const QwenConfig& config, QwenWeights weights, uint32_t max
     require(config_.head_count_kv > 0 && config_.head_count % config_.head_count_kv == 0,
             "attention head_count must be divisible by head_count_kv");
     linear_backend_.reset();   // set again only once everything below succeeded
+    release_graphs();          // they hold the previous buffers
 
     token_embedding_ = std::move(weights.token_embedding);
     output_norm_ = std::move(weights.output_norm);
@@ -103,6 +104,8 @@ void QwenModel::allocate_runtime_buffers() {
     logits_ = compute::make_device_buffer(static_cast<size_t>(config_.vocab_size) * sizeof(float));
     scores_ = compute::make_device_buffer(static_cast<size_t>(config_.head_count) * max_context_ * sizeof(float));
     next_token_ = compute::make_device_buffer(sizeof(int32_t));
+    state_ = compute::make_device_buffer(4 * sizeof(int32_t));
+    tokens_ = compute::make_device_buffer(static_cast<size_t>(max_context_) * sizeof(int32_t));
 }
 
 // attn_q, attn_k and attn_v in one launch when all three are Q4_K/Q6_K
@@ -133,20 +136,39 @@ int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compu
     require(linear_backend_ != nullptr, "model is not loaded");
     require(position < max_context_, "position exceeds max_context");
     require(token_id >= 0 && token_id < static_cast<int32_t>(config_.vocab_size), "token id out of vocab range");
+    enqueue_token(token_id, static_cast<int>(position), nullptr, 0, compute_logits);
+    if (!compute_logits) return -1;
+    return sample_greedy_from_logits();
+}
 
+// The launches of one token.  With `state` (device {token, position, step,
+// 0}) the token and position are read from there, attention is planned for
+// `plan_length`, and the greedy pick advances the state instead of being
+// copied back -- the same kernels and arguments otherwise, so a captured
+// step replays what forward_token computes at every position whose plan
+// length is plan_length.
+void QwenModel::enqueue_token(int32_t token_id, int pos, int32_t* state, int plan_length, bool compute_logits) {
     const int hidden = as_int(config_.embedding_length, "hidden size");
     const int head_dim = as_int(config_.head_dim, "head_dim");
     const int heads = as_int(config_.head_count, "head_count");
     const int kv_heads = as_int(config_.head_count_kv, "head_count_kv");
     const int ff = as_int(config_.feed_forward_length, "feed_forward_length");
-    const int pos = static_cast<int>(position);
+    const int vocab = as_int(config_.vocab_size, "vocab_size");
+    const int32_t* state_position = state ? state + 1 : nullptr;
 
     if (token_embedding_.storage_kind == compute::WeightStorageKind::QuantizedDevice) {
         if (token_embedding_.gguf_type != compute::GgufTensorType::Q6_K)
             throw Error("unsupported quantized embedding type");
-        compute::launch_embed_q6k(token_embedding_.device_quantized_data(), token_id, x_->half_data(), hidden);
+        if (state)
+            compute::launch_embed_q6k_at(token_embedding_.device_quantized_data(), state, vocab, x_->half_data(),
+                                         hidden);
+        else
+            compute::launch_embed_q6k(token_embedding_.device_quantized_data(), token_id, x_->half_data(), hidden);
     } else {
-        compute::launch_embed(token_embedding_.device_half_data(), token_id, x_->half_data(), hidden);
+        if (state)
+            compute::launch_embed_at(token_embedding_.device_half_data(), state, vocab, x_->half_data(), hidden);
+        else
+            compute::launch_embed(token_embedding_.device_half_data(), token_id, x_->half_data(), hidden);
     }
 
     // The reference's per-layer sequence, with three groups of its launches
@@ -168,14 +190,26 @@ int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compu
         add_bias_if_present(layer.attn_q_bias, q_, static_cast<uint64_t>(heads) * head_dim);
         add_bias_if_present(layer.attn_k_bias, k_, static_cast<uint64_t>(kv_heads) * head_dim);
         add_bias_if_present(layer.attn_v_bias, v_, static_cast<uint64_t>(kv_heads) * head_dim);
-        compute::launch_qk_norm_rope_store(
-            q_->half_data(), k_->half_data(), v_->half_data(),
-            layer.attn_q_norm.buffer ? layer.attn_q_norm.device_half_data() : nullptr,
-            layer.attn_k_norm.buffer ? layer.attn_k_norm.device_half_data() : nullptr, heads, kv_heads, head_dim, pos,
-            config_.rope_theta, config_.rms_norm_eps, layer.k_cache->half_data(), layer.v_cache->half_data());
-        compute::launch_attention(q_->half_data(), layer.k_cache->half_data(), layer.v_cache->half_data(),
-                                  static_cast<float*>(scores_->data()), attn_out_->half_data(), pos,
-                                  static_cast<int>(max_context_), heads, kv_heads, head_dim);
+        const uint16_t* q_norm = layer.attn_q_norm.buffer ? layer.attn_q_norm.device_half_data() : nullptr;
+        const uint16_t* k_norm = layer.attn_k_norm.buffer ? layer.attn_k_norm.device_half_data() : nullptr;
+        if (state) {
+            compute::launch_qk_norm_rope_store_at(q_->half_data(), k_->half_data(), v_->half_data(), q_norm, k_norm,
+                                                  heads, kv_heads, head_dim, state_position,
+                                                  static_cast<int>(max_context_), config_.rope_theta,
+                                                  config_.rms_norm_eps, layer.k_cache->half_data(),
+                                                  layer.v_cache->half_data());
+            compute::launch_attention_at(q_->half_data(), layer.k_cache->half_data(), layer.v_cache->half_data(),
+                                         state_position, plan_length, static_cast<float*>(scores_->data()),
+                                         scores_->bytes(), attn_out_->half_data(), heads, kv_heads, head_dim);
+        } else {
+            compute::launch_qk_norm_rope_store(q_->half_data(), k_->half_data(), v_->half_data(), q_norm, k_norm,
+                                               heads, kv_heads, head_dim, pos, config_.rope_theta,
+                                               config_.rms_norm_eps, layer.k_cache->half_data(),
+                                               layer.v_cache->half_data());
+            compute::launch_attention(q_->half_data(), layer.k_cache->half_data(), layer.v_cache->half_data(),
+                                      static_cast<float*>(scores_->data()), attn_out_->half_data(), pos,
+                                      static_cast<int>(max_context_), heads, kv_heads, head_dim);
+        }
         linear_backend_->forward(layer.attn_o, attn_out_, attn_proj_);
         add_bias_if_present(layer.attn_o_bias, attn_proj_, hidden);
         compute::launch_add_rms_norm(x_->half_data(), attn_proj_->half_data(), layer.ffn_norm.device_half_data(),
@@ -209,12 +243,11 @@ int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compu
             normed = false;
         }
     }
-    if (!compute_logits) return -1;
+    if (!compute_logits) return;
 
     if (!normed)
         compute::launch_rms_norm(x_->half_data(), output_norm_.device_half_data(), norm_->half_data(), hidden,
                                  config_.rms_norm_eps);
-    const int vocab = as_int(config_.vocab_size, "vocab_size");
     if (output_weight_.storage_kind == compute::WeightStorageKind::QuantizedDevice) {
         if (output_weight_.gguf_type != compute::GgufTensorType::Q6_K)
             throw Error("unsupported quantized output weight type: " + compute::to_string(output_weight_.gguf_type));
@@ -224,7 +257,93 @@ int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compu
         compute::launch_matvec_fp16_to_float(output_weight_.device_half_data(), norm_->half_data(),
                                              static_cast<float*>(logits_->data()), hidden, vocab);
     }
-    return sample_greedy_from_logits();
+    if (state)
+        compute::launch_argmax_advance(static_cast<const float*>(logits_->data()), vocab, state,
+                                       static_cast<int32_t*>(tokens_->data()), static_cast<int>(max_context_));
+}
+
+namespace {
+
+// Runs the library on `stream` for its lifetime: the work queued on the
+// previous stream is finished first, and that stream is restored (after the
+// new one has drained) at the end.
+class StreamSwitch {
+public:
+    explicit StreamSwitch(void* stream) : previous_(compute::current_stream()) {
+        compute::synchronize();
+        compute::set_stream(stream);
+    }
+    ~StreamSwitch() {
+        try {
+            compute::synchronize();
+        } catch (...) {
+        }
+        try {
+            compute::set_stream(previous_);
+        } catch (...) {
+        }
+    }
+    StreamSwitch(const StreamSwitch&) = delete;
+    StreamSwitch& operator=(const StreamSwitch&) = delete;
+
+private:
+    void* previous_;
+};
+
+}  // namespace
+
+std::vector<int32_t> QwenModel::decode_greedy(int32_t token_id, uint32_t position, uint32_t steps) {
+    require(linear_backend_ != nullptr, "model is not loaded");
+    require(token_id >= 0 && token_id < static_cast<int32_t>(config_.vocab_size), "token id out of vocab range");
+    require(position < max_context_ && steps <= max_context_ - position, "position + steps exceeds max_context");
+    std::vector<int32_t> out(steps);
+    if (steps == 0) return out;
+    if (!stream_) stream_ = compute::create_stream();
+    StreamSwitch on_model_stream(stream_);
+
+    const int32_t init[4] = {token_id, static_cast<int32_t>(position), 0, 0};
+    state_->copy_from_host(init, sizeof(init));
+    uint32_t pos = position, left = steps;
+    while (left > 0) {
+        // positions pos .. plan - 1 share one attention plan, hence one graph
+        const int plan = compute::attention_plan_length(static_cast<int>(pos) + 1, static_cast<int>(max_context_));
+        const uint32_t n = std::min<uint32_t>(left, static_cast<uint32_t>(plan) - pos);
+        void* graph = step_graph(plan);
+        for (uint32_t i = 0; i < n; ++i) compute::graph_launch(graph);
+        pos += n;
+        left -= n;
+    }
+    tokens_->copy_to_host(out.data(), out.size() * sizeof(int32_t));   // waits for the stream
+    return out;
+}
+
+// The captured step for one attention plan length (made on first use).
+void* QwenModel::step_graph(int plan_length) {
+    for (const auto& g : graphs_)
+        if (g.first == plan_length) return g.second;
+    compute::graph_begin();
+    try {
+        enqueue_token(0, 0, static_cast<int32_t*>(state_->data()), plan_length, true);
+    } catch (...) {
+        try {
+            compute::graph_destroy(compute::graph_end());
+        } catch (...) {
+        }
+        throw;
+    }
+    void* graph = compute::graph_end();
+    graphs_.emplace_back(plan_length, graph);
+    return graph;
+}
+
+void QwenModel::release_graphs() noexcept {
+    for (const auto& g : graphs_) compute::graph_destroy(g.second);
+    graphs_.clear();
+}
+
+QwenModel::~QwenModel() {
+    release_graphs();
+    compute::destroy_stream(stream_);
 }
 
 void QwenModel::synchronize() const { compute::synchronize(); }

@@ -398,6 +398,12 @@ bool attention_supported(int head_dim, int group) {
 // wave) so the per-workgroup set-up and the partial write stay amortised;
 // chunk a multiple of 4 tiles, and at most kMaxSplits chunks (the merge's
 // LDS weight table).
+int attention_plan_length(int length, int max_context) {
+    long long b = 256;
+    while (b < length) b <<= 1;
+    return b < max_context ? (int)b : max_context;
+}
+
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
     AttnPlan p{};
     const int group = heads / kv_heads;

@@ -68,10 +68,21 @@ __device__ __forceinline__ float q6k_value(const uint8_t* blk, int e) {
     return host_nan(__builtin_isnan(d) ? __builtin_signbit(d) : true);   // NaN d, or Inf * 0
 }
 
-__global__ void embed_q6k_kernel(const uint8_t* __restrict__ table, int32_t token_id, uint16_t* __restrict__ out,
+// The token comes from `token_at` (device memory) when that is not null; a
+// token there outside [0, vocab) yields a zero row instead of a read past
+// the table (the host validates the scalar form).
+__global__ void embed_q6k_kernel(const uint8_t* __restrict__ table, int32_t token_id,
+                                 const int32_t* __restrict__ token_at, int vocab, uint16_t* __restrict__ out,
                                  int hidden) {
     const int idx = blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= hidden) return;
+    if (token_at) {
+        token_id = *token_at;
+        if (token_id < 0 || token_id >= vocab) {
+            out[idx] = 0;
+            return;
+        }
+    }
     const size_t nb = (size_t)hidden / kQK;
     const uint8_t* row = table + (size_t)token_id * nb * kQ6KBytes;
     out[idx] = f2h_rne(q6k_value(row + (size_t)(idx / kQK) * kQ6KBytes, idx % kQK));
@@ -95,10 +106,11 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ w, uint64_t count, ui
 
 }  // namespace
 
-hipError_t launch_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden, hipStream_t s) {
+hipError_t launch_embed_q6k(const uint8_t* table, int32_t token_id, const int32_t* token_at, int vocab,
+                            uint16_t* out, int hidden, hipStream_t s) {
     const int block = 256;
     launch_kernel(embed_q6k_kernel, dim3((hidden + block - 1) / block), dim3(block), 0, s, table, token_id,
-                       out, hidden);
+                  token_at, vocab, out, hidden);
     return hipGetLastError();
 }
 

@@ -23,10 +23,19 @@ __global__ void store_kv_kernel(const uint16_t* __restrict__ k, const uint16_t* 
     }
 }
 
-__global__ void embed_f16_kernel(const uint16_t* __restrict__ t, int32_t token_id, uint16_t* __restrict__ out,
-                                 int hidden) {
+// token from `token_at` (device) when not null: outside [0, vocab) -> zeros
+__global__ void embed_f16_kernel(const uint16_t* __restrict__ t, int32_t token_id, const int32_t* __restrict__ token_at,
+                                 int vocab, uint16_t* __restrict__ out, int hidden) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < hidden) out[i] = t[(size_t)token_id * hidden + i];
+    if (i >= hidden) return;
+    if (token_at) {
+        token_id = *token_at;
+        if (token_id < 0 || token_id >= vocab) {
+            out[i] = 0;
+            return;
+        }
+    }
+    out[i] = t[(size_t)token_id * hidden + i];
 }
 
 __global__ void copy_kernel(const uint16_t* __restrict__ in, uint16_t* __restrict__ out, int n) {
@@ -97,14 +106,22 @@ __global__ void add_rms_norm_kernel(uint16_t* __restrict__ x, const uint16_t* __
 // v copied into v_cache).  Each stage rounds to fp16 where the separate
 // kernels store, with the same per-head 128-thread reduction, so the
 // results equal the separate launches bit for bit.
+// The position comes from `position_at` (device memory) when that is not
+// null; a position there outside [0, max_positions) writes nothing to the
+// caches (the host validates the scalar form).
 __global__ void qk_norm_rope_store_kernel(uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                           const uint16_t* __restrict__ v, const uint16_t* __restrict__ qw,
                                           const uint16_t* __restrict__ kw, int heads, int head_dim, int position,
-                                          float theta, float eps, uint16_t* __restrict__ k_cache,
-                                          uint16_t* __restrict__ v_cache, int kv_size) {
+                                          const int32_t* __restrict__ position_at, int max_positions, float theta,
+                                          float eps, uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+                                          int kv_size) {
     __shared__ float red[16];
     __shared__ uint16_t vals[256];
     const bool is_q = (int)blockIdx.x < heads;
+    if (position_at) {
+        position = *position_at;
+        if (!is_q && (position < 0 || position >= max_positions)) return;   // whole block: no barrier skipped
+    }
     const int head = is_q ? blockIdx.x : blockIdx.x - heads;
     const uint16_t* src = is_q ? q + (size_t)head * head_dim : k + (size_t)head * head_dim;
     const uint16_t* w = is_q ? qw : kw;
@@ -232,12 +249,27 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(const fl
     if (threadIdx.x == 0) g_argmax_partial[blockIdx.x] = m;
 }
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(int parts, int32_t* __restrict__ out) {
+// With `state` (device int32 {token, position, step, 0}) the pick also
+// becomes the next step's input: tokens[step] = pick (while step <
+// capacity), token = pick, position += 1, step += 1.
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(int parts, int32_t* __restrict__ out,
+                                                                      int32_t* __restrict__ state,
+                                                                      int32_t* __restrict__ tokens, int capacity) {
     __shared__ uint64_t red[kArgmaxThreads / kWave];
     uint64_t k = 0;
     for (int i = threadIdx.x; i < parts; i += kArgmaxThreads) k = g_argmax_partial[i] > k ? g_argmax_partial[i] : k;
     const uint64_t m = block_max_u64(k, red);
-    if (threadIdx.x == 0) out[0] = m == 0 ? 0 : (int32_t)~(uint32_t)(m & 0xffffffffu);
+    if (threadIdx.x == 0) {
+        const int32_t pick = m == 0 ? 0 : (int32_t)~(uint32_t)(m & 0xffffffffu);
+        if (out) out[0] = pick;
+        if (state) {
+            const int32_t step = state[2];
+            if (step >= 0 && step < capacity) tokens[step] = pick;
+            state[0] = pick;
+            state[1] += 1;
+            state[2] = step + 1;
+        }
+    }
 }
 
 __global__ void fill_zero_kernel(uint32_t* __restrict__ p, size_t nwords) {
@@ -289,8 +321,9 @@ hipError_t launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, u
     return hipGetLastError();
 }
 
-hipError_t launch_embed_f16(const uint16_t* t, int32_t token_id, uint16_t* out, int hidden, hipStream_t s) {
-    launch_kernel(embed_f16_kernel, grid_for(hidden), dim3(kBlk), 0, s, t, token_id, out, hidden);
+hipError_t launch_embed_f16(const uint16_t* t, int32_t token_id, const int32_t* token_at, int vocab, uint16_t* out,
+                            int hidden, hipStream_t s) {
+    launch_kernel(embed_f16_kernel, grid_for(hidden), dim3(kBlk), 0, s, t, token_id, token_at, vocab, out, hidden);
     return hipGetLastError();
 }
 
@@ -323,9 +356,10 @@ hipError_t launch_add_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w
 
 hipError_t launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* qw,
                                      const uint16_t* kw, int heads, int kv_heads, int head_dim, int position,
-                                     float theta, float eps, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s) {
+                                     const int32_t* position_at, int max_positions, float theta, float eps,
+                                     uint16_t* k_cache, uint16_t* v_cache, hipStream_t s) {
     launch_kernel(qk_norm_rope_store_kernel, dim3(heads + kv_heads), dim3(kWave * 2), 0, s, q, k, v, qw, kw, heads,
-                  head_dim, position, theta, eps, k_cache, v_cache, kv_heads * head_dim);
+                  head_dim, position, position_at, max_positions, theta, eps, k_cache, v_cache, kv_heads * head_dim);
     return hipGetLastError();
 }
 
@@ -348,7 +382,8 @@ hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool
     return hipGetLastError();
 }
 
-hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s) {
+hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, int32_t* state, int32_t* tokens,
+                         int capacity, hipStream_t s) {
     // about 4 values per thread, at most kArgmaxMaxBlocks partials
     int parts = (n + 4 * kArgmaxThreads - 1) / (4 * kArgmaxThreads);
     if (parts > kArgmaxMaxBlocks) parts = kArgmaxMaxBlocks;
@@ -357,7 +392,8 @@ hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStre
     launch_kernel_in_call(false, argmax_partial_kernel, dim3(parts), dim3(kArgmaxThreads), 0, s, logits, n, per_block);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_kernel(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, parts, out_index);
+    launch_kernel(argmax_final_kernel, dim3(1), dim3(kArgmaxThreads), 0, s, parts, out_index, state, tokens,
+                  capacity);
     return hipGetLastError();
 }
 

@@ -68,19 +68,25 @@ struct AttnPlan {
     int depth;     // K/V tiles in flight per wave (1 or 2)
 };
 bool attention_supported(int head_dim, int group);
+// The length a decode step's attention is planned for: the smallest power
+// of two >= max(length, 256), at most max_context.
+int attention_plan_length(int length, int max_context);
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks);
 size_t attention_workspace_bytes(const AttnPlan& p, int nseq, int heads, int head_dim);
 hipError_t launch_attention(const AttnArgs& a, const AttnPlan& p, hipStream_t s);
 
 // ---- embedding / dequant (dequant.hip) ----
-hipError_t launch_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out, int hidden, hipStream_t s);
+// token_at (device, may be null) replaces token_id; out of [0, vocab) -> zeros
+hipError_t launch_embed_q6k(const uint8_t* table, int32_t token_id, const int32_t* token_at, int vocab,
+                            uint16_t* out, int hidden, hipStream_t s);
 hipError_t launch_dequant_q4k_f16(const uint8_t* w, uint64_t count, uint16_t* out, hipStream_t s);
 hipError_t launch_dequant_q6k_f16(const uint8_t* w, uint64_t count, uint16_t* out, hipStream_t s);
 
 // ---- the rest of the decode step (elementwise.hip) ----
 hipError_t launch_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc, int position,
                            int kv_size, hipStream_t s);
-hipError_t launch_embed_f16(const uint16_t* table, int32_t token_id, uint16_t* out, int hidden, hipStream_t s);
+hipError_t launch_embed_f16(const uint16_t* table, int32_t token_id, const int32_t* token_at, int vocab,
+                            uint16_t* out, int hidden, hipStream_t s);
 hipError_t launch_copy(const uint16_t* in, uint16_t* out, int n, hipStream_t s);
 hipError_t launch_add_inplace(uint16_t* t, const uint16_t* d, int n, hipStream_t s);
 hipError_t launch_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, int n, float eps,
@@ -91,14 +97,17 @@ hipError_t launch_rope(uint16_t* data, int heads, int head_dim, int position, fl
 hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, int n, hipStream_t s);
 hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
                              hipStream_t s);
-hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, hipStream_t s);
+// out_index and/or the decode state {token, position, step, 0} (device)
+hipError_t launch_argmax(const float* logits, int n, int32_t* out_index, int32_t* state, int32_t* tokens,
+                         int capacity, hipStream_t s);
 // fused forward_token steps (no reference counterpart; same results as the
 // separate launches)
 hipError_t launch_add_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w, uint16_t* out, int n, float eps,
                                hipStream_t s);
 hipError_t launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* qw,
                                      const uint16_t* kw, int heads, int kv_heads, int head_dim, int position,
-                                     float theta, float eps, uint16_t* k_cache, uint16_t* v_cache, hipStream_t s);
+                                     const int32_t* position_at, int max_positions, float theta, float eps,
+                                     uint16_t* k_cache, uint16_t* v_cache, hipStream_t s);
 hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const* w, const uint16_t* x,
                                uint16_t* const* y, const int* n, int K, hipStream_t s);
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,

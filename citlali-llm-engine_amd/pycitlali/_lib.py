@@ -73,6 +73,18 @@ SIGNATURES = [
     ("citlali_hip_matvec_gate_up_swiglu", c_int, [c_int, _P, _P, _P, _P, c_int, c_int]),
     ("citlali_hip_matvec_group", c_int, [c_int, POINTER(c_int), POINTER(c_void_p), _P, POINTER(c_void_p),
                                          POINTER(c_int), c_int]),
+    ("citlali_hip_attention_plan_length", c_int, [c_int, c_int]),
+    ("citlali_hip_argmax_advance", c_int, [_P, c_int, _P, _P, c_int]),
+    ("citlali_hip_embed_q6k_at", c_int, [_P, _P, c_int, _P, c_int]),
+    ("citlali_hip_embed_at", c_int, [_P, _P, c_int, _P, c_int]),
+    ("citlali_hip_qk_norm_rope_store_at", c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, c_float,
+                                                  c_float, _P, _P]),
+    ("citlali_hip_stream_create", c_int, [POINTER(c_void_p)]),
+    ("citlali_hip_stream_destroy", c_int, [_P]),
+    ("citlali_hip_graph_begin", c_int, []),
+    ("citlali_hip_graph_end", c_int, [POINTER(c_void_p)]),
+    ("citlali_hip_graph_launch", c_int, [_P]),
+    ("citlali_hip_graph_destroy", c_int, [_P]),
     ("citlali_hip_set_kernel_timing", c_int, [_P, _P]),
     ("citlali_hip_event_create", c_int, [POINTER(c_void_p)]),
     ("citlali_hip_event_record", c_int, [_P]),

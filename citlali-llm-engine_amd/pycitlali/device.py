@@ -232,3 +232,80 @@ def matvec_group(kinds, weights, x, outputs, out_features, in_features: int) -> 
     ys = (ctypes.c_void_p * n)(*[y.ptr for y in outputs])
     rows = (ctypes.c_int * n)(*[int(r) for r in out_features])
     _lib.call("citlali_hip_matvec_group", n, types, ws, _vp(x), ys, rows, int(in_features))
+
+
+# ---- replayable decode steps: inputs read from device memory --------------
+def attention_plan_length(length: int, max_context: int) -> int:
+    return int(_lib.load().citlali_hip_attention_plan_length(int(length), int(max_context)))
+
+
+def argmax_advance(logits, n: int, state, tokens, capacity: int) -> None:
+    """argmax, then tokens[step] = pick, token = pick, position += 1, step += 1
+    in the device int32 state {token, position, step, 0}."""
+    _lib.call("citlali_hip_argmax_advance", _vp(logits), int(n), _vp(state),
+              _vp(tokens) if tokens is not None else ctypes.c_void_p(0), int(capacity))
+
+
+def embed_q6k_at(table, token, vocab: int, out, hidden: int) -> None:
+    _lib.call("citlali_hip_embed_q6k_at", _vp(table), _vp(token), int(vocab), _vp(out), int(hidden))
+
+
+def embed_at(table, token, vocab: int, out, hidden: int) -> None:
+    _lib.call("citlali_hip_embed_at", _vp(table), _vp(token), int(vocab), _vp(out), int(hidden))
+
+
+def qk_norm_rope_store_at(q, k, v, q_norm, k_norm, heads: int, kv_heads: int, head_dim: int, position,
+                          max_positions: int, theta: float, eps: float, k_cache, v_cache) -> None:
+    null = ctypes.c_void_p(0)
+    _lib.call("citlali_hip_qk_norm_rope_store_at", _vp(q), _vp(k), _vp(v),
+              _vp(q_norm) if q_norm is not None else null, _vp(k_norm) if k_norm is not None else null, int(heads),
+              int(kv_heads), int(head_dim), _vp(position), int(max_positions), ctypes.c_float(theta),
+              ctypes.c_float(eps), _vp(k_cache), _vp(v_cache))
+
+
+class Stream:
+    """A HIP stream of the library (citlali_hip_stream_create)."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        _lib.call("citlali_hip_stream_create", ctypes.byref(h))
+        self.handle = h
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.call("citlali_hip_stream_destroy", self.handle)
+            self.handle = None
+
+
+def set_stream(stream) -> None:
+    _lib.check(_lib.load().citlali_hip_set_stream(stream.handle if stream is not None else None))
+
+
+class Graph:
+    """Launches captured on the library stream (citlali_hip_graph_begin/end)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @staticmethod
+    def capture(fn) -> "Graph":
+        _lib.call("citlali_hip_graph_begin")
+        try:
+            fn()
+        except BaseException:
+            h = ctypes.c_void_p()   # end the capture; drop what it made
+            if _lib.load().citlali_hip_graph_end(ctypes.byref(h)) == _lib.OK and h:
+                _lib.load().citlali_hip_graph_destroy(h)
+            raise
+        h = ctypes.c_void_p()
+        _lib.call("citlali_hip_graph_end", ctypes.byref(h))
+        return Graph(h)
+
+    def launch(self) -> None:
+        _lib.call("citlali_hip_graph_launch", self.handle)
+
+    def close(self) -> None:
+        if self.handle:
+            _lib.call("citlali_hip_graph_destroy", self.handle)
+            self.handle = None
+

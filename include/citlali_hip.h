@@ -102,7 +102,9 @@ int citlali_hip_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out,
  * otherwise the library keeps its own per-device workspace (allocated on the
  * first call that needs it, kept until citlali_hip_release_workspace()).
  * It no longer receives the raw scores.  head_dim 64 or 128, heads/kv_heads
- * between 1 and 8. */
+ * between 1 and 8.  The split of the positions over workgroups is planned
+ * for citlali_hip_attention_plan_length(position + 1, max_context), so all
+ * steps of one such length run the same launches. */
 int citlali_hip_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* scores,
                           uint16_t* out, int position, int max_context, int heads, int kv_heads, int head_dim);
 
@@ -117,6 +119,13 @@ int citlali_hip_attention_batched(const uint16_t* q, const uint16_t* k_cache, co
                                   long long seq_stride, const int32_t* positions, int max_positions_bound,
                                   int nseq, int heads, int kv_heads, int head_dim, void* workspace,
                                   size_t workspace_bytes, uint16_t* out);
+/* The length attention is planned for at `length` = position + 1 (no
+ * reference counterpart): the smallest power of two >= max(length, 256),
+ * at most max_context; 0 for length <= 0 or length > max_context.  A step
+ * replayed with the position in device memory (citlali_hip_attention_batched
+ * with nseq 1 and this max_positions_bound) equals citlali_hip_attention at
+ * every position of the bucket, bit for bit. */
+int citlali_hip_attention_plan_length(int length, int max_context);
 size_t citlali_hip_attention_workspace_bytes(int max_positions_bound, int nseq, int heads, int kv_heads,
                                              int head_dim);
 int citlali_hip_release_workspace(void);
@@ -153,6 +162,41 @@ int citlali_hip_rope(uint16_t* data, int heads, int head_dim, int position, floa
  * 448-465).  Uses a per-device partials table in the library: argmax calls
  * that overlap on one device (several streams) race. */
 int citlali_hip_argmax(const float* logits, int n, int32_t* out_index);
+
+/* ---- replayable decode steps (no reference counterpart) ------------------ *
+ * A decode step whose inputs live in device memory can be captured once in
+ * a HIP graph and replayed per token without host synchronisation.  The
+ * decode state is device int32 state[4] = {token, position, step, 0},
+ * 16-byte aligned.
+ * citlali_hip_argmax_advance: citlali_hip_argmax of logits, then
+ *   tokens[step] = pick (when step < capacity), token = pick, position += 1,
+ *   step += 1.
+ * citlali_hip_embed_q6k_at / citlali_hip_embed_at: embed_q6k / embed with the
+ *   token read from `token` (device); a token outside [0, vocab) gives a
+ *   zero row.
+ * citlali_hip_qk_norm_rope_store_at: qk_norm_rope_store with the position
+ *   read from `position` (device); a position outside [0, max_positions)
+ *   writes nothing to the caches. */
+int citlali_hip_argmax_advance(const float* logits, int n, int32_t* state, int32_t* tokens, int capacity);
+int citlali_hip_embed_q6k_at(const uint8_t* table, const int32_t* token, int vocab, uint16_t* out, int hidden);
+int citlali_hip_embed_at(const uint16_t* table, const int32_t* token, int vocab, uint16_t* out, int hidden);
+int citlali_hip_qk_norm_rope_store_at(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
+                                      const uint16_t* k_norm, int heads, int kv_heads, int head_dim,
+                                      const int32_t* position, int max_positions, float theta, float eps,
+                                      uint16_t* k_cache, uint16_t* v_cache);
+/* Streams and graphs.  citlali_hip_graph_begin starts capturing the launches
+ * the calling thread makes on the library stream (which must not be the null
+ * stream); citlali_hip_graph_end stops the capture (also after a failed
+ * launch) and returns an executable graph, replayed on the library stream by
+ * citlali_hip_graph_launch.  Nothing may allocate during a capture (the
+ * attention workspace must come from the caller).  A graph keeps the
+ * pointers and scalars it captured. */
+int citlali_hip_stream_create(void** stream);
+int citlali_hip_stream_destroy(void* stream);
+int citlali_hip_graph_begin(void);
+int citlali_hip_graph_end(void** graph);
+int citlali_hip_graph_launch(void* graph);
+int citlali_hip_graph_destroy(void* graph);
 
 /* ---- timing (bench and tests) --------------------------------------------- */
 /* Reads `bytes` (16-byte multiple) of a device buffer once, as fast as the

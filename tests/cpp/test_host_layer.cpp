@@ -614,6 +614,46 @@ void test_forward_greedy() {
     check(all_ties <= 3, "at most one numerical tie per 64-step run on average");
 }
 
+// QwenModel::decode_greedy (captured steps replayed per token) against the
+// forward_token loop: the same tokens exactly, across attention plan lengths
+// 256, 512 and the max_context cap (600), replayed several times with eager
+// work and synchronisations in between, and split over two calls.
+void test_decode_greedy_graph() {
+    SynthModel s = make_model(11, 2048, 16, 8, 4096, 2, 8192);
+    const int ctx = 600, first = 240, steps = ctx - first;
+    model::QwenModel gpu;
+    gpu.load(s.cfg, device_weights(s), ctx);
+    Rng r{77};
+    for (int p = 0; p < first; ++p) gpu.forward_token((int32_t)(r.next() % 8192), (uint32_t)p, false);
+    const int32_t start = (int32_t)(r.next() % 8192);
+    std::vector<int32_t> eager;
+    int32_t tok = start;
+    for (int i = 0; i < steps; ++i) {
+        tok = gpu.forward_token(tok, (uint32_t)(first + i));
+        eager.push_back(tok);
+    }
+    for (int rep = 0; rep < 3; ++rep) {
+        const std::vector<int32_t> got = gpu.decode_greedy(start, first, steps);
+        check(got == eager, "decode_greedy replay " + std::to_string(rep) + " equals the forward_token loop");
+        // eager work between replays: a forward_token whose cache write lies
+        // past every position the replays read
+        const int32_t t = gpu.forward_token(got.back(), ctx - 1);
+        check(t >= 0 && t < 8192, "eager step between replays");
+    }
+    const std::vector<int32_t> a = gpu.decode_greedy(start, first, 17);
+    const std::vector<int32_t> b = gpu.decode_greedy(a.back(), first + 17, steps - 17);
+    std::vector<int32_t> ab = a;
+    ab.insert(ab.end(), b.begin(), b.end());
+    check(ab == eager, "decode_greedy split over two calls equals one call");
+    check(gpu.decode_greedy(start, first, 0).empty(), "zero steps");
+    expect_error([&] { gpu.decode_greedy(start, first, steps + 1); }, "position + steps exceeds max_context",
+                 "steps past max_context");
+    expect_error([&] { gpu.decode_greedy(8192, first, 1); }, "token id out of vocab range", "bad token");
+    // forward_token after decode_greedy still runs on the library stream
+    check(gpu.forward_token(start, first) == eager[0], "forward_token after decode_greedy");
+    std::printf("decode_greedy: %d graph-replayed steps x 3 equal the forward_token loop\n", steps);
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -639,6 +679,7 @@ int main(int argc, char** argv) {
             test_attention();
             test_embed();
             test_forward_greedy();
+            test_decode_greedy_graph();
             compute::synchronize();
         } else {
             std::printf("usage: %s cpu|gpu\n", argv[0]);
