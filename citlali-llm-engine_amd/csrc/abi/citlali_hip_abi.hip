@@ -89,7 +89,7 @@ int workspace_for(size_t bytes, float** out) {
     return CITLALI_OK;
 }
 
-constexpr int kAttnTargetBlocks = 512;
+constexpr int kAttnTargetBlocks = 256;   // one workgroup per CU
 
 }  // namespace
 

@@ -84,6 +84,8 @@ void launch_attention_at(const uint16_t* q, const uint16_t* k_cache, const uint1
                          const int32_t* position, int plan_length, float* workspace, std::size_t workspace_bytes,
                          uint16_t* output, int heads, int kv_heads, int head_dim);
 int attention_plan_length(int length, int max_context);
+// Bytes of split partials one sequence's attention planned for `length` uses.
+std::size_t attention_workspace_bytes(int length, int heads, int kv_heads, int head_dim);
 // launch_argmax, then tokens[step] = pick, token = pick, position += 1, step += 1
 void launch_argmax_advance(const float* logits, int n, int32_t* state, int32_t* tokens, int capacity);
 

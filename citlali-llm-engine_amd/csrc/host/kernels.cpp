@@ -153,6 +153,10 @@ int attention_plan_length(int length, int max_context) {
     return n;
 }
 
+std::size_t attention_workspace_bytes(int length, int heads, int kv_heads, int head_dim) {
+    return citlali_hip_attention_workspace_bytes(length, 1, heads, kv_heads, head_dim);
+}
+
 void launch_argmax_advance(const float* logits, int n, int32_t* state, int32_t* tokens, int capacity) {
     CITLALI_HIP_CHECK(citlali_hip_argmax_advance(logits, n, state, tokens, capacity));
 }

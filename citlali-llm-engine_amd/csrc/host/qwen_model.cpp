@@ -102,7 +102,16 @@ void QwenModel::allocate_runtime_buffers() {
     ff_act_ = compute::make_device_half_buffer(ff);
     ff_out_ = compute::make_device_half_buffer(hidden);
     logits_ = compute::make_device_buffer(static_cast<size_t>(config_.vocab_size) * sizeof(float));
-    scores_ = compute::make_device_buffer(static_cast<size_t>(config_.head_count) * max_context_ * sizeof(float));
+    // the reference's heads x max_context floats, or more: the attention
+    // split partials of the longest plan (the split count never falls as the
+    // plan length grows), so no step -- a captured one included -- needs the
+    // library's own workspace
+    const size_t reference_scores = static_cast<size_t>(config_.head_count) * max_context_ * sizeof(float);
+    scores_ = compute::make_device_buffer(std::max(
+        reference_scores,
+        compute::attention_workspace_bytes(static_cast<int>(max_context_), static_cast<int>(config_.head_count),
+                                           static_cast<int>(config_.head_count_kv),
+                                           static_cast<int>(config_.head_dim))));
     next_token_ = compute::make_device_buffer(sizeof(int32_t));
     state_ = compute::make_device_buffer(4 * sizeof(int32_t));
     tokens_ = compute::make_device_buffer(static_cast<size_t>(max_context_) * sizeof(int32_t));

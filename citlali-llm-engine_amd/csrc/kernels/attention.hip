@@ -298,6 +298,223 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// head_dim 128, GQA group 2..8: the same chunk / merge structure with both
+// products on the matrix cores (v_mfma_f32_16x16x16f16).  The group's heads
+// are the 16 MFMA columns (padding heads have q = 0 and are never written).
+// Per wave, a tile of 16 positions:
+//  * scores S[pos][head] = K[pos][:] . q[head][:]: K rows go from global
+//    memory straight into the A operand (lane = row `col`, a 64-byte slab
+//    `grp` of it; the 128 dims in 8 steps of 16, dim 32t + 8grp + 4h + j of
+//    step (t, h) being operand k = 4grp + j), q is the B operand in the same
+//    dim order; lane (col, grp) gets the scores of positions 4grp + i for
+//    head col.
+//  * online softmax per head column (max and sum over the 16 lanes' groups),
+//    exponentials in base 2 as the VALU kernel.
+//  * out[head][dim] += P[head][pos] V[pos][dim]: the scores' lane layout is
+//    the A operand of P as it stands; P goes in as fp16 hi + lo halves (two
+//    MFMAs), so its fp32 value counts to about 2^-22.  V rows are staged in a
+//    wave-private LDS tile and gathered per lane as 4 positions x 4 dims
+//    (dims 64c + 4col + e feed output block 4c + e).
+// ---------------------------------------------------------------------------
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+constexpr int kMTile = 16;                     // positions per MFMA tile
+constexpr int kMStride = 128 + 8;              // V tile row in LDS (halves)
+constexpr size_t kMWaveLds = (size_t)kMTile * kMStride * 2;
+// merge: (max, sum)[kWaves][8], acc[kWaves][2 row groups][8 blocks][16 cols][4]
+constexpr size_t kMMlFloats = (size_t)kWaves * 8 * 2;
+constexpr size_t kMLds = (kMMlFloats + (size_t)kWaves * 2 * 8 * 16 * 4) * sizeof(float);
+constexpr size_t kMfmaLds = kMLds > kMWaveLds * kWaves ? kMLds : kMWaveLds * kWaves;
+
+__device__ __forceinline__ f32x4 mfma16(half4 a, half4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half4 as_half4(uint32_t lo, uint32_t hi) {
+    return __builtin_bit_cast(half4, u32x2{lo, hi});
+}
+
+template <int GP, int kDepth>
+__global__ __launch_bounds__(kBlock) void attn_mfma_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
+    long long seq_stride, const int32_t* __restrict__ positions, int position, int max_len, int heads,
+    int kv_heads, int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits,
+    uint16_t* __restrict__ out) {
+    constexpr int HD = 128;
+    static_assert(GP >= 2 && GP <= 8, "group");
+    extern __shared__ __align__(16) uint8_t smem[];
+
+    const int split = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const SeqSpan span = seq_span(positions, position, seq, chunk, max_len);
+    const int L = span.len, n_valid = span.n_valid;
+    const int b0 = split * chunk;
+    if (b0 >= L) return;
+    const int b1 = min(L, b0 + chunk);
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int col = lane & 15, grp = lane >> 4;
+    const int sub = (((b1 - b0 + kWaves - 1) / kWaves + kMTile - 1) / kMTile) * kMTile;
+    const int w0 = min(b1, b0 + wave * sub);
+    const int w1 = min(b1, w0 + sub);
+
+    uint16_t* vt = reinterpret_cast<uint16_t*>(smem + (size_t)wave * kMWaveLds);
+    const uint16_t* kbase = k_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + 8 * grp;
+    const uint16_t* vbase = v_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + 8 * grp;
+    const size_t row_step = (size_t)kv_heads * HD;
+
+    // q of head `col` (zero past the group) as B operands, dims 32t + 8grp + 4h + j
+    half4 qb[4][2];
+    {
+        const bool ok = col < group;
+        const uint16_t* qh = q + ((size_t)seq * heads + kvh * group + (ok ? col : group - 1)) * HD + 8 * grp;
+        const uint32_t keep = ok ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(qh + 32 * t);
+            qb[t][0] = as_half4(v.x & keep, v.y & keep);
+            qb[t][1] = as_half4(v.z & keep, v.w & keep);
+        }
+    }
+    f32x4 o[8];   // o[4c + e][i]: head 4grp + i, dim 64c + 4col + e
+#pragma unroll
+    for (int b = 0; b < 8; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;   // head col
+
+    // kDepth tiles of K and V rows in flight; branch-free (rows past the
+    // range re-read row w1 - 1, in bounds also for an empty range)
+    u32x4 kr[kDepth][4], vr[kDepth][4];
+    auto load_tile = [&](int d, int t0) {
+        const size_t pos = (size_t)min(t0 + col, w1 - 1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            kr[d][t] = *reinterpret_cast<const u32x4*>(kbase + pos * row_step + 32 * t);
+            vr[d][t] = *reinterpret_cast<const u32x4*>(vbase + pos * row_step + 32 * t);
+        }
+    };
+
+    auto process = [&](int d, int t0) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) *reinterpret_cast<u32x4*>(vt + col * kMStride + 32 * t + 8 * grp) = vr[d][t];
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            s = mfma16(as_half4(kr[d][t].x, kr[d][t].y), qb[t][0], s);
+            s = mfma16(as_half4(kr[d][t].z, kr[d][t].w), qb[t][1], s);
+        }
+        // the slot is consumed: refill it with the tile kDepth ahead (the
+        // address waits for the scores, so the load is issued after them)
+        load_tile(d, issue_after(t0 + kDepth * kMTile, s[0], s[3]));
+        __builtin_amdgcn_sched_barrier(0);
+
+        float sv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = t0 + 4 * grp + i < w1 ? s[i] * scale_log2 : -INFINITY;
+        const float mt = column_max<16>(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+        const float m_new = fmaxf(m_run, mt);
+        const bool live = m_new != -INFINITY;
+        const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+        float pv[4];
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pv[i] = live ? __builtin_amdgcn_exp2f(sv[i] - m_new) : 0.f;
+            ps += pv[i];
+        }
+        l_run = l_run * alpha + column_sum<16>(ps);
+        m_run = m_new;
+
+        // rescale the heads this lane accumulates (head 4grp + i: alpha of column 4grp + i)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = __shfl(alpha, 4 * grp + i, kWave);
+#pragma unroll
+            for (int b = 0; b < 8; ++b) o[b][i] *= a;
+        }
+        half4 ph, pl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const _Float16 h = (_Float16)pv[j];
+            ph[j] = h;
+            pl[j] = (_Float16)(pv[j] - (float)h);
+        }
+        wave_lds_sync();   // the V rows stored above
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            uint32_t w[4][2];   // rows 4grp + j, dims 64c + 4col .. + 3
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const u32x2 x = *reinterpret_cast<const u32x2*>(vt + (4 * grp + j) * kMStride + 64 * c + 4 * col);
+                w[j][0] = x.x;
+                w[j][1] = x.y;
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+                const half4 vb = as_half4(__builtin_amdgcn_perm(w[1][e >> 1], w[0][e >> 1], sel),
+                                          __builtin_amdgcn_perm(w[3][e >> 1], w[2][e >> 1], sel));
+                o[4 * c + e] = mfma16(ph, vb, o[4 * c + e]);
+                o[4 * c + e] = mfma16(pl, vb, o[4 * c + e]);
+            }
+        }
+        wave_lds_sync();   // before the next tile overwrites the rows
+    };
+
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) {
+        load_tile(d, w0 + d * kMTile);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    for (int t0 = w0; t0 < w1; t0 += kDepth * kMTile) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) process(d, t0 + d * kMTile);
+    }
+
+    // ---- merge the four waves in LDS ----
+    __syncthreads();   // every wave is done with its V tile
+    float* ml = reinterpret_cast<float*>(smem);   // [kWaves][8] (max, sum)
+    float* ms = ml + kMMlFloats;                  // [kWaves][2][8][16][4]
+    if (grp == 0 && col < GP) {
+        ml[(wave * 8 + col) * 2] = m_run;
+        ml[(wave * 8 + col) * 2 + 1] = l_run;
+    }
+    if (grp < (GP + 3) / 4) {
+#pragma unroll
+        for (int b = 0; b < 8; ++b)
+            *reinterpret_cast<f32x4*>(ms + ((((size_t)wave * 2 + grp) * 8 + b) * 16 + col) * 4) = o[b];
+    }
+    __syncthreads();
+
+    for (int idx = threadIdx.x; idx < group * HD; idx += kBlock) {
+        const int h = idx / HD, dim = idx - h * HD;
+        const int hg = h >> 2, hi = h & 3;
+        const int b = 4 * (dim >> 6) + (dim & 3), c16 = (dim & 63) >> 2;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[(w * 8 + h) * 2]);
+        float Ls = 0.f, A = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = ml[(w * 8 + h) * 2];
+            const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+            Ls += ml[(w * 8 + h) * 2 + 1] * f;
+            A += ms[((((size_t)w * 2 + hg) * 8 + b) * 16 + c16) * 4 + hi] * f;
+        }
+        const int hq = kvh * group + h;
+        if (n_valid == 1) {
+            out[((size_t)seq * heads + hq) * HD + dim] = f2h_rne(A / Ls);
+        } else {
+            float* pe = part + (((size_t)seq * heads + hq) * n_splits + split) * (HD + 4);
+            pe[dim] = A;
+            if (dim == 0) {
+                pe[HD] = M;
+                pe[HD + 1] = Ls;
+            }
+        }
+    }
+}
+
 // Grid: (query head, seq).  Log-sum-exp merge of one head's chunk partials
 // ([chunk][HD + 4]: acc[HD], max, sum).  Phase 1: wave 0 finds the max and
 // keeps the chunk weights exp2(m - max) in LDS; phase 2: thread = (4 dims,
@@ -367,8 +584,29 @@ hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream
     return hipGetLastError();
 }
 
+template <int GP, int kDepth>
+hipError_t launch_mfma(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
+    const float scale_log2 = (float)(1.4426950408889634 / sqrt(128.0));
+    launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth>), dim3(p.n_splits, a.kv_heads, a.nseq),
+                          dim3(kBlock), kMfmaLds, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
+                          a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
+                          a.workspace, p.n_splits, a.out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.n_splits <= 1) return e;
+    launch_kernel((attn_merge_kernel<128>), dim3(a.heads, a.nseq), dim3(kBlock), kMergeLds, stream, a.workspace,
+                  a.positions, a.position, a.max_len, a.heads, p.chunk, p.n_splits, a.out);
+    return hipGetLastError();
+}
+
 template <int HD, int GP>
 hipError_t launch_depth(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
+    if constexpr (HD == 128 && GP >= 2) {
+        switch (p.depth) {
+            case 1: return launch_mfma<GP, 1>(a, p, s);
+            case 2: return launch_mfma<GP, 2>(a, p, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (p.depth) {
         case 1: return launch_split<HD, GP, 1>(a, p, s);
         case 2: return launch_split<HD, GP, 2>(a, p, s);
@@ -393,26 +631,29 @@ bool attention_supported(int head_dim, int group) {
     return (head_dim == 64 || head_dim == 128) && group >= 1 && group <= 8;
 }
 
-// Work split: enough chunks for about `target_blocks` workgroups over all
-// (sequence, kv head) units, but 256..512 positions per chunk (64..128 per
-// wave) so the per-workgroup set-up and the partial write stay amortised;
-// chunk a multiple of 4 tiles, and at most kMaxSplits chunks (the merge's
-// LDS weight table).
 int attention_plan_length(int length, int max_context) {
     long long b = 256;
     while (b < length) b <<= 1;
     return b < max_context ? (int)b : max_context;
 }
 
+// Work split: enough chunks for about `target_blocks` workgroups over all
+// (sequence, kv head) units, within a range of chunk lengths that keeps the
+// per-workgroup set-up and the partial write amortised -- 64..256 positions
+// for the matrix-core kernel (head_dim 128, group >= 2), 256..512 for the
+// other (measured on MI355X at 512..8192 positions); the chunk a multiple of
+// 4 tiles, and at most kMaxSplits chunks (the merge's LDS weight table).
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
     AttnPlan p{};
     const int group = heads / kv_heads;
     p.gp = group <= 1 ? 1 : group <= 2 ? 2 : group <= 4 ? 4 : 8;
-    const int tp = (64 / p.gp) < 32 ? 64 / p.gp : 32;
+    const bool mfma = head_dim == 128 && p.gp >= 2;
+    const int tp = mfma ? kMTile : (64 / p.gp) < 32 ? 64 / p.gp : 32;
     const int quantum = tp * kWaves;
     const long long units = (long long)nseq * kv_heads;
+    const long long lo = mfma ? 64 : 256, hi = mfma ? 256 : 512;
     long long chunk = ((long long)max_len * units + target_blocks - 1) / target_blocks;
-    chunk = chunk < 256 ? 256 : chunk > 512 ? 512 : chunk;
+    chunk = chunk < lo ? lo : chunk > hi ? hi : chunk;
     const long long min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;   // merge LDS bound
     if (chunk < min_chunk) chunk = min_chunk;
     chunk = ((chunk + quantum - 1) / quantum) * quantum;
@@ -421,7 +662,6 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     // one tile in flight per wave: deeper rings measured no faster on
     // gfx950 (the per-tile work, not the load latency, bounds a wave)
     p.depth = 1;
-    (void)head_dim;
     return p;
 }
 

@@ -132,7 +132,11 @@ def test_attention_at_device_position_equals_scalar_attention(hip, max_context):
     kc = up(hip, hip.synth.normal_f16(rng, max_context * kv_heads * hd))
     vc = up(hip, hip.synth.normal_f16(rng, max_context * kv_heads * hd))
     q = up(hip, hip.synth.normal_f16(rng, heads * hd))
-    scores = hip.DeviceArray(heads * max_context * 4)
+    # the partials of the longest plan (more than the reference's
+    # heads x max_context floats when chunks are short)
+    ws_bytes = max(heads * max_context * 4,
+                   hip.device.attention_workspace_bytes(max_context, 1, heads, kv_heads, hd))
+    scores = hip.DeviceArray(ws_bytes)
     for pos in (0, 100, 255, 256, 300, 511, 700, max_context - 1):
         if pos >= max_context:
             continue
@@ -140,7 +144,7 @@ def test_attention_at_device_position_equals_scalar_attention(hip, max_context):
         hip.device.attention(q, kc, vc, scores, a, pos, max_context, heads, kv_heads, hd)
         plan = hip.device.attention_plan_length(pos + 1, max_context)
         hip.device.attention_batched(q, kc, vc, 0, up(hip, np.array([pos], np.int32)), plan, 1, heads, kv_heads, hd,
-                                     scores, heads * max_context * 4, b)
+                                     scores, ws_bytes, b)
         assert np.array_equal(a.download(np.uint16), b.download(np.uint16)), pos
 
 
