@@ -23,8 +23,10 @@ steps, from HIP events that the kernel's own dispatches stamp
 (hipExtLaunchKernel; for attention, split start to merge end).  cpu_baseline: the
 oracle's restatement of the reference's host arithmetic (dequant to fp16 with
 the host rule, fp32 dot; fp32 attention) on a bounded sample of the same
-layer, on this machine's host cores.  decode_cfg5: BASELINE config 5 (the
-whole synthetic Qwen3-8B, greedy decode tok/s) from bin/decode_qwen3.
+layer, on this machine's host cores.  attention_cfg4
+(16 sequences in one batched attention launch).  decode_cfg5: BASELINE
+config 5 (the whole synthetic Qwen3-8B, greedy decode tok/s) from
+bin/decode_qwen3.
 """
 from __future__ import annotations
 
@@ -193,6 +195,52 @@ def run_gpu(args):
     return total_ms, dominant, dom_ms, per, (stream_gbps, copy_gbps), host
 
 
+def attention_cfg4():
+    """BASELINE config 4 beside the headline: 16 independent sequences at the
+    Qwen3-8B head shape (32 / 8 heads, head_dim 128) in one batched attention
+    launch, KV lengths uniform in [4096, 32768] from seed 4, caches of
+    ~2.1 GB (far beyond the Infinity Cache).  GB/s = K and V bytes read per
+    launch (sum of the lengths x 8 kv heads x 128 x 2 B x 2) over the mean
+    launch time of 20 launches (HIP events, split + merge)."""
+    import pycitlali as hip
+    nseq, max_len = 16, 32768
+    rng = np.random.default_rng(4)
+    lens = rng.integers(4096, max_len + 1, nseq)
+    stride = max_len * KV_HEADS * HEAD_DIM
+    kc, vc = hip.DeviceArray(nseq * stride * 2), hip.DeviceArray(nseq * stride * 2)
+    block = rng.standard_normal(32 << 20, dtype=np.float32).astype(np.float16)   # 64 MB, tiled
+    for buf in (kc, vc):
+        for off in range(0, buf.nbytes, block.nbytes):
+            n = min(block.nbytes, buf.nbytes - off)
+            buf.upload(block[: n // 2], off)
+    q = hip.DeviceArray.from_numpy(rng.standard_normal(nseq * HEADS * HEAD_DIM).astype(np.float16))
+    pos = hip.DeviceArray.from_numpy((lens - 1).astype(np.int32))
+    ws_bytes = hip.device.attention_workspace_bytes(max_len, nseq, HEADS, KV_HEADS, HEAD_DIM)
+    ws = hip.DeviceArray(max(ws_bytes, 16))
+    out = hip.DeviceArray(nseq * HEADS * HEAD_DIM * 2)
+
+    def launch():
+        hip.device.attention_batched(q, kc, vc, stride, pos, max_len, nseq, HEADS, KV_HEADS, HEAD_DIM, ws, ws_bytes,
+                                     out)
+    for _ in range(3):
+        launch()
+    reps = 20
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record()
+    for _ in range(reps):
+        launch()
+    e1.record()
+    e1.synchronize()
+    us = e0.elapsed_ms(e1) / reps * 1e3
+    kv_bytes = int(lens.sum()) * KV_HEADS * HEAD_DIM * 2 * 2
+    for a in (kc, vc, q, pos, ws, out):
+        a.close()
+    return {"workload": "BASELINE config 4: 16 sequences, 32/8 heads, head_dim 128, KV lengths uniform in "
+                        "[4096, 32768] (seed 4), one batched launch",
+            "positions": int(lens.sum()), "kv_bytes": kv_bytes, "us_per_launch": round(us, 2),
+            "GBps": round(kv_bytes / (us * 1e-6) / 1e9, 1), "frac_of_8TBps": round(kv_bytes / (us * 1e-6) / 8e12, 4)}
+
+
 def cpu_baseline(host, budget_s):
     """The oracle (restated reference arithmetic) on the host cores: one
     layer step -- every GEMV as repo dequant to fp16 + fp32 dot, attention in
@@ -300,6 +348,7 @@ def main():
         "copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": None,
     }
+    line["attention_cfg4"] = attention_cfg4()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
     line["decode_cfg5"] = None if args.no_decode else decode_cfg5()

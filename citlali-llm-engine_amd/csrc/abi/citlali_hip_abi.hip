@@ -552,7 +552,8 @@ CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_
     REQUIRE(w_up && aligned(w_up, walign), "matvec_gate_up_swiglu: bad up weight");
     if (in_f != 4096 && in_f != 8192)
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_gate_up_swiglu: in_features %d has no fused kernel", in_f);
-    HIP_TRY(launch_matvec_gate_up_swiglu(gguf_type == 14 ? 6 : 4, w_gate, w_up, x, act, in_f, out_f, g_stream));
+    HIP_TRY(launch_matvec_gate_up_swiglu(gguf_type == 14 ? 6 : 4, w_gate, w_up, x, act, in_f, out_f, nullptr,
+                                         g_stream));
     return CITLALI_OK;
 }
 
@@ -575,7 +576,82 @@ CITLALI_EXPORT int citlali_hip_matvec_group(int count, const int* gguf_types, co
     REQUIRE(rows <= INT_MAX, "matvec_group: %lld rows in total exceed INT_MAX", rows);
     if (in_f % 4096 != 0 || in_f > 16384)
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: in_features %d has no grouped kernel", in_f);
-    HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, g_stream));
+    HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, nullptr, g_stream));
+    return CITLALI_OK;
+}
+
+// ---------------------------------------------------------------- GEMVs with the add + RMSNorm prologue
+namespace {
+int check_norm(const char* who, const uint16_t* x, const citlali_hip_norm* n, int in_f, NormIn* out) {
+    REQUIRE(n, "%s: null norm", who);
+    REQUIRE(n->weight && aligned(n->weight, 16), "%s: norm weight must be non-null and 16-byte aligned", who);
+    REQUIRE(!n->delta || aligned(n->delta, 16), "%s: delta must be 16-byte aligned", who);
+    REQUIRE(!n->sum_out || aligned(n->sum_out, 16), "%s: sum_out must be 16-byte aligned", who);
+    REQUIRE(!n->sum_out || (n->sum_out != x && n->sum_out != n->delta),
+            "%s: sum_out must not be the input or the delta (every workgroup reads them)", who);
+    *out = NormIn{n->delta, n->weight, n->sum_out, n->eps};
+    (void)in_f;
+    return CITLALI_OK;
+}
+bool norm_length_ok(int in_f) { return in_f % 4096 == 0 && in_f <= 16384; }
+}  // namespace
+
+CITLALI_EXPORT int citlali_hip_matvec_group_norm(int count, const int* gguf_types, const uint8_t* const* weights,
+                                                 const uint16_t* x, const citlali_hip_norm* norm,
+                                                 uint16_t* const* outputs, const int* out_features, int in_f) {
+    REQUIRE(count >= 1 && count <= 3, "matvec_group_norm: count %d is not 1, 2 or 3", count);
+    REQUIRE(gguf_types && weights && outputs && out_features, "matvec_group_norm received a null array");
+    NormIn nrm;
+    int st = check_norm("matvec_group_norm", x, norm, in_f, &nrm);
+    if (st) return st;
+    int kinds[3];
+    long long rows = 0;
+    for (int i = 0; i < count; ++i) {
+        REQUIRE(gguf_types[i] == 12 || gguf_types[i] == 14, "matvec_group_norm: GGUF type %d is not Q4_K or Q6_K",
+                gguf_types[i]);
+        st = check_matvec("matvec_group_norm", weights[i], x, outputs[i], in_f, out_features[i],
+                          gguf_types[i] == 12 ? 16 : 4, 2);
+        if (st) return st;
+        kinds[i] = gguf_types[i] == 14 ? 6 : 4;
+        rows += out_features[i];
+    }
+    REQUIRE(rows <= INT_MAX, "matvec_group_norm: %lld rows in total exceed INT_MAX", rows);
+    if (!norm_length_ok(in_f))
+        return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group_norm: in_features %d has no grouped kernel", in_f);
+    HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, &nrm, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu_norm(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up,
+                                                          const uint16_t* x, const citlali_hip_norm* norm,
+                                                          uint16_t* act, int in_f, int out_f) {
+    REQUIRE(gguf_type == 12 || gguf_type == 14, "matvec_gate_up_swiglu_norm: GGUF type %d is not Q4_K or Q6_K",
+            gguf_type);
+    NormIn nrm;
+    int st = check_norm("matvec_gate_up_swiglu_norm", x, norm, in_f, &nrm);
+    if (st) return st;
+    const uintptr_t walign = gguf_type == 12 ? 16 : 4;
+    st = check_matvec("matvec_gate_up_swiglu_norm", w_gate, x, act, in_f, out_f, walign, 2);
+    if (st) return st;
+    REQUIRE(w_up && aligned(w_up, walign), "matvec_gate_up_swiglu_norm: bad up weight");
+    if (in_f != 4096 && in_f != 8192)
+        return fail(CITLALI_ERR_UNSUPPORTED, "matvec_gate_up_swiglu_norm: in_features %d has no fused kernel", in_f);
+    HIP_TRY(launch_matvec_gate_up_swiglu(gguf_type == 14 ? 6 : 4, w_gate, w_up, x, act, in_f, out_f, &nrm,
+                                         g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_matvec_norm(int gguf_type, const uint8_t* w, const uint16_t* x,
+                                           const citlali_hip_norm* norm, void* y, int f32_out, int in_f, int out_f) {
+    REQUIRE(gguf_type == 12 || gguf_type == 14, "matvec_norm: GGUF type %d is not Q4_K or Q6_K", gguf_type);
+    NormIn nrm;
+    int st = check_norm("matvec_norm", x, norm, in_f, &nrm);
+    if (st) return st;
+    st = check_matvec("matvec_norm", w, x, y, in_f, out_f, gguf_type == 12 ? 16 : 4, f32_out ? 4 : 2);
+    if (st) return st;
+    if (!norm_length_ok(in_f))
+        return fail(CITLALI_ERR_UNSUPPORTED, "matvec_norm: in_features %d has no prologue kernel", in_f);
+    HIP_TRY(launch_matvec_norm(gguf_type == 14 ? 6 : 4, w, x, nrm, y, f32_out != 0, in_f, out_f, g_stream));
     return CITLALI_OK;
 }
 

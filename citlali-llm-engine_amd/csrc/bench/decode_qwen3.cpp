@@ -15,7 +15,7 @@
 // replayed from a captured HIP graph); both must give the same tokens.
 // Prints one JSON line.
 //
-// usage: decode_qwen3 [--layers 36] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1]
+// usage: decode_qwen3 [--layers 36] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1] [--no-graph]
 #include "citlali/common.h"
 #include "citlali/compute/hip/kernels.h"
 #include "citlali/model/qwen_model.h"
@@ -109,6 +109,9 @@ int main(int argc, char** argv) {
     const int steps = arg(argc, argv, "--steps", 256);
     const int distinct = arg(argc, argv, "--distinct", 4);
     const uint64_t seed = (uint64_t)arg(argc, argv, "--seed", 1);
+    bool graph_pass = true;   // --no-graph: forward_token loop only (for tracing tools)
+    for (int i = 1; i < argc; ++i)
+        if (std::strcmp(argv[i], "--no-graph") == 0) graph_pass = false;
     try {
         if (citlali_hip_init(0) != CITLALI_OK) throw Error(citlali_hip_last_error());
         model::QwenConfig cfg;
@@ -204,11 +207,15 @@ int main(int argc, char** argv) {
         // a captured graph, no host synchronisation between steps): the first
         // call captures the graphs, the second is timed, wall clock around
         // the whole call including the copy of the tokens
-        const std::vector<int32_t> warm = m.decode_greedy(first, first_pos, (uint32_t)steps);
-        const auto g0 = std::chrono::steady_clock::now();
-        const std::vector<int32_t> graph = m.decode_greedy(first, first_pos, (uint32_t)steps);
-        const auto g1 = std::chrono::steady_clock::now();
-        const double graph_wall = std::chrono::duration<double>(g1 - g0).count();
+        std::vector<int32_t> warm = eager, graph = eager;
+        double graph_wall = eager_wall;
+        if (graph_pass) {
+            warm = m.decode_greedy(first, first_pos, (uint32_t)steps);
+            const auto g0 = std::chrono::steady_clock::now();
+            graph = m.decode_greedy(first, first_pos, (uint32_t)steps);
+            const auto g1 = std::chrono::steady_clock::now();
+            graph_wall = std::chrono::duration<double>(g1 - g0).count();
+        }
         const bool match = graph == eager && warm == eager;
         uint64_t checksum = 0;
         for (int32_t t : graph) checksum = checksum * 1000003ull + (uint64_t)t;
@@ -221,12 +228,14 @@ int main(int argc, char** argv) {
                                   (double)layers * 2 * 2 * NKV * mean_len;
         std::printf("{\"workload\": \"BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode\", \"layers\": %d, "
                     "\"distinct_layer_weight_sets\": %d, \"prompt\": %d, \"steps\": %d, \"decode_tok_per_s\": %.2f, "
-                    "\"decode_ms_per_token\": %.4f, \"decode_mode\": \"QwenModel::decode_greedy (graph replay), "
-                    "wall clock\", \"decode_GBps\": %.1f, \"decode_tok_per_s_forward_token\": %.2f, "
+                    "\"decode_ms_per_token\": %.4f, \"decode_mode\": \"%s\", "
+                    "\"decode_GBps\": %.1f, \"decode_tok_per_s_forward_token\": %.2f, "
                     "\"decode_ms_per_token_forward_token\": %.4f, \"decode_ms_per_token_forward_token_wall\": %.4f, "
                     "\"graph_tokens_equal_forward_token\": %s, \"prompt_tok_per_s\": %.2f, "
                     "\"prompt_ms_per_token_wall\": %.4f, \"setup_s\": %.1f, \"token_checksum\": %llu}\n",
                     layers, distinct, prompt, steps, steps / (decode_ms * 1e-3), decode_ms / steps,
+                    graph_pass ? "QwenModel::decode_greedy (graph replay), wall clock"
+                               : "forward_token loop, wall clock (--no-graph)",
                     step_bytes / (decode_ms * 1e-3 / steps) / 1e9, steps / (eager_ms * 1e-3), eager_ms / steps,
                     eager_wall * 1e3 / steps, match ? "true" : "false", prompt / (prompt_ms * 1e-3),
                     prompt_wall * 1e3 / prompt, setup_s, (unsigned long long)checksum);

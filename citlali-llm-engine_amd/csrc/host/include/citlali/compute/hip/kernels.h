@@ -56,6 +56,27 @@ void launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v
 // type is not Q4_K/Q6_K or no grouped kernel covers in_features.
 bool launch_matvec_group(int count, const GgufTensorType* types, const uint8_t* const* weights,
                          const uint16_t* input, uint16_t* const* outputs, const int* out_features, int in_features);
+// GEMVs whose input is the residual add + RMSNorm of `input` (see
+// citlali_hip_norm): the input fp16(s * rsqrt(mean(s^2) + eps) * weight),
+// s = fp16(input + delta) (s = input without delta), is formed inside each
+// launch, and sum_out (may be null) receives s.  The same results as
+// launch_add_rms_norm / launch_rms_norm followed by the GEMV, bit for bit.
+// Each returns false, launching nothing, when no kernel covers the shape or
+// type.
+struct NormInput {
+    const uint16_t* delta;
+    const uint16_t* weight;
+    uint16_t* sum_out;
+    float eps;
+};
+bool launch_matvec_group_norm(int count, const GgufTensorType* types, const uint8_t* const* weights,
+                              const uint16_t* input, const NormInput& norm, uint16_t* const* outputs,
+                              const int* out_features, int in_features);
+bool launch_matvec_gate_up_swiglu_norm(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
+                                       const uint16_t* input, const NormInput& norm, uint16_t* output,
+                                       int in_features, int out_features);
+bool launch_matvec_norm(GgufTensorType type, const uint8_t* weight, const uint16_t* input, const NormInput& norm,
+                        void* output, bool f32_out, int in_features, int out_features);
 // The ffn_gate and ffn_up GEMVs (both of `type`) then launch_swiglu; returns
 // false, launching nothing, when no fused kernel covers the shape.
 bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,

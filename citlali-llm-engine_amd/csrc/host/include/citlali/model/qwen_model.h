@@ -9,6 +9,7 @@
 // (qwen_model.cpp:448-465) on the device and copies back one index.
 #pragma once
 
+#include "citlali/compute/hip/kernels.h"
 #include "citlali/compute/hip/tensor.h"
 #include "citlali/model/linear_backend.h"
 #include "citlali/model/qwen_config.h"
@@ -74,7 +75,8 @@ public:
 
 private:
     void allocate_runtime_buffers();
-    bool launch_qkv_grouped(const QwenLayerWeights& layer, int hidden);
+    bool launch_qkv_grouped(const QwenLayerWeights& layer, int hidden, const uint16_t* input,
+                            const compute::NormInput* norm);
     void enqueue_token(int32_t token_id, int position, int32_t* state, int plan_length, bool compute_logits);
     void* step_graph(int plan_length);
     void release_graphs() noexcept;
@@ -87,7 +89,7 @@ private:
     WeightHandle output_weight_;
     std::vector<QwenLayerWeights> layers_;
 
-    compute::DeviceBufferPtr x_, norm_, q_, k_, v_, attn_out_, attn_proj_;
+    compute::DeviceBufferPtr x_, x_alt_, norm_, q_, k_, v_, attn_out_, attn_proj_;
     compute::DeviceBufferPtr gate_, up_, ff_act_, ff_out_, logits_, scores_, next_token_;
     compute::DeviceBufferPtr state_, tokens_;   // decode_greedy: {token, position, step, 0}, picks
     std::unique_ptr<LinearBackend> linear_backend_;

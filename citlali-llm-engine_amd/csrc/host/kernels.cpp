@@ -108,6 +108,47 @@ bool launch_matvec_group(int count, const GgufTensorType* types, const uint8_t* 
     return true;
 }
 
+namespace {
+citlali_hip_norm to_abi(const NormInput& n) { return citlali_hip_norm{n.delta, n.weight, n.sum_out, n.eps}; }
+bool kquant(GgufTensorType t) { return t == GgufTensorType::Q4_K || t == GgufTensorType::Q6_K; }
+bool launched(int st) {
+    if (st == CITLALI_ERR_UNSUPPORTED) return false;
+    CITLALI_HIP_CHECK(st);
+    return true;
+}
+}  // namespace
+
+bool launch_matvec_group_norm(int count, const GgufTensorType* types, const uint8_t* const* weights,
+                              const uint16_t* input, const NormInput& norm, uint16_t* const* outputs,
+                              const int* out_features, int in_features) {
+    require(count >= 1 && count <= 3, "launch_matvec_group_norm: count must be 1, 2 or 3");
+    int codes[3];
+    for (int i = 0; i < count; ++i) {
+        if (!kquant(types[i])) return false;
+        codes[i] = static_cast<int>(types[i]);
+    }
+    const citlali_hip_norm n = to_abi(norm);
+    return launched(citlali_hip_matvec_group_norm(count, codes, weights, input, &n, outputs, out_features,
+                                                  in_features));
+}
+
+bool launch_matvec_gate_up_swiglu_norm(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
+                                       const uint16_t* input, const NormInput& norm, uint16_t* output,
+                                       int in_features, int out_features) {
+    if (!kquant(type)) return false;
+    const citlali_hip_norm n = to_abi(norm);
+    return launched(citlali_hip_matvec_gate_up_swiglu_norm(static_cast<int>(type), w_gate, w_up, input, &n, output,
+                                                           in_features, out_features));
+}
+
+bool launch_matvec_norm(GgufTensorType type, const uint8_t* weight, const uint16_t* input, const NormInput& norm,
+                        void* output, bool f32_out, int in_features, int out_features) {
+    if (!kquant(type)) return false;
+    const citlali_hip_norm n = to_abi(norm);
+    return launched(citlali_hip_matvec_norm(static_cast<int>(type), weight, input, &n, output, f32_out ? 1 : 0,
+                                            in_features, out_features));
+}
+
 bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
                                   const uint16_t* input, uint16_t* output, int in_features, int out_features) {
     if (type != GgufTensorType::Q4_K && type != GgufTensorType::Q6_K) return false;

@@ -91,6 +91,7 @@ void QwenModel::allocate_runtime_buffers() {
     const size_t kv = static_cast<size_t>(config_.head_count_kv) * config_.head_dim;
     const size_t ff = config_.feed_forward_length;
     x_ = compute::make_device_half_buffer(hidden);
+    x_alt_ = compute::make_device_half_buffer(hidden);   // the residual stream alternates between the two
     norm_ = compute::make_device_half_buffer(hidden);
     q_ = compute::make_device_half_buffer(q);
     k_ = compute::make_device_half_buffer(kv);
@@ -118,10 +119,12 @@ void QwenModel::allocate_runtime_buffers() {
 }
 
 // attn_q, attn_k and attn_v in one launch when all three are Q4_K/Q6_K
-// device tensors (the separate GEMVs' results bit for bit); false, nothing
+// device tensors (the separate GEMVs' results bit for bit), reading `input`
+// or, with `norm`, the residual add + RMSNorm of it; false, nothing
 // launched, otherwise -- then LinearBackend::forward runs (and reports what
 // it rejects).  The bias adds that follow are independent of order.
-bool QwenModel::launch_qkv_grouped(const QwenLayerWeights& layer, int hidden) {
+bool QwenModel::launch_qkv_grouped(const QwenLayerWeights& layer, int hidden, const uint16_t* input,
+                                   const compute::NormInput* norm) {
     const WeightHandle* w[3] = {&layer.attn_q, &layer.attn_k, &layer.attn_v};
     const compute::DeviceBufferPtr* out[3] = {&q_, &k_, &v_};
     compute::GgufTensorType types[3];
@@ -138,7 +141,8 @@ bool QwenModel::launch_qkv_grouped(const QwenLayerWeights& layer, int hidden) {
         outputs[i] = (*out[i])->half_data();
         rows[i] = as_int(w[i]->rows(), w[i]->name + " rows");
     }
-    return compute::launch_matvec_group(3, types, weights, norm_->half_data(), outputs, rows, hidden);
+    if (norm) return compute::launch_matvec_group_norm(3, types, weights, input, *norm, outputs, rows, hidden);
+    return compute::launch_matvec_group(3, types, weights, input, outputs, rows, hidden);
 }
 
 int32_t QwenModel::forward_token(int32_t token_id, uint32_t position, bool compute_logits) {
@@ -180,22 +184,41 @@ void QwenModel::enqueue_token(int32_t token_id, int pos, int32_t* state, int pla
             compute::launch_embed(token_embedding_.device_half_data(), token_id, x_->half_data(), hidden);
     }
 
-    // The reference's per-layer sequence, with three groups of its launches
-    // done by fused kernels that give the same results bit for bit: the
-    // residual add with the RMSNorm that follows it, the q/k head norms with
-    // RoPE and the KV store, and (when gate and up share a type and have no
-    // bias) the gate/up GEMVs with SwiGLU.
-    bool normed = false;   // norm_ already holds this layer's attn_norm(x)
+    // The reference's per-layer sequence.  Its launches are grouped or fused
+    // where a kernel gives the same results bit for bit: attn_q/k/v in one
+    // launch; each residual add + RMSNorm inside the GEMV launch that reads
+    // the normed vector (its workgroups form the input themselves, and the
+    // sum goes to the other residual buffer); the q/k head norms with RoPE
+    // and the KV store; gate/up with SwiGLU.  Where no such kernel covers a
+    // shape, the add + norm runs as its own launch into norm_.
+    const float eps = config_.rms_norm_eps;
+    uint16_t* xr[2] = {x_->half_data(), x_alt_->half_data()};
+    int cur = 0;                          // xr[cur] is the residual stream
+    const uint16_t* pending = nullptr;    // ffn_down output not yet added to it
+    auto prologue = [&](const WeightHandle& w, const uint16_t* delta) {
+        return compute::NormInput{delta, w.device_half_data(), delta ? xr[1 - cur] : nullptr, eps};
+    };
+    auto norm_into_buffer = [&](const WeightHandle& w, const uint16_t* delta) {
+        if (delta)
+            compute::launch_add_rms_norm(xr[cur], delta, w.device_half_data(), norm_->half_data(), hidden, eps);
+        else
+            compute::launch_rms_norm(xr[cur], w.device_half_data(), norm_->half_data(), hidden, eps);
+    };
+
     for (size_t li = 0; li < layers_.size(); ++li) {
         QwenLayerWeights& layer = layers_[li];
-        if (!normed)
-            compute::launch_rms_norm(x_->half_data(), layer.attn_norm.device_half_data(), norm_->half_data(),
-                                     hidden, config_.rms_norm_eps);
-        if (!launch_qkv_grouped(layer, hidden)) {
-            linear_backend_->forward(layer.attn_q, norm_, q_);
-            linear_backend_->forward(layer.attn_k, norm_, k_);
-            linear_backend_->forward(layer.attn_v, norm_, v_);
+        const compute::NormInput attn_in = prologue(layer.attn_norm, pending);
+        if (launch_qkv_grouped(layer, hidden, xr[cur], &attn_in)) {
+            if (pending) cur ^= 1;
+        } else {
+            norm_into_buffer(layer.attn_norm, pending);
+            if (!launch_qkv_grouped(layer, hidden, norm_->half_data(), nullptr)) {
+                linear_backend_->forward(layer.attn_q, norm_, q_);
+                linear_backend_->forward(layer.attn_k, norm_, k_);
+                linear_backend_->forward(layer.attn_v, norm_, v_);
+            }
         }
+        pending = nullptr;
         add_bias_if_present(layer.attn_q_bias, q_, static_cast<uint64_t>(heads) * head_dim);
         add_bias_if_present(layer.attn_k_bias, k_, static_cast<uint64_t>(kv_heads) * head_dim);
         add_bias_if_present(layer.attn_v_bias, v_, static_cast<uint64_t>(kv_heads) * head_dim);
@@ -204,67 +227,68 @@ void QwenModel::enqueue_token(int32_t token_id, int pos, int32_t* state, int pla
         if (state) {
             compute::launch_qk_norm_rope_store_at(q_->half_data(), k_->half_data(), v_->half_data(), q_norm, k_norm,
                                                   heads, kv_heads, head_dim, state_position,
-                                                  static_cast<int>(max_context_), config_.rope_theta,
-                                                  config_.rms_norm_eps, layer.k_cache->half_data(),
-                                                  layer.v_cache->half_data());
+                                                  static_cast<int>(max_context_), config_.rope_theta, eps,
+                                                  layer.k_cache->half_data(), layer.v_cache->half_data());
             compute::launch_attention_at(q_->half_data(), layer.k_cache->half_data(), layer.v_cache->half_data(),
                                          state_position, plan_length, static_cast<float*>(scores_->data()),
                                          scores_->bytes(), attn_out_->half_data(), heads, kv_heads, head_dim);
         } else {
             compute::launch_qk_norm_rope_store(q_->half_data(), k_->half_data(), v_->half_data(), q_norm, k_norm,
-                                               heads, kv_heads, head_dim, pos, config_.rope_theta,
-                                               config_.rms_norm_eps, layer.k_cache->half_data(),
-                                               layer.v_cache->half_data());
+                                               heads, kv_heads, head_dim, pos, config_.rope_theta, eps,
+                                               layer.k_cache->half_data(), layer.v_cache->half_data());
             compute::launch_attention(q_->half_data(), layer.k_cache->half_data(), layer.v_cache->half_data(),
                                       static_cast<float*>(scores_->data()), attn_out_->half_data(), pos,
                                       static_cast<int>(max_context_), heads, kv_heads, head_dim);
         }
         linear_backend_->forward(layer.attn_o, attn_out_, attn_proj_);
         add_bias_if_present(layer.attn_o_bias, attn_proj_, hidden);
-        compute::launch_add_rms_norm(x_->half_data(), attn_proj_->half_data(), layer.ffn_norm.device_half_data(),
-                                     norm_->half_data(), hidden, config_.rms_norm_eps);
+
         const bool fuse_ffn = layer.ffn_gate.storage_kind == compute::WeightStorageKind::QuantizedDevice &&
                               layer.ffn_up.storage_kind == compute::WeightStorageKind::QuantizedDevice &&
                               layer.ffn_gate.gguf_type == layer.ffn_up.gguf_type && !layer.ffn_gate_bias.buffer &&
                               !layer.ffn_up_bias.buffer;
-        if (!fuse_ffn || !compute::launch_matvec_gate_up_swiglu(layer.ffn_gate.gguf_type,
-                                                                layer.ffn_gate.device_quantized_data(),
-                                                                layer.ffn_up.device_quantized_data(),
-                                                                norm_->half_data(), ff_act_->half_data(), hidden, ff)) {
-            linear_backend_->forward(layer.ffn_gate, norm_, gate_);
-            add_bias_if_present(layer.ffn_gate_bias, gate_, ff);
-            linear_backend_->forward(layer.ffn_up, norm_, up_);
-            add_bias_if_present(layer.ffn_up_bias, up_, ff);
-            compute::launch_swiglu(gate_->half_data(), up_->half_data(), ff_act_->half_data(), ff);
+        const compute::NormInput ffn_in = prologue(layer.ffn_norm, attn_proj_->half_data());
+        if (fuse_ffn && compute::launch_matvec_gate_up_swiglu_norm(layer.ffn_gate.gguf_type,
+                                                                   layer.ffn_gate.device_quantized_data(),
+                                                                   layer.ffn_up.device_quantized_data(), xr[cur],
+                                                                   ffn_in, ff_act_->half_data(), hidden, ff)) {
+            cur ^= 1;
+        } else {
+            norm_into_buffer(layer.ffn_norm, attn_proj_->half_data());
+            if (!fuse_ffn || !compute::launch_matvec_gate_up_swiglu(layer.ffn_gate.gguf_type,
+                                                                    layer.ffn_gate.device_quantized_data(),
+                                                                    layer.ffn_up.device_quantized_data(),
+                                                                    norm_->half_data(), ff_act_->half_data(), hidden,
+                                                                    ff)) {
+                linear_backend_->forward(layer.ffn_gate, norm_, gate_);
+                add_bias_if_present(layer.ffn_gate_bias, gate_, ff);
+                linear_backend_->forward(layer.ffn_up, norm_, up_);
+                add_bias_if_present(layer.ffn_up_bias, up_, ff);
+                compute::launch_swiglu(gate_->half_data(), up_->half_data(), ff_act_->half_data(), ff);
+            }
         }
         linear_backend_->forward(layer.ffn_down, ff_act_, ff_out_);
         add_bias_if_present(layer.ffn_down_bias, ff_out_, hidden);
-        // residual add, fused with the norm that reads x next when there is one
-        const WeightHandle* next_norm = li + 1 < layers_.size() ? &layers_[li + 1].attn_norm
-                                        : compute_logits             ? &output_norm_
-                                                                     : nullptr;
-        if (next_norm) {
-            compute::launch_add_rms_norm(x_->half_data(), ff_out_->half_data(), next_norm->device_half_data(),
-                                         norm_->half_data(), hidden, config_.rms_norm_eps);
-            normed = true;
-        } else {
-            compute::launch_add_inplace(x_->half_data(), ff_out_->half_data(), hidden);
-            normed = false;
-        }
+        pending = ff_out_->half_data();
     }
+    // without logits nothing reads the last residual add
     if (!compute_logits) return;
 
-    if (!normed)
-        compute::launch_rms_norm(x_->half_data(), output_norm_.device_half_data(), norm_->half_data(), hidden,
-                                 config_.rms_norm_eps);
+    float* logits = static_cast<float*>(logits_->data());
+    const compute::NormInput out_in = prologue(output_norm_, pending);
     if (output_weight_.storage_kind == compute::WeightStorageKind::QuantizedDevice) {
         if (output_weight_.gguf_type != compute::GgufTensorType::Q6_K)
             throw Error("unsupported quantized output weight type: " + compute::to_string(output_weight_.gguf_type));
-        compute::launch_matvec_q6k_to_float(output_weight_.device_quantized_data(), norm_->half_data(),
-                                            static_cast<float*>(logits_->data()), hidden, vocab);
+        if (!compute::launch_matvec_norm(output_weight_.gguf_type, output_weight_.device_quantized_data(), xr[cur],
+                                         out_in, logits, true, hidden, vocab)) {
+            norm_into_buffer(output_norm_, pending);
+            compute::launch_matvec_q6k_to_float(output_weight_.device_quantized_data(), norm_->half_data(), logits,
+                                                hidden, vocab);
+        }
     } else {
-        compute::launch_matvec_fp16_to_float(output_weight_.device_half_data(), norm_->half_data(),
-                                             static_cast<float*>(logits_->data()), hidden, vocab);
+        norm_into_buffer(output_norm_, pending);
+        compute::launch_matvec_fp16_to_float(output_weight_.device_half_data(), norm_->half_data(), logits, hidden,
+                                             vocab);
     }
     if (state)
         compute::launch_argmax_advance(static_cast<const float*>(logits_->data()), vocab, state,

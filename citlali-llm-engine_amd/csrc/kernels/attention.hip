@@ -321,10 +321,13 @@ typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 constexpr int kMTile = 16;                     // positions per MFMA tile
 constexpr int kMStride = 128 + 8;              // V tile row in LDS (halves)
 constexpr size_t kMWaveLds = (size_t)kMTile * kMStride * 2;
-// merge: (max, sum)[kWaves][8], acc[kWaves][2 row groups][8 blocks][16 cols][4]
-constexpr size_t kMMlFloats = (size_t)kWaves * 8 * 2;
-constexpr size_t kMLds = (kMMlFloats + (size_t)kWaves * 2 * 8 * 16 * 4) * sizeof(float);
-constexpr size_t kMfmaLds = kMLds > kMWaveLds * kWaves ? kMLds : kMWaveLds * kWaves;
+// merge: (max, sum)[NW][8], acc[NW][2 row groups][8 blocks][16 cols][4]
+template <int NW>
+struct MfmaLds {
+    static constexpr size_t kMlFloats = (size_t)NW * 8 * 2;
+    static constexpr size_t kMerge = (kMlFloats + (size_t)NW * 2 * 8 * 16 * 4) * sizeof(float);
+    static constexpr size_t kBytes = kMerge > kMWaveLds * NW ? kMerge : kMWaveLds * NW;
+};
 
 __device__ __forceinline__ f32x4 mfma16(half4 a, half4 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
@@ -334,8 +337,8 @@ __device__ __forceinline__ half4 as_half4(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(half4, u32x2{lo, hi});
 }
 
-template <int GP, int kDepth>
-__global__ __launch_bounds__(kBlock) void attn_mfma_kernel(
+template <int GP, int kDepth, int NW>
+__global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     long long seq_stride, const int32_t* __restrict__ positions, int position, int max_len, int heads,
     int kv_heads, int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits,
@@ -354,7 +357,7 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int col = lane & 15, grp = lane >> 4;
-    const int sub = (((b1 - b0 + kWaves - 1) / kWaves + kMTile - 1) / kMTile) * kMTile;
+    const int sub = (((b1 - b0 + NW - 1) / NW + kMTile - 1) / kMTile) * kMTile;
     const int w0 = min(b1, b0 + wave * sub);
     const int w1 = min(b1, w0 + sub);
 
@@ -471,10 +474,10 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(
         for (int d = 0; d < kDepth; ++d) process(d, t0 + d * kMTile);
     }
 
-    // ---- merge the four waves in LDS ----
+    // ---- merge the waves in LDS ----
     __syncthreads();   // every wave is done with its V tile
-    float* ml = reinterpret_cast<float*>(smem);   // [kWaves][8] (max, sum)
-    float* ms = ml + kMMlFloats;                  // [kWaves][2][8][16][4]
+    float* ml = reinterpret_cast<float*>(smem);   // [NW][8] (max, sum)
+    float* ms = ml + MfmaLds<NW>::kMlFloats;      // [NW][2][8][16][4]
     if (grp == 0 && col < GP) {
         ml[(wave * 8 + col) * 2] = m_run;
         ml[(wave * 8 + col) * 2 + 1] = l_run;
@@ -486,16 +489,16 @@ __global__ __launch_bounds__(kBlock) void attn_mfma_kernel(
     }
     __syncthreads();
 
-    for (int idx = threadIdx.x; idx < group * HD; idx += kBlock) {
+    for (int idx = threadIdx.x; idx < group * HD; idx += NW * kWave) {
         const int h = idx / HD, dim = idx - h * HD;
         const int hg = h >> 2, hi = h & 3;
         const int b = 4 * (dim >> 6) + (dim & 3), c16 = (dim & 63) >> 2;
         float M = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) M = fmaxf(M, ml[(w * 8 + h) * 2]);
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, ml[(w * 8 + h) * 2]);
         float Ls = 0.f, A = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float mw = ml[(w * 8 + h) * 2];
             const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
             Ls += ml[(w * 8 + h) * 2 + 1] * f;
@@ -584,11 +587,11 @@ hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream
     return hipGetLastError();
 }
 
-template <int GP, int kDepth>
+template <int GP, int kDepth, int NW = kWaves>
 hipError_t launch_mfma(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
     const float scale_log2 = (float)(1.4426950408889634 / sqrt(128.0));
-    launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth>), dim3(p.n_splits, a.kv_heads, a.nseq),
-                          dim3(kBlock), kMfmaLds, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
+    launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth, NW>), dim3(p.n_splits, a.kv_heads, a.nseq),
+                          dim3(NW * kWave), MfmaLds<NW>::kBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
                           a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
                           a.workspace, p.n_splits, a.out);
     const hipError_t e = hipGetLastError();

@@ -137,6 +137,48 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// ---- residual add + RMSNorm in runs of eight fp16 values -----------------
+// The order shared by add_rms_norm_kernel and the GEMV input prologue: in a
+// 256-thread block, thread t owns runs t, t + 256, ...; xs = fp16(x + d)
+// (xs = x without d); its sum of squares runs over its runs, then its eight
+// values, in order; then wave_sum and the four wave sums in order.
+constexpr int kNormThreads = 256;
+
+__device__ __forceinline__ uint32_t add_pair(uint32_t x, uint32_t d) {
+    const uint32_t lo = f2h_rne(h2f(x & 0xffffu) + h2f(d & 0xffffu));
+    const uint32_t hi = f2h_rne(h2f(x >> 16) + h2f(d >> 16));
+    return lo | (hi << 16);
+}
+__device__ __forceinline__ u32x4 add_run(u32x4 x, u32x4 d, bool has_d) {
+    if (!has_d) return x;
+    return u32x4{add_pair(x.x, d.x), add_pair(x.y, d.y), add_pair(x.z, d.z), add_pair(x.w, d.w)};
+}
+__device__ __forceinline__ float sq_pair(uint32_t v, float s) {
+    const float a = h2f(v & 0xffffu), b = h2f(v >> 16);
+    s += a * a;
+    return s + b * b;
+}
+__device__ __forceinline__ float sq_run(u32x4 v, float s) {
+    return sq_pair(v.w, sq_pair(v.z, sq_pair(v.y, sq_pair(v.x, s))));
+}
+__device__ __forceinline__ uint32_t norm_pair(uint32_t v, uint32_t w, float inv) {
+    const uint32_t lo = f2h_rne(h2f(v & 0xffffu) * inv * h2f(w & 0xffffu));
+    const uint32_t hi = f2h_rne(h2f(v >> 16) * inv * h2f(w >> 16));
+    return lo | (hi << 16);
+}
+__device__ __forceinline__ u32x4 norm_run(u32x4 v, u32x4 w, float inv) {
+    return u32x4{norm_pair(v.x, w.x, inv), norm_pair(v.y, w.y, inv), norm_pair(v.z, w.z, inv),
+                 norm_pair(v.w, w.w, inv)};
+}
+// Sum over the 256 threads; `red` holds 4 floats of LDS.  LDS-only barriers,
+// so global loads in flight stay in flight.
+__device__ __forceinline__ float norm_block_sum(float s, float* red) {
+    s = wave_sum(s);
+    if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = s;
+    lds_barrier();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
 // Orders LDS traffic between lanes of one wave (no workgroup barrier): the
 // fence makes earlier LDS writes visible, the wave barrier stops the compiler
 // from moving memory operations across this point.

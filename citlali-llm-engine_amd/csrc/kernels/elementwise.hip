@@ -61,8 +61,8 @@ __device__ float block_sum(float v, float* red) {
     return s;
 }
 
-// one block per vector (rms_norm: 1 vector; rms_norm_heads: `heads` vectors,
-// weight shared by all heads)
+// one block per head (rms_norm_heads: `heads` vectors, weight shared by all
+// heads)
 __global__ void rms_norm_kernel(const uint16_t* __restrict__ in, const uint16_t* __restrict__ w,
                                 uint16_t* __restrict__ out, int n, float eps) {
     __shared__ float red[16];
@@ -77,25 +77,62 @@ __global__ void rms_norm_kernel(const uint16_t* __restrict__ in, const uint16_t*
     for (int i = threadIdx.x; i < n; i += blockDim.x) out[base + i] = f2h_rne(h2f(in[base + i]) * inv * h2f(w[i]));
 }
 
+// RMSNorm of one vector (launch_rms_norm, kernels.cu:67-92) in the run order
+// of device_common.hpp shared with add_rms_norm_kernel and the GEMV input
+// prologue, so the three agree bit for bit.
+__global__ __launch_bounds__(kNormThreads) void rms_norm_vec_kernel(const uint16_t* __restrict__ in,
+                                                                    const uint16_t* __restrict__ w,
+                                                                    uint16_t* __restrict__ out, int n, float eps) {
+    __shared__ float red[4];
+    float s = 0.f;
+    for (int r = threadIdx.x; r * 8 < n; r += kNormThreads)
+        for (int j = 0; j < 8; ++j) {
+            const int i = r * 8 + j;
+            if (i < n) {
+                const float v = h2f(in[i]);
+                s += v * v;
+            }
+        }
+    s = norm_block_sum(s, red);
+    const float inv = rsqrtf(s / (float)n + eps);
+    for (int r = threadIdx.x; r * 8 < n; r += kNormThreads)
+        for (int j = 0; j < 8; ++j) {
+            const int i = r * 8 + j;
+            if (i < n) out[i] = f2h_rne(h2f(in[i]) * inv * h2f(w[i]));
+        }
+}
+
 // Residual add then RMSNorm of the sum, one launch for the reference's
 // launch_add_inplace + launch_rms_norm pair (qwen_model.cpp:340-341, 372 and
 // the next layer's 306 or the final norm at 385): x = fp16(x + d) is stored,
 // then norm = fp16(x * rsqrt(mean(x^2) + eps) * w) over the stored values.
-// Same single 1024-thread block and reduction order as rms_norm_kernel, so
-// the results equal the two separate launches bit for bit.
-__global__ void add_rms_norm_kernel(uint16_t* __restrict__ x, const uint16_t* __restrict__ d,
-                                    const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int n, float eps) {
-    __shared__ float red[16];
+// One 256-thread block in the order of device_common.hpp's run helpers --
+// the order the GEMVs' norm prologue uses, so a GEMV fed by this kernel and
+// the GEMV with the prologue give the same results bit for bit.
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(uint16_t* __restrict__ x,
+                                                                    const uint16_t* __restrict__ d,
+                                                                    const uint16_t* __restrict__ w,
+                                                                    uint16_t* __restrict__ out, int n, float eps) {
+    __shared__ float red[4];
     float s = 0.f;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) {
-        const uint16_t xi = f2h_rne(h2f(x[i]) + h2f(d[i]));
-        x[i] = xi;
-        const float v = h2f(xi);
-        s += v * v;
+    for (int r = threadIdx.x; r * 8 < n; r += kNormThreads) {
+        for (int j = 0; j < 8; ++j) {
+            const int i = r * 8 + j;
+            if (i < n) {
+                const uint16_t xi = f2h_rne(h2f(x[i]) + h2f(d[i]));
+                x[i] = xi;
+                const float v = h2f(xi);
+                s += v * v;
+            }
+        }
     }
-    s = block_sum(s, red);
+    s = norm_block_sum(s, red);
     const float inv = rsqrtf(s / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = f2h_rne(h2f(x[i]) * inv * h2f(w[i]));
+    for (int r = threadIdx.x; r * 8 < n; r += kNormThreads)
+        for (int j = 0; j < 8; ++j) {
+            const int i = r * 8 + j;
+            if (i < n) out[i] = f2h_rne(h2f(x[i]) * inv * h2f(w[i]));
+        }
 }
 
 // Per-head RMSNorm of q and k (when their weights are given), NeoX RoPE of
@@ -338,7 +375,7 @@ hipError_t launch_add_inplace(uint16_t* t, const uint16_t* d, int n, hipStream_t
 }
 
 hipError_t launch_rms_norm(const uint16_t* in, const uint16_t* w, uint16_t* out, int n, float eps, hipStream_t s) {
-    launch_kernel(rms_norm_kernel, dim3(1), dim3(1024), 0, s, in, w, out, n, eps);
+    launch_kernel(rms_norm_vec_kernel, dim3(1), dim3(kNormThreads), 0, s, in, w, out, n, eps);
     return hipGetLastError();
 }
 
@@ -350,7 +387,7 @@ hipError_t launch_rms_norm_heads(const uint16_t* in, const uint16_t* w, uint16_t
 
 hipError_t launch_add_rms_norm(uint16_t* x, const uint16_t* d, const uint16_t* w, uint16_t* out, int n, float eps,
                                hipStream_t s) {
-    launch_kernel(add_rms_norm_kernel, dim3(1), dim3(1024), 0, s, x, d, w, out, n, eps);
+    launch_kernel(add_rms_norm_kernel, dim3(1), dim3(kNormThreads), 0, s, x, d, w, out, n, eps);
     return hipGetLastError();
 }
 

@@ -108,10 +108,23 @@ hipError_t launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint1
                                      const uint16_t* kw, int heads, int kv_heads, int head_dim, int position,
                                      const int32_t* position_at, int max_positions, float theta, float eps,
                                      uint16_t* k_cache, uint16_t* v_cache, hipStream_t s);
+// GEMV input prologue (residual add + RMSNorm): the GEMV reads
+// fp16(xs * rsqrt(mean(xs^2) + eps) * w) with xs = fp16(x + d) (xs = x when
+// d is null); workgroup 0 stores xs to xs_out when that is not null.  Equal
+// bit for bit to launch_add_rms_norm followed by the plain GEMV.
+struct NormIn {
+    const uint16_t* d;
+    const uint16_t* w;
+    uint16_t* xs_out;
+    float eps;
+};
 hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const* w, const uint16_t* x,
-                               uint16_t* const* y, const int* n, int K, hipStream_t s);
+                               uint16_t* const* y, const int* n, int K, const NormIn* norm, hipStream_t s);
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
-                                        uint16_t* act, int K, int N, hipStream_t s);
+                                        uint16_t* act, int K, int N, const NormIn* norm, hipStream_t s);
+// kind 4 / 6 GEMV with the input prologue; K a multiple of 4096 up to 16384
+hipError_t launch_matvec_norm(int kind, const uint8_t* w, const uint16_t* x, const NormIn& norm, void* y,
+                              bool f32_out, int K, int N, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);
 hipError_t launch_stream_read(const void* buf, size_t bytes, uint32_t* sink, hipStream_t s);
 

@@ -78,15 +78,47 @@ __device__ __forceinline__ void stage_x8(const u32x4 raw, int v8, uint32_t* xp, 
 // x staging split in two so its global loads can be issued before the weight
 // loads: vmcnt retires loads in order, so x issued last would wait for every
 // weight load.  kIter = K / (8 * kBlock) runs of eight values per thread.
-template <int kLayout, int kIter>
+// kNorm: the staged input is the residual add + RMSNorm of x (NormIn, in the
+// run order of device_common.hpp; d, w and xs_out 16-byte aligned), its
+// loads issued with x's; `red` is 4 floats of LDS.
+template <int kLayout, int kIter, bool kNorm = false>
 struct XStage {
     u32x4 raw[kIter];
-    __device__ __forceinline__ void load(const uint16_t* __restrict__ x) {
+    u32x4 dr[kNorm ? kIter : 1], wr[kNorm ? kIter : 1];
+    __device__ __forceinline__ void load(const uint16_t* __restrict__ x, const NormIn& n) {
 #pragma unroll
         for (int i = 0; i < kIter; ++i)
             raw[i] = *reinterpret_cast<const u32x4*>(x + ((size_t)i * kBlock + threadIdx.x) * 8);
+        if constexpr (kNorm) {
+            // branch-free: without d the loads re-read x (unused)
+            const uint16_t* dp = n.d ? n.d : x;
+#pragma unroll
+            for (int i = 0; i < kIter; ++i) {
+                dr[i] = *reinterpret_cast<const u32x4*>(dp + ((size_t)i * kBlock + threadIdx.x) * 8);
+                wr[i] = *reinterpret_cast<const u32x4*>(n.w + ((size_t)i * kBlock + threadIdx.x) * 8);
+            }
+        }
     }
-    __device__ __forceinline__ void store(uint32_t* xp, float* sx) const {
+    __device__ __forceinline__ void store(uint32_t* xp, float* sx, float* red, const NormIn& n) {
+        if constexpr (kNorm) {
+            static_assert(kBlock == kNormThreads, "norm order");
+            const bool has_d = n.d != nullptr;
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < kIter; ++i) {
+                raw[i] = add_run(raw[i], dr[i], has_d);
+                s = sq_run(raw[i], s);
+            }
+            if (n.xs_out && blockIdx.x == 0) {
+#pragma unroll
+                for (int i = 0; i < kIter; ++i)
+                    *reinterpret_cast<u32x4*>(n.xs_out + ((size_t)i * kBlock + threadIdx.x) * 8) = raw[i];
+            }
+            s = norm_block_sum(s, red);
+            const float inv = rsqrtf(s / (float)(kIter * kBlock * 8) + n.eps);
+#pragma unroll
+            for (int i = 0; i < kIter; ++i) raw[i] = norm_run(raw[i], wr[i], inv);
+        }
 #pragma unroll
         for (int i = 0; i < kIter; ++i) stage_x8<kLayout>(raw[i], i * kBlock + threadIdx.x, xp, sx);
         lds_barrier();
@@ -280,9 +312,9 @@ struct RowSet {
 // last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave
 // computes its M rows (all loaded up front) and stops; the grid then has
 // M * W >= rows.
-template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true>
+template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false>
 __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __restrict__ x, int K, uint8_t* smem,
-                                            int gw, int W) {
+                                            int gw, int W, const NormIn& nrm) {
     constexpr int nb = S * QT::kSbPerStep;   // K = 256 nb
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
@@ -304,8 +336,8 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
         return QT::load(w + f * QT::kBytes, l4);
     };
 
-    XStage<QT::kSumLayout, nb / 8> xs;   // nb / 8 runs of eight values per thread
-    xs.load(x);
+    XStage<QT::kSumLayout, nb / 8, kNorm> xs;   // nb / 8 runs of eight values per thread
+    xs.load(x, nrm);
     __builtin_amdgcn_sched_barrier(0);   // issue order: x, first fragments, staging
     typename QT::Frag fr[D];
 #pragma unroll
@@ -315,7 +347,7 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
             fr[m * S + t] = frag_at(gw + m * W, t);
             __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
         }
-    xs.store(xp, sx);
+    xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
 
     for (int row = gw; row < N; row += M * W) {
 #pragma unroll
@@ -344,27 +376,30 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
     }
 }
 
-template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true>
-__global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_stream_kernel(RowSet rs, const uint16_t* __restrict__ x, int K) {
+template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false>
+__global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_stream_kernel(RowSet rs, const uint16_t* __restrict__ x,
+                                                                             int K, NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
-    stream_rows<QT, kF32, S, M, kSegs, kRefill>(rs, x, K, smem, blockIdx.x * kWavesPerBlock + threadIdx.x / kWave,
-                                       gridDim.x * kWavesPerBlock);
+    stream_rows<QT, kF32, S, M, kSegs, kRefill, kNorm>(rs, x, K, smem,
+                                                       blockIdx.x * kWavesPerBlock + threadIdx.x / kWave,
+                                                       gridDim.x * kWavesPerBlock, nrm);
 }
 
 // Two row sets of different types in one launch: blocks [0, blocks_a) walk
 // set `a` (type QA), the rest walk set `b` (type QB).  Each row is computed
 // exactly as the single-matrix launch computes it.
-template <class QA, class QB, int S, int M, bool kRefill = true>
+template <class QA, class QB, int S, int M, bool kRefill = true, bool kNorm = false>
 __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_group_kernel(RowSet a, RowSet b, int blocks_a,
-                                                              const uint16_t* __restrict__ x, int K) {
+                                                                            const uint16_t* __restrict__ x, int K,
+                                                                            NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int wave = threadIdx.x / kWave;
     if ((int)blockIdx.x < blocks_a)
-        stream_rows<QA, false, S, M, 3, kRefill>(a, x, K, smem, blockIdx.x * kWavesPerBlock + wave,
-                                                 blocks_a * kWavesPerBlock);
+        stream_rows<QA, false, S, M, 3, kRefill, kNorm>(a, x, K, smem, blockIdx.x * kWavesPerBlock + wave,
+                                                        blocks_a * kWavesPerBlock, nrm);
     else
-        stream_rows<QB, false, S, M, 3, kRefill>(b, x, K, smem, (blockIdx.x - blocks_a) * kWavesPerBlock + wave,
-                                        (gridDim.x - blocks_a) * kWavesPerBlock);
+        stream_rows<QB, false, S, M, 3, kRefill, kNorm>(b, x, K, smem, (blockIdx.x - blocks_a) * kWavesPerBlock + wave,
+                                                        (gridDim.x - blocks_a) * kWavesPerBlock, nrm);
 }
 
 // ffn_gate and ffn_up GEMVs plus SwiGLU in one launch (the reference's two
@@ -373,11 +408,11 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_group_kernel(Row
 // does (same lane mapping and summation order), rounds both to fp16 where
 // the separate GEMVs store, and writes act[r] = fp16(silu(g) * u) with the
 // swiglu_kernel expression -- the separate launches' results bit for bit.
-template <class QT, int S, int M>
+template <class QT, int S, int M, bool kNorm = false>
 __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(const uint8_t* __restrict__ wg,
                                                                 const uint8_t* __restrict__ wu,
                                                                 const uint16_t* __restrict__ x,
-                                                                uint16_t* __restrict__ act, int K, int N) {
+                                                                uint16_t* __restrict__ act, int K, int N, NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
@@ -395,8 +430,8 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
         return QT::load(w + f * QT::kBytes, l4);
     };
 
-    XStage<QT::kSumLayout, nb / 8> xs;   // K = 256 nb
-    xs.load(x);
+    XStage<QT::kSumLayout, nb / 8, kNorm> xs;   // K = 256 nb
+    xs.load(x, nrm);
     __builtin_amdgcn_sched_barrier(0);
     typename QT::Frag fg[D], fu[D];
 #pragma unroll
@@ -407,7 +442,7 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
             fu[m * S + t] = frag_at(wu, gw + m * W, t);
             __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
         }
-    xs.store(xp, sx);
+    xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
 
     for (int row = gw; row < N; row += M * W) {
 #pragma unroll
@@ -508,58 +543,62 @@ int stream_grid(int rows) {
     return grid > need ? need : grid;
 }
 
-template <class QT, bool kF32, int S, int M, int kSegs>
-void launch_stream(const RowSet& rs, const uint16_t* x, size_t lds, hipStream_t stream) {
-    launch_kernel((matvec_stream_kernel<QT, kF32, S, M, kSegs>), dim3(stream_grid(rs.end[kSegs - 1])), dim3(kBlock),
-                  lds, stream, rs, x, S * 4096);
+template <class QT, bool kF32, int S, int M, int kSegs, bool kNorm>
+void launch_stream(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
+    launch_kernel((matvec_stream_kernel<QT, kF32, S, M, kSegs, true, kNorm>), dim3(stream_grid(rs.end[kSegs - 1])),
+                  dim3(kBlock), lds, stream, rs, x, S * 4096, nrm);
 }
 
 // K = 4096, few rows: every wave loads its M rows up front and computes
 // them, no refills (M * waves >= rows).
-template <class QT, bool kF32, int M, int kSegs>
-void launch_rows_once(const RowSet& rs, const uint16_t* x, size_t lds, hipStream_t stream) {
+template <class QT, bool kF32, int M, int kSegs, bool kNorm>
+void launch_rows_once(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
     const int rows = rs.end[kSegs - 1];
     const int grid = (rows + M * kWavesPerBlock - 1) / (M * kWavesPerBlock);
-    launch_kernel((matvec_stream_kernel<QT, kF32, 1, M, kSegs, false>), dim3(grid), dim3(kBlock), lds, stream, rs, x,
-                  4096);
+    launch_kernel((matvec_stream_kernel<QT, kF32, 1, M, kSegs, false, kNorm>), dim3(grid), dim3(kBlock), lds, stream,
+                  rs, x, 4096, nrm);
 }
 
 // K = 4096 S.  Shapes measured on MI355X: at K = 4096 a launch of up to 4096
 // rows is fastest as one pass of one or two rows per wave (the refill loop's
 // loads past the last row cost more than they hide); longer matrices stream
 // with one row in flight, two once each wave walks at least four rows.
-template <class QT, bool kF32, int kSegs>
-bool launch_stream_for(int nb, const RowSet& rs, const uint16_t* x, size_t lds, hipStream_t stream) {
+template <class QT, bool kF32, int kSegs, bool kNorm = false>
+bool launch_stream_for(int nb, const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm,
+                       hipStream_t stream) {
     const int rows = rs.end[kSegs - 1];
     switch (nb) {
         case 16:
             if (rows <= 1024)
-                launch_rows_once<QT, kF32, 1, kSegs>(rs, x, lds, stream);
+                launch_rows_once<QT, kF32, 1, kSegs, kNorm>(rs, x, lds, nrm, stream);
             else if (rows <= 4096)
-                launch_rows_once<QT, kF32, 2, kSegs>(rs, x, lds, stream);
+                launch_rows_once<QT, kF32, 2, kSegs, kNorm>(rs, x, lds, nrm, stream);
             else if (rows >= 4 * kWavesPerBlock * stream_grid(rows))
-                launch_stream<QT, kF32, 1, 2, kSegs>(rs, x, lds, stream);
+                launch_stream<QT, kF32, 1, 2, kSegs, kNorm>(rs, x, lds, nrm, stream);
             else
-                launch_stream<QT, kF32, 1, 1, kSegs>(rs, x, lds, stream);
+                launch_stream<QT, kF32, 1, 1, kSegs, kNorm>(rs, x, lds, nrm, stream);
             return true;
-        case 32: launch_stream<QT, kF32, 2, 1, kSegs>(rs, x, lds, stream); return true;
-        case 48: launch_stream<QT, kF32, 3, 1, kSegs>(rs, x, lds, stream); return true;
-        case 64: launch_stream<QT, kF32, 4, 1, kSegs>(rs, x, lds, stream); return true;
+        case 32: launch_stream<QT, kF32, 2, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
+        case 48: launch_stream<QT, kF32, 3, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
+        case 64: launch_stream<QT, kF32, 4, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
         default: return false;
     }
 }
 
+// staged x (fp16 pairs), the x-sum table and 4 floats of reduction scratch
 template <class QT>
 size_t lds_bytes(int K) {
-    return (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float);
+    return (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float) + 4 * sizeof(float);
 }
+
+constexpr NormIn kNoNorm{nullptr, nullptr, nullptr, 0.f};
 
 template <class QT, bool kF32>
 hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, int N, hipStream_t stream) {
     const int nb = K / kQK;
     const size_t lds = lds_bytes<QT>(K);
     const RowSet rs{{w, w, w}, {y, y, y}, {N, N, N}};
-    if (!launch_stream_for<QT, kF32, 1>(nb, rs, x, lds, stream)) {
+    if (!launch_stream_for<QT, kF32, 1>(nb, rs, x, lds, kNoNorm, stream)) {
         // any other length: flat walk over the super-blocks of 4 rows
         constexpr int kRows = 4;
         // floor(f / nb) == (f * magic) >> 32 for every f < 2^20 (nb <= 112)
@@ -572,8 +611,18 @@ hipError_t launch_matvec(const uint8_t* w, const uint16_t* x, void* y, int K, in
     return hipGetLastError();
 }
 
-template <int S, int M>
-void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int K, hipStream_t stream) {
+template <class QT, bool kF32>
+hipError_t launch_matvec_prologue(const uint8_t* w, const uint16_t* x, const NormIn& nrm, void* y, int K, int N,
+                                  hipStream_t stream) {
+    const RowSet rs{{w, w, w}, {y, y, y}, {N, N, N}};
+    if (!launch_stream_for<QT, kF32, 1, true>(K / kQK, rs, x, lds_bytes<QT>(K), nrm, stream))
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+template <int S, int M, bool kNorm>
+void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int K, const NormIn& nrm,
+                        hipStream_t stream) {
     const int na = a.end[2], nbr = b.end[2];
     const size_t lds = std::max(lds_bytes<Q4K>(K), lds_bytes<Q6K>(K));
     if (S == 1 && na + nbr <= 8192) {
@@ -582,8 +631,8 @@ void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int
         constexpr int kM = 2;
         const int ga = (na + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
         const int gb = (nbr + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
-        launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false>), dim3(ga + gb), dim3(kBlock), lds, stream, a, b, ga,
-                      x, K);
+        launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false, kNorm>), dim3(ga + gb), dim3(kBlock), lds, stream,
+                      a, b, ga, x, K, nrm);
         return;
     }
     // blocks split in proportion to the bytes each set streams
@@ -592,22 +641,39 @@ void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int
     int ga = (int)(grid * ba / (ba + bb) + 0.5);
     ga = std::max(1, std::min(ga, std::min(grid - 1, stream_grid(na))));
     const int gb = std::max(1, std::min(grid - ga, stream_grid(nbr)));
-    launch_kernel((matvec_group_kernel<Q4K, Q6K, S, M>), dim3(ga + gb), dim3(kBlock), lds, stream, a, b, ga, x, K);
+    launch_kernel((matvec_group_kernel<Q4K, Q6K, S, M, true, kNorm>), dim3(ga + gb), dim3(kBlock), lds, stream, a, b,
+                  ga, x, K, nrm);
 }
 
-template <class QT>
+template <bool kNorm>
+bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], const uint16_t* x, int K, const NormIn& nrm,
+                  hipStream_t s) {
+    if (cnt[1] == 0) return launch_stream_for<Q4K, false, 3, kNorm>(nb, set[0], x, lds_bytes<Q4K>(K), nrm, s);
+    if (cnt[0] == 0) return launch_stream_for<Q6K, false, 3, kNorm>(nb, set[1], x, lds_bytes<Q6K>(K), nrm, s);
+    switch (nb) {
+        case 16: launch_group_mixed<1, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
+        case 32: launch_group_mixed<2, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
+        case 48: launch_group_mixed<3, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
+        case 64: launch_group_mixed<4, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
+        default: return false;
+    }
+}
+
+template <class QT, bool kNorm>
 hipError_t launch_gate_up(const uint8_t* wg, const uint8_t* wu, const uint16_t* x, uint16_t* act, int K, int N,
-                          hipStream_t stream) {
-    const size_t lds = (size_t)K * 2 + (size_t)(K / kQK) * QT::kSxPerBlock * sizeof(float);
+                          const NormIn& nrm, hipStream_t stream) {
+    const size_t lds = lds_bytes<QT>(K);
     int grid = 2 * device_cus();
     const int need = (N + kWavesPerBlock - 1) / kWavesPerBlock;
     if (grid > need) grid = need;
     switch (K / kQK) {
         case 16:   // M = 1: measured faster than 2 at 12288 x 4096 on MI355X
-            launch_kernel((matvec_gate_up_kernel<QT, 1, 1>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x, act, K, N);
+            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x,
+                          act, K, N, nrm);
             break;
         case 32:
-            launch_kernel((matvec_gate_up_kernel<QT, 2, 1>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x, act, K, N);
+            launch_kernel((matvec_gate_up_kernel<QT, 2, 1, kNorm>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x,
+                          act, K, N, nrm);
             break;
         default: return hipErrorInvalidValue;
     }
@@ -617,7 +683,7 @@ hipError_t launch_gate_up(const uint8_t* wg, const uint8_t* wu, const uint16_t* 
 }  // namespace
 
 size_t matvec_lds_bytes(int kind, int K) {
-    return (size_t)K * 2 + (size_t)(K / kQK) * (kind == 6 ? 16 : 8) * sizeof(float);
+    return kind == 6 ? lds_bytes<Q6K>(K) : lds_bytes<Q4K>(K);
 }
 
 hipError_t launch_matvec_q4k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
@@ -630,14 +696,20 @@ hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool 
     return f32_out ? launch_matvec<Q6K, true>(w, x, y, K, N, s) : launch_matvec<Q6K, false>(w, x, y, K, N, s);
 }
 
-}  // namespace citlali::hip
+hipError_t launch_matvec_norm(int kind, const uint8_t* w, const uint16_t* x, const NormIn& norm, void* y,
+                              bool f32_out, int K, int N, hipStream_t s) {
+    if (kind == 6)
+        return f32_out ? launch_matvec_prologue<Q6K, true>(w, x, norm, y, K, N, s)
+                       : launch_matvec_prologue<Q6K, false>(w, x, norm, y, K, N, s);
+    return f32_out ? launch_matvec_prologue<Q4K, true>(w, x, norm, y, K, N, s)
+                   : launch_matvec_prologue<Q4K, false>(w, x, norm, y, K, N, s);
+}
 
-namespace citlali::hip {
 // count matrices (1..3) reading x: kinds[i] 4 = Q4_K, 6 = Q6_K, n[i] rows,
 // fp16 outputs y[i].  hipErrorInvalidValue, nothing launched, for a length
 // other than 4096, 8192, 12288 or 16384.
 hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const* w, const uint16_t* x,
-                               uint16_t* const* y, const int* n, int K, hipStream_t s) {
+                               uint16_t* const* y, const int* n, int K, const NormIn* norm, hipStream_t s) {
     RowSet set[2];
     int cnt[2] = {0, 0};
     for (int i = 0; i < count; ++i) {
@@ -654,27 +726,19 @@ hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const
             set[t].end[j] = set[t].end[j - 1];
         }
     const int nb = K / kQK;
-    bool ok = false;
-    if (cnt[1] == 0) {
-        ok = launch_stream_for<Q4K, false, 3>(nb, set[0], x, lds_bytes<Q4K>(K), s);
-    } else if (cnt[0] == 0) {
-        ok = launch_stream_for<Q6K, false, 3>(nb, set[1], x, lds_bytes<Q6K>(K), s);
-    } else {
-        ok = true;
-        switch (nb) {
-            case 16: launch_group_mixed<1, 1>(set[0], set[1], x, K, s); break;
-            case 32: launch_group_mixed<2, 1>(set[0], set[1], x, K, s); break;
-            case 48: launch_group_mixed<3, 1>(set[0], set[1], x, K, s); break;
-            case 64: launch_group_mixed<4, 1>(set[0], set[1], x, K, s); break;
-            default: ok = false;
-        }
-    }
+    const bool ok = norm ? launch_group<true>(nb, set, cnt, x, K, *norm, s)
+                         : launch_group<false>(nb, set, cnt, x, K, kNoNorm, s);
     return ok ? hipGetLastError() : hipErrorInvalidValue;
 }
 
 // kind 4: Q4_K, 6: Q6_K; in_features 4096 or 8192 (16 or 32 super-blocks)
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
-                                        uint16_t* act, int K, int N, hipStream_t s) {
-    return kind == 6 ? launch_gate_up<Q6K>(wg, wu, x, act, K, N, s) : launch_gate_up<Q4K>(wg, wu, x, act, K, N, s);
+                                        uint16_t* act, int K, int N, const NormIn* norm, hipStream_t s) {
+    if (norm)
+        return kind == 6 ? launch_gate_up<Q6K, true>(wg, wu, x, act, K, N, *norm, s)
+                         : launch_gate_up<Q4K, true>(wg, wu, x, act, K, N, *norm, s);
+    return kind == 6 ? launch_gate_up<Q6K, false>(wg, wu, x, act, K, N, kNoNorm, s)
+                     : launch_gate_up<Q4K, false>(wg, wu, x, act, K, N, kNoNorm, s);
 }
+
 }  // namespace citlali::hip

@@ -28,6 +28,11 @@ class CitlaliError(RuntimeError):
 
 # (name, restype, argtypes) for every function of include/citlali_hip.h
 _P = c_void_p
+class Norm(ctypes.Structure):
+    """citlali_hip_norm: residual add + RMSNorm feeding a GEMV."""
+    _fields_ = [("delta", c_void_p), ("weight", c_void_p), ("sum_out", c_void_p), ("eps", c_float)]
+
+
 SIGNATURES = [
     ("citlali_hip_last_error", c_char_p, []),
     ("citlali_hip_abi_version", c_int, []),
@@ -85,6 +90,10 @@ SIGNATURES = [
     ("citlali_hip_graph_end", c_int, [POINTER(c_void_p)]),
     ("citlali_hip_graph_launch", c_int, [_P]),
     ("citlali_hip_graph_destroy", c_int, [_P]),
+    ("citlali_hip_matvec_group_norm", c_int, [c_int, POINTER(c_int), POINTER(c_void_p), _P, POINTER(Norm),
+                                              POINTER(c_void_p), POINTER(c_int), c_int]),
+    ("citlali_hip_matvec_gate_up_swiglu_norm", c_int, [c_int, _P, _P, _P, POINTER(Norm), _P, c_int, c_int]),
+    ("citlali_hip_matvec_norm", c_int, [c_int, _P, _P, POINTER(Norm), _P, c_int, c_int, c_int]),
     ("citlali_hip_set_kernel_timing", c_int, [_P, _P]),
     ("citlali_hip_event_create", c_int, [POINTER(c_void_p)]),
     ("citlali_hip_event_record", c_int, [_P]),

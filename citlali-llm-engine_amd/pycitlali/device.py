@@ -309,3 +309,33 @@ class Graph:
             _lib.call("citlali_hip_graph_destroy", self.handle)
             self.handle = None
 
+
+# ---- GEMVs with the residual add + RMSNorm prologue -------------------------
+def _norm(delta, weight, sum_out, eps):
+    nv = lambda a: a.ptr if a is not None else None
+    return _lib.Norm(nv(delta), nv(weight), nv(sum_out), float(eps))
+
+
+def matvec_group_norm(kinds, weights, x, delta, weight, sum_out, eps, outputs, out_features, in_features) -> None:
+    n = len(kinds)
+    types = (ctypes.c_int * n)(*[12 if k == "q4k" else 14 for k in kinds])
+    ws = (ctypes.c_void_p * n)(*[w.ptr for w in weights])
+    ys = (ctypes.c_void_p * n)(*[y.ptr for y in outputs])
+    rows = (ctypes.c_int * n)(*[int(r) for r in out_features])
+    nrm = _norm(delta, weight, sum_out, eps)
+    _lib.call("citlali_hip_matvec_group_norm", n, types, ws, _vp(x), ctypes.byref(nrm), ys, rows, int(in_features))
+
+
+def matvec_gate_up_swiglu_norm(kind, w_gate, w_up, x, delta, weight, sum_out, eps, act, in_features: int,
+                               out_features: int) -> None:
+    nrm = _norm(delta, weight, sum_out, eps)
+    _lib.call("citlali_hip_matvec_gate_up_swiglu_norm", 12 if kind == "q4k" else 14, _vp(w_gate), _vp(w_up), _vp(x),
+              ctypes.byref(nrm), _vp(act), int(in_features), int(out_features))
+
+
+def matvec_norm(kind, w, x, delta, weight, sum_out, eps, y, in_features: int, out_features: int,
+                f32_out: bool = False) -> None:
+    nrm = _norm(delta, weight, sum_out, eps)
+    _lib.call("citlali_hip_matvec_norm", 12 if kind == "q4k" else 14, _vp(w), _vp(x), ctypes.byref(nrm), _vp(y),
+              1 if f32_out else 0, int(in_features), int(out_features))
+

@@ -232,6 +232,33 @@ int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, cons
 int citlali_hip_matvec_group(int count, const int* gguf_types, const uint8_t* const* weights, const uint16_t* x,
                              uint16_t* const* outputs, const int* out_features, int in_features);
 
+/* GEMVs whose input is a residual add + RMSNorm (no reference counterpart):
+ * the GEMV reads fp16(s * rsqrt(mean(s^2) + eps) * weight) with
+ * s = fp16(x + delta) (s = x when delta is NULL); when sum_out is not NULL
+ * it receives s.  The results equal citlali_hip_add_rms_norm(x, delta,
+ * weight, tmp) followed by the plain GEMV on tmp, bit for bit (same
+ * reduction order), without the separate launch: the reference's
+ * add_inplace + rms_norm before attn_q/k/v, ffn_gate/up and the output
+ * (qwen_model.cpp:306, 340-341, 372, 385).  weight, delta and sum_out
+ * 16-byte aligned; sum_out must not be x or delta.  in_features 4096,
+ * 8192, 12288 or 16384 (gate_up: 4096 or 8192), else
+ * CITLALI_ERR_UNSUPPORTED with nothing launched. */
+typedef struct citlali_hip_norm {
+    const uint16_t* delta;
+    const uint16_t* weight;
+    uint16_t* sum_out;
+    float eps;
+} citlali_hip_norm;
+int citlali_hip_matvec_group_norm(int count, const int* gguf_types, const uint8_t* const* weights, const uint16_t* x,
+                                  const citlali_hip_norm* norm, uint16_t* const* outputs, const int* out_features,
+                                  int in_features);
+int citlali_hip_matvec_gate_up_swiglu_norm(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up,
+                                           const uint16_t* x, const citlali_hip_norm* norm, uint16_t* act,
+                                           int in_features, int out_features);
+/* gguf_type 12 / 14; y fp16 (f32_out 0) or fp32 (f32_out 1) */
+int citlali_hip_matvec_norm(int gguf_type, const uint8_t* w, const uint16_t* x, const citlali_hip_norm* norm,
+                            void* y, int f32_out, int in_features, int out_features);
+
 /* Kernel timing (no reference counterpart; for benchmarks): while armed with
  * two events of citlali_hip_event_create, the first kernel the calling thread
  * launches records `start` when it begins and every kernel records `stop`

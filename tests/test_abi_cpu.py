@@ -97,6 +97,39 @@ def test_matvec_group_validation():
     assert st == 1 and "null array" in msg
 
 
+def test_norm_prologue_validation():
+    import pycitlali
+    fake = P(0x10000)
+    ints = lambda *v: (ctypes.c_int * len(v))(*v)
+    ptrs = lambda *v: (ctypes.c_void_p * len(v))(*v)
+    Norm = pycitlali._lib.Norm
+    ok = Norm(0x20000, 0x30000, 0x40000, 1e-6)
+    st, msg = _status("citlali_hip_matvec_norm", 12, fake, fake, None, fake, 0, 4096, 8)
+    assert st == 1 and "null norm" in msg
+    st, msg = _status("citlali_hip_matvec_norm", 12, fake, fake, ctypes.byref(Norm(0x20000, 0, 0, 1e-6)), fake, 0,
+                      4096, 8)
+    assert st == 1 and "norm weight" in msg
+    st, msg = _status("citlali_hip_matvec_norm", 12, fake, fake, ctypes.byref(Norm(0x20004, 0x30000, 0, 1e-6)), fake,
+                      0, 4096, 8)
+    assert st == 1 and "delta must be 16-byte aligned" in msg
+    st, msg = _status("citlali_hip_matvec_norm", 12, fake, fake, ctypes.byref(Norm(0x20000, 0x30000, 0x10000, 1e-6)),
+                      fake, 0, 4096, 8)
+    assert st == 1 and "sum_out must not be the input" in msg
+    st, msg = _status("citlali_hip_matvec_norm", 10, fake, fake, ctypes.byref(ok), fake, 0, 4096, 8)
+    assert st == 1 and "not Q4_K or Q6_K" in msg
+    st, msg = _status("citlali_hip_matvec_norm", 14, fake, fake, ctypes.byref(ok), fake, 1, 2048, 8)
+    assert st == 2 and "no prologue kernel" in msg
+    st, msg = _status("citlali_hip_matvec_group_norm", 1, ints(12), ptrs(0x10000), fake, ctypes.byref(ok),
+                      ptrs(0x50000), ints(8), 20480)
+    assert st == 2 and "no grouped kernel" in msg
+    st, msg = _status("citlali_hip_matvec_group_norm", 0, ints(12), ptrs(0x10000), fake, ctypes.byref(ok),
+                      ptrs(0x50000), ints(8), 4096)
+    assert st == 1 and "count" in msg
+    st, msg = _status("citlali_hip_matvec_gate_up_swiglu_norm", 12, fake, fake, fake, ctypes.byref(ok), P(0x50000),
+                      12288, 8)
+    assert st == 2 and "no fused kernel" in msg
+
+
 def test_attention_validation():
     fake = P(0x10000)
     st, msg = _status("citlali_hip_attention", fake, fake, fake, fake, fake, 5, 5, 16, 8, 128)
