@@ -68,8 +68,8 @@ size_t split_lds_bytes() {
     return tiles > C::kMergeLds ? tiles : C::kMergeLds;
 }
 
-// merge kernel: weights [kMaxSplits], lsum (padded to 16 B), red[kBlock] float4
-constexpr size_t kMergeLds = (size_t)(kMaxSplits + 4) * sizeof(float) + (size_t)kBlock * 16;
+// merge kernel: per-thread accumulator (float4) and (max, sum) pair
+constexpr size_t kMergeLds = (size_t)kBlock * (16 + 8);
 
 // Positions a sequence covers and its chunk count.  A position at or beyond
 // the caller's bound `max_len` is cut there, so neither the cache reads nor
@@ -366,19 +366,17 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     const uint16_t* vbase = v_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + 8 * grp;
     const size_t row_step = (size_t)kv_heads * HD;
 
-    // q of head `col` (zero past the group) as B operands, dims 32t + 8grp + 4h + j
-    half4 qb[4][2];
+    // q of head `col` (zero past the group) as B operands, dims 32t + 8grp + 4h
+    // + j; loaded here, turned into operands after the first tiles' loads are
+    // issued, so that q's round trip overlaps theirs
+    const bool q_ok = col < group;
+    u32x4 q_raw[4];
     {
-        const bool ok = col < group;
-        const uint16_t* qh = q + ((size_t)seq * heads + kvh * group + (ok ? col : group - 1)) * HD + 8 * grp;
-        const uint32_t keep = ok ? 0xffffffffu : 0u;
+        const uint16_t* qh = q + ((size_t)seq * heads + kvh * group + (q_ok ? col : group - 1)) * HD + 8 * grp;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(qh + 32 * t);
-            qb[t][0] = as_half4(v.x & keep, v.y & keep);
-            qb[t][1] = as_half4(v.z & keep, v.w & keep);
-        }
+        for (int t = 0; t < 4; ++t) q_raw[t] = *reinterpret_cast<const u32x4*>(qh + 32 * t);
     }
+    half4 qb[4][2];
     f32x4 o[8];   // o[4c + e][i]: head 4grp + i, dim 64c + 4col + e
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -469,6 +467,14 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
         load_tile(d, w0 + d * kMTile);
         __builtin_amdgcn_sched_barrier(0);
     }
+    {
+        const uint32_t keep = q_ok ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            qb[t][0] = as_half4(q_raw[t].x & keep, q_raw[t].y & keep);
+            qb[t][1] = as_half4(q_raw[t].z & keep, q_raw[t].w & keep);
+        }
+    }
     for (int t0 = w0; t0 < w1; t0 += kDepth * kMTile) {
 #pragma unroll
         for (int d = 0; d < kDepth; ++d) process(d, t0 + d * kMTile);
@@ -519,9 +525,10 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
 }
 
 // Grid: (query head, seq).  Log-sum-exp merge of one head's chunk partials
-// ([chunk][HD + 4]: acc[HD], max, sum).  Phase 1: wave 0 finds the max and
-// keeps the chunk weights exp2(m - max) in LDS; phase 2: thread = (4 dims,
-// chunk subset) with 16-byte loads, reduced through LDS.
+// ([chunk][HD + 4]: acc[HD], max, sum) in one pass: thread = (4 dims, chunk
+// subset) loads its chunks' accumulators and (max, sum) pairs together and
+// merges them with a running max (one global round trip); the subsets then
+// merge in LDS.
 template <int HD>
 __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restrict__ part,
                                                             const int32_t* __restrict__ positions, int position,
@@ -532,43 +539,65 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restr
     const int n_valid = seq_span(positions, position, seq, chunk, max_len).n_valid;
     if (n_valid <= 1) return;   // written by the split kernel
     const size_t h0 = (size_t)seq * heads + hq;
-    const float* hp = part + h0 * n_splits * (HD + 4);
     constexpr size_t ent = HD + 4;
-    float* wts = reinterpret_cast<float*>(smem);   // [kMaxSplits]
-    float* lsum = wts + kMaxSplits;                // 4 floats reserved
-    if (threadIdx.x < kWave) {
-        const int lane = threadIdx.x;
-        float M = -INFINITY;
-        for (int s = lane; s < n_valid; s += kWave) M = fmaxf(M, hp[(size_t)s * ent + HD]);
-        M = wave_max(M);
-        float Ls = 0.f;
-        for (int s = lane; s < n_valid; s += kWave) {
-            const float w = exp2f(hp[(size_t)s * ent + HD] - M);
-            wts[s] = w;
-            Ls += hp[(size_t)s * ent + HD + 1] * w;
-        }
-        Ls = wave_sum(Ls);
-        if (lane == 0) lsum[0] = Ls;
-    }
-    __syncthreads();
+    const float* hp = part + h0 * n_splits * ent;
     constexpr int kQuads = HD / 4;
     constexpr int kGroups = kBlock / kQuads;
-    f32x4* red = reinterpret_cast<f32x4*>(lsum + 4);
     const int d4 = threadIdx.x % kQuads, g = threadIdx.x / kQuads;
+
+    constexpr int kBatch = 4;   // chunks whose loads are issued together
+    float m = -INFINITY, l = 0.f;
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    const float* e = hp + 4 * d4;
-#pragma unroll 8
-    for (int s = g; s < n_valid; s += kGroups) a += *reinterpret_cast<const f32x4*>(e + (size_t)s * ent) * wts[s];
-    red[threadIdx.x] = a;
+    for (int s0 = g; s0 < n_valid; s0 += kBatch * kGroups) {
+        f32x4 v[kBatch];
+        f32x2 ml[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int s = s0 + j * kGroups;
+            v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+            ml[j] = f32x2{-INFINITY, 0.f};
+            if (s < n_valid) {
+                const float* e = hp + (size_t)s * ent;
+                ml[j] = *reinterpret_cast<const f32x2*>(e + HD);
+                v[j] = *reinterpret_cast<const f32x4*>(e + 4 * d4);
+            }
+        }
+        float mn = m;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) mn = fmaxf(mn, ml[j].x);
+        const float fo = m == -INFINITY ? 0.f : exp2f(m - mn);
+        a *= fo;
+        l *= fo;
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const float f = ml[j].x == -INFINITY ? 0.f : exp2f(ml[j].x - mn);
+            a += v[j] * f;
+            l += ml[j].y * f;
+        }
+        m = mn;
+    }
+    f32x4* ra = reinterpret_cast<f32x4*>(smem);                // [kBlock]
+    f32x2* rm = reinterpret_cast<f32x2*>(ra + kBlock);         // [kBlock] (max, sum)
+    ra[threadIdx.x] = a;
+    rm[threadIdx.x] = f32x2{m, l};
     __syncthreads();
     if (g == 0) {
-        for (int gg = 1; gg < kGroups; ++gg) a += red[gg * kQuads + d4];
-        const float inv = 1.f / lsum[0];
+        float M = m;
+        for (int gg = 1; gg < kGroups; ++gg) M = fmaxf(M, rm[gg * kQuads + d4].x);
+        f32x4 A = {0.f, 0.f, 0.f, 0.f};
+        float L = 0.f;
+        for (int gg = 0; gg < kGroups; ++gg) {
+            const f32x2 x = rm[gg * kQuads + d4];
+            const float f = x.x == -INFINITY ? 0.f : exp2f(x.x - M);
+            A += ra[gg * kQuads + d4] * f;
+            L += x.y * f;
+        }
+        const float inv = 1.f / L;
         uint16_t* o = out + h0 * HD + 4 * d4;
-        o[0] = f2h_rne(a.x * inv);
-        o[1] = f2h_rne(a.y * inv);
-        o[2] = f2h_rne(a.z * inv);
-        o[3] = f2h_rne(a.w * inv);
+        o[0] = f2h_rne(A.x * inv);
+        o[1] = f2h_rne(A.y * inv);
+        o[2] = f2h_rne(A.z * inv);
+        o[3] = f2h_rne(A.w * inv);
     }
 }
 
@@ -645,7 +674,8 @@ int attention_plan_length(int length, int max_context) {
 // per-workgroup set-up and the partial write amortised -- 64..256 positions
 // for the matrix-core kernel (head_dim 128, group >= 2), 256..512 for the
 // other (measured on MI355X at 512..8192 positions); the chunk a multiple of
-// 4 tiles, and at most kMaxSplits chunks (the merge's LDS weight table).
+// 4 tiles, and at most kMaxSplits chunks (bounds the merge's per-thread loop
+// and the partials workspace).
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
     AttnPlan p{};
     const int group = heads / kv_heads;
@@ -657,7 +687,7 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     const long long lo = mfma ? 64 : 256, hi = mfma ? 256 : 512;
     long long chunk = ((long long)max_len * units + target_blocks - 1) / target_blocks;
     chunk = chunk < lo ? lo : chunk > hi ? hi : chunk;
-    const long long min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;   // merge LDS bound
+    const long long min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;
     if (chunk < min_chunk) chunk = min_chunk;
     chunk = ((chunk + quantum - 1) / quantum) * quantum;
     p.chunk = (int)chunk;
