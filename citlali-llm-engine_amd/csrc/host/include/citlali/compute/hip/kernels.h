@@ -87,6 +87,12 @@ bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, co
 void launch_argmax(const float* logits, int n, int32_t* out_index);
 // Waits for every launch queued on the library stream.
 void synchronize();
+// Load-time dequantisation on the device (no reference launcher: the
+// reference dequantises on the host, weight_loader.cpp:147-323): `count`
+// values of raw Q4_K / Q6_K blocks to fp16 with the host rounding rule, the
+// same bits as the host routines.
+void launch_dequant_q4k_f16(const uint8_t* blocks, uint64_t count, uint16_t* output);
+void launch_dequant_q6k_f16(const uint8_t* blocks, uint64_t count, uint16_t* output);
 
 // ---- replayable decode steps (no reference counterpart) -------------------
 // The same launches with the token / position read from device memory

@@ -1,9 +1,11 @@
 // citlali/model/qwen_config.h -- model hyper-parameters.
 //
 // Same fields and defaults as the reference's QwenConfig
-// (include/citlali/model/qwen_config.h:8-23); reading them from GGUF
-// metadata (QwenConfig::from_gguf) belongs to the loader, outside this path.
+// (include/citlali/model/qwen_config.h:8-25), read from GGUF metadata by
+// from_gguf (src/model/qwen_config.cpp:59-151).
 #pragma once
+
+#include "citlali/io/gguf_reader.h"
 
 #include <cstdint>
 #include <string>
@@ -23,6 +25,14 @@ struct QwenConfig {
     uint32_t value_dim = 0;
     float rms_norm_eps = 1e-6f;
     float rope_theta = 1000000.0f;
+
+    // `<arch>.*` keys (arch = general.architecture, default "qwen3", must
+    // contain "qwen"), then `qwen2.*` for sizes still 0; vocab_size = the
+    // length of tokenizer.ggml.tokens.  head_dim / value_dim missing from the
+    // metadata come from blk.0.attn_q / attn_v rows per head, else
+    // embedding_length / head_count.  Throws citlali::Error for a size it
+    // cannot find or value_dim != head_dim.
+    static QwenConfig from_gguf(const io::GgufFile& gguf);
 };
 
 }  // namespace citlali::model

@@ -14,6 +14,7 @@
 #include "citlali/model/linear_backend.h"
 #include "citlali/model/qwen_config.h"
 #include "citlali/model/weight_handle.h"
+#include "citlali/model/weight_loader.h"
 
 #include <cstdint>
 #include <memory>
@@ -54,6 +55,11 @@ public:
     QwenModel(const QwenModel&) = delete;
     QwenModel& operator=(const QwenModel&) = delete;
 
+    // From a GGUF file, as the reference's load (qwen_model.cpp:45-186,
+    // remote layers aside): config by QwenConfig::from_gguf, tensors by their
+    // GGUF names through a WeightLoader (KeepQuantized when `quantized`,
+    // else DequantizeToFp16), then the load below.
+    void load(const io::GgufFile& gguf, uint32_t max_context = 0, bool quantized = false);
     // max_context 0 -> min(context_length, 2048), as the reference.
     void load(const QwenConfig& config, QwenWeights weights, uint32_t max_context = 0);
     // Runs one token at `position`; returns the greedy next token, or -1

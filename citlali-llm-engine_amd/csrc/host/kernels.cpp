@@ -165,6 +165,14 @@ void launch_argmax(const float* logits, int n, int32_t* out_index) {
 
 void synchronize() { CITLALI_HIP_CHECK(citlali_hip_synchronize()); }
 
+void launch_dequant_q4k_f16(const uint8_t* blocks, uint64_t count, uint16_t* output) {
+    CITLALI_HIP_CHECK(citlali_hip_dequant_q4k_f16(blocks, count, output));
+}
+
+void launch_dequant_q6k_f16(const uint8_t* blocks, uint64_t count, uint16_t* output) {
+    CITLALI_HIP_CHECK(citlali_hip_dequant_q6k_f16(blocks, count, output));
+}
+
 void launch_embed_q6k_at(const uint8_t* embedding, const int32_t* token, int vocab, uint16_t* output, int hidden) {
     CITLALI_HIP_CHECK(citlali_hip_embed_q6k_at(embedding, token, vocab, output, hidden));
 }

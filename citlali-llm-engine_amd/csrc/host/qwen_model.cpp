@@ -34,6 +34,39 @@ void add_bias_if_present(const WeightHandle& bias, const compute::DeviceBufferPt
 
 }  // namespace
 
+void QwenModel::load(const io::GgufFile& gguf, uint32_t max_context, bool quantized) {
+    const QwenConfig config = QwenConfig::from_gguf(gguf);
+    const WeightLoader loader(gguf, quantized ? WeightLoadPolicy::KeepQuantized : WeightLoadPolicy::DequantizeToFp16);
+    const auto blk = [](uint32_t i, const char* suffix) { return "blk." + std::to_string(i) + "." + suffix; };
+    QwenWeights w;
+    w.token_embedding = loader.load_required("token_embd.weight");
+    w.output_norm = loader.load_required("output_norm.weight");
+    w.output_weight = loader.load_optional("output.weight");   // absent: tied to token_embd
+    w.layers.resize(config.block_count);
+    for (uint32_t i = 0; i < config.block_count; ++i) {
+        QwenLayerWeights& l = w.layers[i];
+        l.attn_norm = loader.load_required(blk(i, "attn_norm.weight"));
+        l.attn_q = loader.load_required(blk(i, "attn_q.weight"));
+        l.attn_q_bias = loader.load_optional(blk(i, "attn_q.bias"));
+        l.attn_k = loader.load_required(blk(i, "attn_k.weight"));
+        l.attn_k_bias = loader.load_optional(blk(i, "attn_k.bias"));
+        l.attn_v = loader.load_required(blk(i, "attn_v.weight"));
+        l.attn_v_bias = loader.load_optional(blk(i, "attn_v.bias"));
+        l.attn_o = loader.load_required(blk(i, "attn_output.weight"));
+        l.attn_o_bias = loader.load_optional(blk(i, "attn_output.bias"));
+        l.attn_q_norm = loader.load_optional(blk(i, "attn_q_norm.weight"));
+        l.attn_k_norm = loader.load_optional(blk(i, "attn_k_norm.weight"));
+        l.ffn_norm = loader.load_required(blk(i, "ffn_norm.weight"));
+        l.ffn_gate = loader.load_required(blk(i, "ffn_gate.weight"));
+        l.ffn_gate_bias = loader.load_optional(blk(i, "ffn_gate.bias"));
+        l.ffn_up = loader.load_required(blk(i, "ffn_up.weight"));
+        l.ffn_up_bias = loader.load_optional(blk(i, "ffn_up.bias"));
+        l.ffn_down = loader.load_required(blk(i, "ffn_down.weight"));
+        l.ffn_down_bias = loader.load_optional(blk(i, "ffn_down.bias"));
+    }
+    load(config, std::move(w), max_context);
+}
+
 void QwenModel::load(const QwenConfig& config, QwenWeights weights, uint32_t max_context) {
     config_ = config;
     max_context_ = max_context == 0 ? std::min<uint32_t>(config_.context_length, 2048)

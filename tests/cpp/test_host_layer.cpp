@@ -5,12 +5,14 @@
 //                         LinearBackend dispatch and its errors; no GPU.
 //   test_host_layer gpu   DeviceBuffer, LinearBackend::forward (Q4_K, Q6_K,
 //                         fp16), launch_attention, launch_embed_q6k on the
-//                         GPU, compared with the oracle.
+//                         GPU, compared with the oracle; QwenModel decode,
+//                         also loaded from a GGUF file of the same model.
 // Prints one line per check and exits non-zero on the first failure.
 #include "citlali/common.h"
 #include "citlali/compute/common/dtype.h"
 #include "citlali/compute/hip/kernels.h"
 #include "citlali/compute/hip/tensor.h"
+#include "citlali/io/gguf_reader.h"
 #include "citlali/model/linear_backend.h"
 #include "citlali/model/qwen_model.h"
 #include "citlali_hip.h"
@@ -23,6 +25,8 @@
 #include <functional>
 #include <string>
 #include <vector>
+
+#include <unistd.h>
 
 using namespace citlali;
 using compute::GgufTensorType;
@@ -660,6 +664,218 @@ void test_decode_greedy_graph(int hidden, int heads) {
                 steps);
 }
 
+// ---- the synthetic model as a GGUF file ----------------------------------
+// The layout the reader parses (the reference's gguf_reader.cpp:160-241):
+// header, metadata, tensor directory, data at 32-byte aligned offsets.
+// Matrices keep their Q4_K / Q6_K blocks with dims [in, out]; the norm
+// vectors are stored as F32, as Qwen GGUF files store them.
+class GgufOut {
+public:
+    void u32(const std::string& k, uint32_t v) { key(k, 4); put(kv_, v); }
+    void f32(const std::string& k, float v) { key(k, 6); put(kv_, v); }
+    void str(const std::string& k, const std::string& v) { key(k, 8); text(kv_, v); }
+    void tokens(const std::string& k, int n) {
+        key(k, 9);
+        put<uint32_t>(kv_, 8);
+        put<uint64_t>(kv_, (uint64_t)n);
+        for (int i = 0; i < n; ++i) text(kv_, "t" + std::to_string(i));
+    }
+    void tensor(const std::string& name, std::vector<uint64_t> dims, GgufTensorType t, const void* p, size_t n) {
+        while (data_.size() % 32) data_.push_back(0);
+        text(dir_, name);
+        put<uint32_t>(dir_, (uint32_t)dims.size());
+        for (uint64_t d : dims) put(dir_, d);
+        put<uint32_t>(dir_, (uint32_t)t);
+        put<uint64_t>(dir_, (uint64_t)data_.size());
+        data_.insert(data_.end(), (const uint8_t*)p, (const uint8_t*)p + n);
+        ++n_tensors_;
+    }
+    void matrix(const std::string& name, const HostMatrix& m) {
+        tensor(name, {(uint64_t)m.cols, (uint64_t)m.rows}, m.type, m.bytes.data(), m.bytes.size());
+    }
+    void norm(const std::string& name, const std::vector<uint16_t>& h) {
+        std::vector<float> f(h.size());
+        for (size_t i = 0; i < h.size(); ++i) f[i] = orc_h2f(h[i]);
+        tensor(name, {(uint64_t)h.size()}, GgufTensorType::F32, f.data(), f.size() * 4);
+    }
+    void write(const std::string& path) const {
+        std::vector<uint8_t> head = {'G', 'G', 'U', 'F'};
+        put<uint32_t>(head, 3);
+        put<uint64_t>(head, n_tensors_);
+        put<uint64_t>(head, n_kv_);
+        head.insert(head.end(), kv_.begin(), kv_.end());
+        head.insert(head.end(), dir_.begin(), dir_.end());
+        while (head.size() % 32) head.push_back(0);
+        FILE* f = std::fopen(path.c_str(), "wb");
+        check(f != nullptr, "open " + path);
+        if (!f) return;
+        const bool ok = std::fwrite(head.data(), 1, head.size(), f) == head.size() &&
+                        std::fwrite(data_.data(), 1, data_.size(), f) == data_.size();
+        std::fclose(f);
+        check(ok, "write " + path);
+    }
+
+private:
+    template <typename T>
+    static void put(std::vector<uint8_t>& b, T v) {
+        const uint8_t* p = reinterpret_cast<const uint8_t*>(&v);
+        b.insert(b.end(), p, p + sizeof v);
+    }
+    static void text(std::vector<uint8_t>& b, const std::string& s) {
+        put<uint64_t>(b, s.size());
+        b.insert(b.end(), s.begin(), s.end());
+    }
+    void key(const std::string& k, uint32_t type) {
+        text(kv_, k);
+        put(kv_, type);
+        ++n_kv_;
+    }
+    std::vector<uint8_t> kv_, dir_, data_;
+    uint64_t n_kv_ = 0, n_tensors_ = 0;
+};
+
+void write_synth_gguf(const SynthModel& s, const std::string& path) {
+    GgufOut o;
+    const model::QwenConfig& c = s.cfg;
+    o.str("general.architecture", "qwen3");
+    o.tokens("tokenizer.ggml.tokens", (int)c.vocab_size);
+    o.u32("qwen3.context_length", c.context_length);
+    o.u32("qwen3.embedding_length", c.embedding_length);
+    o.u32("qwen3.block_count", c.block_count);
+    o.u32("qwen3.feed_forward_length", c.feed_forward_length);
+    o.u32("qwen3.attention.head_count", c.head_count);
+    o.u32("qwen3.attention.head_count_kv", c.head_count_kv);
+    o.u32("qwen3.attention.key_length", c.head_dim);
+    o.u32("qwen3.attention.value_length", c.head_dim);
+    o.f32("qwen3.attention.layer_norm_rms_epsilon", c.rms_norm_eps);
+    o.f32("qwen3.rope.freq_base", c.rope_theta);
+    o.matrix("token_embd.weight", s.embd);
+    o.norm("output_norm.weight", s.output_norm);
+    o.matrix("output.weight", s.output);
+    for (size_t l = 0; l < s.layers.size(); ++l) {
+        const auto& L = s.layers[l];
+        const std::string b = "blk." + std::to_string(l) + ".";
+        o.norm(b + "attn_norm.weight", L.attn_norm);
+        o.matrix(b + "attn_q.weight", L.q);
+        o.matrix(b + "attn_k.weight", L.k);
+        o.matrix(b + "attn_v.weight", L.v);
+        o.matrix(b + "attn_output.weight", L.o);
+        o.norm(b + "attn_q_norm.weight", L.q_norm);
+        o.norm(b + "attn_k_norm.weight", L.k_norm);
+        o.norm(b + "ffn_norm.weight", L.ffn_norm);
+        o.matrix(b + "ffn_gate.weight", L.gate);
+        o.matrix(b + "ffn_up.weight", L.up);
+        o.matrix(b + "ffn_down.weight", L.down);
+    }
+    o.write(path);
+}
+
+std::string temp_path(const std::string& name) {
+    const char* d = std::getenv("TMPDIR");
+    return std::string(d && *d ? d : "/tmp") + "/citlali_" + std::to_string((long long)getpid()) + "_" + name;
+}
+
+std::vector<uint16_t> dequant_f16(const HostMatrix& m) {
+    std::vector<uint16_t> out((size_t)m.rows * m.cols);
+    if (m.type == GgufTensorType::Q4_K) {
+        orc_dequant_q4k_f16(m.bytes.data(), out.size(), out.data());
+    } else {
+        orc_dequant_q6k_f16(m.bytes.data(), out.size(), out.data());
+    }
+    return out;
+}
+
+// QwenModel::load from a GGUF file of the synthetic model.  KeepQuantized:
+// the same device bytes as the model built from WeightHandles, so the same
+// logits bit for bit and the same tokens.  DequantizeToFp16: fp16 weights and
+// the fp16 GEMVs, against the oracle run over the same fp16 dequantisation
+// (bound as greedy_run: within the oracle's own spread under 1-ulp input
+// noise; a differing token only where the oracle's gap is within twice the
+// logit error).
+void test_load_from_gguf() {
+    SynthModel s = make_model(23, 1024, 8, 4, 2048, 2, 512);
+    const int ctx = 64, vocab = 512, prompt = 8, steps = 40;
+    const std::string path = temp_path("synth_qwen3.gguf");
+    write_synth_gguf(s, path);
+    io::GgufFile g;
+    g.load(path);
+    const model::QwenConfig c = model::QwenConfig::from_gguf(g);
+    check(c.architecture == "qwen3" && c.vocab_size == 512 && c.embedding_length == 1024 && c.block_count == 2 &&
+              c.feed_forward_length == 2048 && c.head_count == 8 && c.head_count_kv == 4 && c.head_dim == 128 &&
+              c.value_dim == 128 && c.context_length == s.cfg.context_length && c.rms_norm_eps == s.cfg.rms_norm_eps &&
+              c.rope_theta == s.cfg.rope_theta,
+          "QwenConfig::from_gguf of the written model");
+
+    model::QwenModel a, b, f;
+    a.load(s.cfg, device_weights(s), ctx);
+    b.load(g, ctx, /*quantized=*/true);
+    f.load(g, ctx, /*quantized=*/false);
+    std::remove(path.c_str());   // the loaded weights live in device memory
+
+    // the oracle over fp16 weights, and a twin with 1-ulp embedding noise
+    std::vector<std::vector<uint16_t>> keep;
+    auto f16 = [&](const HostMatrix& m) {
+        keep.push_back(dequant_f16(m));
+        return OrcMatrix{ORC_F16, keep.back().data()};
+    };
+    keep.reserve(2 * (2 + 7 * s.layers.size()));
+    OracleModel orc(s, ctx, 2), ctl(s, ctx, 2);
+    for (OracleModel* o : {&orc, &ctl}) {
+        o->m.token_embd = f16(s.embd);
+        o->m.output = f16(s.output);
+        for (size_t l = 0; l < s.layers.size(); ++l) {
+            const auto& L = s.layers[l];
+            OrcLayer& d = o->layers[l];
+            d.q = f16(L.q); d.k = f16(L.k); d.v = f16(L.v); d.o = f16(L.o);
+            d.gate = f16(L.gate); d.up = f16(L.up); d.down = f16(L.down);
+        }
+    }
+    std::vector<uint16_t> noisy(static_cast<const uint16_t*>(ctl.m.token_embd.data),
+                                static_cast<const uint16_t*>(ctl.m.token_embd.data) + (size_t)vocab * 1024);
+    Rng flip{5};
+    for (auto& h : noisy)
+        if ((h & 0x7fff) && (flip.next() & 1)) h ^= 1;
+    ctl.m.token_embd = {ORC_F16, noisy.data()};
+
+    Rng r{99};
+    std::vector<float> la(vocab), lb(vocab), lf(vocab), lo(vocab), lc(vocab);
+    int32_t tok = 0, mismatched = 0;
+    double worst = 0, ctl_worst = 0;
+    for (int p = 0; p < prompt + steps; ++p) {
+        const int32_t in = p < prompt ? (int32_t)(r.next() % vocab) : tok;
+        const int32_t ta = a.forward_token(in, (uint32_t)p);
+        const int32_t tb = b.forward_token(in, (uint32_t)p);
+        const int32_t tf = f.forward_token(in, (uint32_t)p);
+        const int32_t to = orc.step(in, p, lo.data());
+        ctl.step(in, p, lc.data());
+        a.logits()->copy_to_host(la.data(), la.size() * 4);
+        b.logits()->copy_to_host(lb.data(), lb.size() * 4);
+        f.logits()->copy_to_host(lf.data(), lf.size() * 4);
+        check(ta == tb && std::memcmp(la.data(), lb.data(), la.size() * 4) == 0,
+              "GGUF KeepQuantized load = WeightHandle load, logits bit for bit at position " + std::to_string(p));
+        double err = 0, cerr = 0, ss = 0;
+        for (int i = 0; i < vocab; ++i) {
+            err = std::max(err, std::fabs((double)lf[i] - lo[i]));
+            cerr = std::max(cerr, std::fabs((double)lc[i] - lo[i]));
+            ss += (double)lo[i] * lo[i];
+        }
+        const double rms = std::sqrt(ss / vocab);
+        worst = std::max(worst, err / rms);
+        ctl_worst = std::max(ctl_worst, cerr / rms);
+        if (p >= prompt && tf != to) {
+            ++mismatched;
+            check((double)lo[to] - lo[tf] <= 2.0 * err, "fp16-path token at step " + std::to_string(p - prompt) +
+                                                            " differs beyond the logit error");
+        }
+        tok = ta;
+    }
+    std::printf("GGUF load: KeepQuantized = WeightHandles over %d positions; DequantizeToFp16 vs fp16 oracle: "
+                "max |logit diff| / rms = %.2e (oracle under 1-ulp embedding noise %.2e), %d/%d greedy tokens differ\n",
+                prompt + steps, worst, ctl_worst, mismatched, steps);
+    check(worst <= std::max(ctl_worst, 1e-3), "fp16-path logits within the oracle's own 1-ulp sensitivity");
+    check(mismatched <= 2, "fp16-path greedy tokens");
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -687,6 +903,7 @@ int main(int argc, char** argv) {
             test_forward_greedy();
             test_decode_greedy_graph(2048, 16);
             test_decode_greedy_graph(4096, 32);
+            test_load_from_gguf();
             compute::synchronize();
         } else {
             std::printf("usage: %s cpu|gpu\n", argv[0]);
