@@ -26,7 +26,8 @@ the host rule, fp32 dot; fp32 attention) on a bounded sample of the same
 layer, on this machine's host cores.  attention_cfg4
 (16 sequences in one batched attention launch).  decode_cfg5: BASELINE
 config 5 (the whole synthetic Qwen3-8B, greedy decode tok/s) from
-bin/decode_qwen3.
+bin/decode_qwen3, its weights written to a GGUF file in the temp directory
+and loaded by QwenModel::load(GgufFile) (load time and GB/s reported).
 """
 from __future__ import annotations
 
@@ -276,12 +277,19 @@ DECODE_BIN = os.path.join(ROOT, "citlali-llm-engine_amd", "bin", "decode_qwen3")
 
 def decode_cfg5():
     """BASELINE config 5 beside the headline: the synthetic Qwen3-8B greedy
-    decode through QwenModel (bin/decode_qwen3, a child process), 512-token
-    prompt then 256 greedy steps; decode tok/s from HIP events."""
+    decode through QwenModel (bin/decode_qwen3, a child process), loaded from
+    a GGUF file of its weights (written to the temp directory, removed after
+    loading), 512-token prompt then 256 greedy steps; decode tok/s."""
     import subprocess
+    import tempfile
     if not os.path.exists(DECODE_BIN):
         return {"error": "citlali-llm-engine_amd/bin/decode_qwen3 is not built"}
-    p = subprocess.run([DECODE_BIN], capture_output=True, text=True, timeout=600)
+    path = os.path.join(tempfile.gettempdir(), f"citlali_cfg5_{os.getpid()}.gguf")
+    try:
+        p = subprocess.run([DECODE_BIN, "--gguf", path], capture_output=True, text=True, timeout=600)
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
     if p.returncode != 0:
         return {"error": (p.stderr or p.stdout)[-300:]}
     return json.loads(p.stdout.strip().splitlines()[-1])

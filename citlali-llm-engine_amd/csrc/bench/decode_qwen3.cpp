@@ -13,13 +13,21 @@
 // weights from HBM.  The greedy steps run twice: as the reference's loop of
 // forward_token calls, then through QwenModel::decode_greedy (each step
 // replayed from a captured HIP graph); both must give the same tokens.
+// With `--gguf PATH` the same weights are first written to a GGUF file at
+// PATH (layers of one byte set share their data in the file; the norms are
+// F32 ones) and the model is loaded from it by QwenModel::load(GgufFile)
+// with KeepQuantized, the reference's load path (qwen_model.cpp:45-186); the
+// file is removed after loading and the load time is reported.
 // Prints one JSON line.
 //
 // usage: decode_qwen3 [--layers 36] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1] [--no-graph]
+//                     [--gguf PATH]
 #include "citlali/common.h"
 #include "citlali/compute/hip/kernels.h"
+#include "citlali/io/gguf_reader.h"
 #include "citlali/model/qwen_model.h"
 #include "citlali_hip.h"
+#include "gguf_out.hpp"
 
 #include <chrono>
 #include <cmath>
@@ -95,6 +103,12 @@ model::WeightHandle norm_handle(int n, const std::string& name) {
     return w;
 }
 
+const char* str_arg(int argc, char** argv, const char* key) {
+    for (int i = 1; i + 1 < argc; ++i)
+        if (std::strcmp(argv[i], key) == 0) return argv[i + 1];
+    return nullptr;
+}
+
 int arg(int argc, char** argv, const char* key, int def) {
     for (int i = 1; i + 1 < argc; ++i)
         if (std::strcmp(argv[i], key) == 0) return std::atoi(argv[i + 1]);
@@ -143,33 +157,97 @@ int main(int argc, char** argv) {
             sets[i].up = quant_bytes(s + 6, GgufTensorType::Q4_K, F, H, 1.0);
             sets[i].down = quant_bytes(s + 7, GgufTensorType::Q6_K, H, F, 0.5);
         }
-        model::QwenWeights w;
-        w.token_embedding = quant_handle(quant_bytes(seed * 7 + 11, GgufTensorType::Q6_K, V, H, std::sqrt(4096.0)),
-                                         GgufTensorType::Q6_K, V, H, "token_embd.weight");
-        w.output_norm = norm_handle(H, "output_norm.weight");
-        w.output_weight = quant_handle(quant_bytes(seed * 7 + 13, GgufTensorType::Q6_K, V, H, 3.0),
-                                       GgufTensorType::Q6_K, V, H, "output.weight");
-        for (int l = 0; l < layers; ++l) {
-            const LayerBytes& b = sets[l % distinct];
-            const std::string n = "blk." + std::to_string(l) + ".";
-            model::QwenLayerWeights L;
-            L.attn_norm = norm_handle(H, n + "attn_norm.weight");
-            L.attn_q = quant_handle(b.q, GgufTensorType::Q4_K, NQ, H, n + "attn_q.weight");
-            L.attn_k = quant_handle(b.k, GgufTensorType::Q4_K, NKV, H, n + "attn_k.weight");
-            L.attn_v = quant_handle(b.v, GgufTensorType::Q6_K, NKV, H, n + "attn_v.weight");
-            L.attn_o = quant_handle(b.o, GgufTensorType::Q4_K, H, NQ, n + "attn_output.weight");
-            L.attn_q_norm = norm_handle(128, n + "attn_q_norm.weight");
-            L.attn_k_norm = norm_handle(128, n + "attn_k_norm.weight");
-            L.ffn_norm = norm_handle(H, n + "ffn_norm.weight");
-            L.ffn_gate = quant_handle(b.gate, GgufTensorType::Q4_K, F, H, n + "ffn_gate.weight");
-            L.ffn_up = quant_handle(b.up, GgufTensorType::Q4_K, F, H, n + "ffn_up.weight");
-            L.ffn_down = quant_handle(b.down, GgufTensorType::Q6_K, H, F, n + "ffn_down.weight");
-            w.layers.push_back(std::move(L));
+        const std::vector<uint8_t> embd = quant_bytes(seed * 7 + 11, GgufTensorType::Q6_K, V, H, std::sqrt(4096.0));
+        const std::vector<uint8_t> outw = quant_bytes(seed * 7 + 13, GgufTensorType::Q6_K, V, H, 3.0);
+        const int ctx = prompt + steps;
+        model::QwenModel m;
+        const char* gguf_path = str_arg(argc, argv, "--gguf");
+        double gguf_write_s = 0, load_s = 0, file_bytes = 0, loaded_bytes = 0;
+        if (gguf_path != nullptr) {
+            // the weights as a GGUF file, then the reference's load path
+            bench::GgufOut o;
+            o.str("general.architecture", "qwen3");
+            o.strings("tokenizer.ggml.tokens", V);
+            o.u32("qwen3.context_length", cfg.context_length);
+            o.u32("qwen3.embedding_length", H);
+            o.u32("qwen3.block_count", (uint32_t)layers);
+            o.u32("qwen3.feed_forward_length", F);
+            o.u32("qwen3.attention.head_count", 32);
+            o.u32("qwen3.attention.head_count_kv", 8);
+            o.u32("qwen3.attention.key_length", 128);
+            o.u32("qwen3.attention.value_length", 128);
+            o.f32("qwen3.attention.layer_norm_rms_epsilon", cfg.rms_norm_eps);
+            o.f32("qwen3.rope.freq_base", cfg.rope_theta);
+            const std::vector<float> ones(H, 1.0f);
+            const auto Q4 = GgufTensorType::Q4_K, Q6 = GgufTensorType::Q6_K, F32T = GgufTensorType::F32;
+            const uint64_t h = (uint64_t)H, f = (uint64_t)F, nq = (uint64_t)NQ, nkv = (uint64_t)NKV;
+            o.tensor("token_embd.weight", {h, (uint64_t)V}, Q6, embd.data(), embd.size());
+            o.tensor("output_norm.weight", {h}, F32T, ones.data(), (size_t)H * 4);
+            o.tensor("output.weight", {h, (uint64_t)V}, Q6, outw.data(), outw.size());
+            std::vector<size_t> first(distinct * 7);
+            for (int l = 0; l < layers; ++l) {
+                const LayerBytes& b = sets[l % distinct];
+                const std::string n = "blk." + std::to_string(l) + ".";
+                o.tensor(n + "attn_norm.weight", {h}, F32T, ones.data(), (size_t)H * 4);
+                o.tensor(n + "attn_q_norm.weight", {128}, F32T, ones.data(), 128 * 4);
+                o.tensor(n + "attn_k_norm.weight", {128}, F32T, ones.data(), 128 * 4);
+                o.tensor(n + "ffn_norm.weight", {h}, F32T, ones.data(), (size_t)H * 4);
+                const struct {
+                    const char* name;
+                    const std::vector<uint8_t>* bytes;
+                    GgufTensorType t;
+                    uint64_t in, out;
+                } mats[7] = {{"attn_q.weight", &b.q, Q4, h, nq},       {"attn_k.weight", &b.k, Q4, h, nkv},
+                             {"attn_v.weight", &b.v, Q6, h, nkv},      {"attn_output.weight", &b.o, Q4, nq, h},
+                             {"ffn_gate.weight", &b.gate, Q4, h, f},   {"ffn_up.weight", &b.up, Q4, h, f},
+                             {"ffn_down.weight", &b.down, Q6, f, h}};
+                for (int j = 0; j < 7; ++j) {
+                    size_t& slot = first[(l % distinct) * 7 + j];
+                    if (l < distinct) {
+                        slot = o.tensor(n + mats[j].name, {mats[j].in, mats[j].out}, mats[j].t, mats[j].bytes->data(),
+                                        mats[j].bytes->size());
+                    } else {
+                        o.alias(n + mats[j].name, {mats[j].in, mats[j].out}, mats[j].t, slot);
+                    }
+                }
+            }
+            const auto w0 = std::chrono::steady_clock::now();
+            file_bytes = (double)o.write(gguf_path);
+            const auto w1 = std::chrono::steady_clock::now();
+            gguf_write_s = std::chrono::duration<double>(w1 - w0).count();
+            io::GgufFile g;
+            g.load(gguf_path);
+            m.load(g, (uint32_t)ctx, /*quantized=*/true);
+            m.synchronize();
+            load_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - w1).count();
+            for (const auto& t : g.tensors()) loaded_bytes += (double)t.nbytes;
+            std::remove(gguf_path);
+        } else {
+            model::QwenWeights w;
+            w.token_embedding = quant_handle(embd, GgufTensorType::Q6_K, V, H, "token_embd.weight");
+            w.output_norm = norm_handle(H, "output_norm.weight");
+            w.output_weight = quant_handle(outw, GgufTensorType::Q6_K, V, H, "output.weight");
+            for (int l = 0; l < layers; ++l) {
+                const LayerBytes& b = sets[l % distinct];
+                const std::string n = "blk." + std::to_string(l) + ".";
+                model::QwenLayerWeights L;
+                L.attn_norm = norm_handle(H, n + "attn_norm.weight");
+                L.attn_q = quant_handle(b.q, GgufTensorType::Q4_K, NQ, H, n + "attn_q.weight");
+                L.attn_k = quant_handle(b.k, GgufTensorType::Q4_K, NKV, H, n + "attn_k.weight");
+                L.attn_v = quant_handle(b.v, GgufTensorType::Q6_K, NKV, H, n + "attn_v.weight");
+                L.attn_o = quant_handle(b.o, GgufTensorType::Q4_K, H, NQ, n + "attn_output.weight");
+                L.attn_q_norm = norm_handle(128, n + "attn_q_norm.weight");
+                L.attn_k_norm = norm_handle(128, n + "attn_k_norm.weight");
+                L.ffn_norm = norm_handle(H, n + "ffn_norm.weight");
+                L.ffn_gate = quant_handle(b.gate, GgufTensorType::Q4_K, F, H, n + "ffn_gate.weight");
+                L.ffn_up = quant_handle(b.up, GgufTensorType::Q4_K, F, H, n + "ffn_up.weight");
+                L.ffn_down = quant_handle(b.down, GgufTensorType::Q6_K, H, F, n + "ffn_down.weight");
+                w.layers.push_back(std::move(L));
+            }
+            m.load(cfg, std::move(w), (uint32_t)ctx);
+            m.synchronize();
         }
         sets.clear();
-        model::QwenModel m;
-        m.load(cfg, std::move(w), (uint32_t)(prompt + steps));
-        m.synchronize();
         const double setup_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
 
         // prompt, one token at a time (logits only for the last one)
@@ -232,13 +310,17 @@ int main(int argc, char** argv) {
                     "\"decode_GBps\": %.1f, \"decode_tok_per_s_forward_token\": %.2f, "
                     "\"decode_ms_per_token_forward_token\": %.4f, \"decode_ms_per_token_forward_token_wall\": %.4f, "
                     "\"graph_tokens_equal_forward_token\": %s, \"prompt_tok_per_s\": %.2f, "
-                    "\"prompt_ms_per_token_wall\": %.4f, \"setup_s\": %.1f, \"token_checksum\": %llu}\n",
+                    "\"prompt_ms_per_token_wall\": %.4f, \"setup_s\": %.1f, \"token_checksum\": %llu, "
+                    "\"weights_from\": \"%s\", \"gguf_file_bytes\": %.0f, \"gguf_write_s\": %.2f, "
+                    "\"gguf_load_s\": %.3f, \"gguf_load_GBps\": %.2f}\n",
                     layers, distinct, prompt, steps, steps / (decode_ms * 1e-3), decode_ms / steps,
                     graph_pass ? "QwenModel::decode_greedy (graph replay), wall clock"
                                : "forward_token loop, wall clock (--no-graph)",
                     step_bytes / (decode_ms * 1e-3 / steps) / 1e9, steps / (eager_ms * 1e-3), eager_ms / steps,
                     eager_wall * 1e3 / steps, match ? "true" : "false", prompt / (prompt_ms * 1e-3),
-                    prompt_wall * 1e3 / prompt, setup_s, (unsigned long long)checksum);
+                    prompt_wall * 1e3 / prompt, setup_s, (unsigned long long)checksum,
+                    gguf_path ? "GGUF file, QwenModel::load(GgufFile) KeepQuantized" : "WeightHandles",
+                    file_bytes, gguf_write_s, load_s, load_s > 0 ? loaded_bytes / load_s / 1e9 : 0.0);
         if (!match) {
             std::fprintf(stderr, "decode_qwen3: decode_greedy tokens differ from the forward_token loop\n");
             return 1;

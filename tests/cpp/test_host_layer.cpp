@@ -17,6 +17,7 @@
 #include "citlali/model/qwen_model.h"
 #include "citlali_hip.h"
 #include "citlali_oracle.h"
+#include "gguf_out.hpp"
 
 #include <cmath>
 #include <cstdio>
@@ -665,80 +666,23 @@ void test_decode_greedy_graph(int hidden, int heads) {
 }
 
 // ---- the synthetic model as a GGUF file ----------------------------------
-// The layout the reader parses (the reference's gguf_reader.cpp:160-241):
-// header, metadata, tensor directory, data at 32-byte aligned offsets.
 // Matrices keep their Q4_K / Q6_K blocks with dims [in, out]; the norm
 // vectors are stored as F32, as Qwen GGUF files store them.
-class GgufOut {
-public:
-    void u32(const std::string& k, uint32_t v) { key(k, 4); put(kv_, v); }
-    void f32(const std::string& k, float v) { key(k, 6); put(kv_, v); }
-    void str(const std::string& k, const std::string& v) { key(k, 8); text(kv_, v); }
-    void tokens(const std::string& k, int n) {
-        key(k, 9);
-        put<uint32_t>(kv_, 8);
-        put<uint64_t>(kv_, (uint64_t)n);
-        for (int i = 0; i < n; ++i) text(kv_, "t" + std::to_string(i));
-    }
-    void tensor(const std::string& name, std::vector<uint64_t> dims, GgufTensorType t, const void* p, size_t n) {
-        while (data_.size() % 32) data_.push_back(0);
-        text(dir_, name);
-        put<uint32_t>(dir_, (uint32_t)dims.size());
-        for (uint64_t d : dims) put(dir_, d);
-        put<uint32_t>(dir_, (uint32_t)t);
-        put<uint64_t>(dir_, (uint64_t)data_.size());
-        data_.insert(data_.end(), (const uint8_t*)p, (const uint8_t*)p + n);
-        ++n_tensors_;
-    }
-    void matrix(const std::string& name, const HostMatrix& m) {
-        tensor(name, {(uint64_t)m.cols, (uint64_t)m.rows}, m.type, m.bytes.data(), m.bytes.size());
-    }
-    void norm(const std::string& name, const std::vector<uint16_t>& h) {
-        std::vector<float> f(h.size());
-        for (size_t i = 0; i < h.size(); ++i) f[i] = orc_h2f(h[i]);
-        tensor(name, {(uint64_t)h.size()}, GgufTensorType::F32, f.data(), f.size() * 4);
-    }
-    void write(const std::string& path) const {
-        std::vector<uint8_t> head = {'G', 'G', 'U', 'F'};
-        put<uint32_t>(head, 3);
-        put<uint64_t>(head, n_tensors_);
-        put<uint64_t>(head, n_kv_);
-        head.insert(head.end(), kv_.begin(), kv_.end());
-        head.insert(head.end(), dir_.begin(), dir_.end());
-        while (head.size() % 32) head.push_back(0);
-        FILE* f = std::fopen(path.c_str(), "wb");
-        check(f != nullptr, "open " + path);
-        if (!f) return;
-        const bool ok = std::fwrite(head.data(), 1, head.size(), f) == head.size() &&
-                        std::fwrite(data_.data(), 1, data_.size(), f) == data_.size();
-        std::fclose(f);
-        check(ok, "write " + path);
-    }
-
-private:
-    template <typename T>
-    static void put(std::vector<uint8_t>& b, T v) {
-        const uint8_t* p = reinterpret_cast<const uint8_t*>(&v);
-        b.insert(b.end(), p, p + sizeof v);
-    }
-    static void text(std::vector<uint8_t>& b, const std::string& s) {
-        put<uint64_t>(b, s.size());
-        b.insert(b.end(), s.begin(), s.end());
-    }
-    void key(const std::string& k, uint32_t type) {
-        text(kv_, k);
-        put(kv_, type);
-        ++n_kv_;
-    }
-    std::vector<uint8_t> kv_, dir_, data_;
-    uint64_t n_kv_ = 0, n_tensors_ = 0;
-};
-
 void write_synth_gguf(const SynthModel& s, const std::string& path) {
-    GgufOut o;
+    bench::GgufOut o;
+    std::vector<std::vector<float>> norms;   // borrowed by `o` until write()
+    norms.reserve(1 + 4 * s.layers.size());
+    const auto matrix = [&](const std::string& name, const HostMatrix& m) {
+        o.tensor(name, {(uint64_t)m.cols, (uint64_t)m.rows}, m.type, m.bytes.data(), m.bytes.size());
+    };
+    const auto norm = [&](const std::string& name, const std::vector<uint16_t>& h) {
+        norms.emplace_back(h.size());
+        for (size_t i = 0; i < h.size(); ++i) norms.back()[i] = orc_h2f(h[i]);
+        o.tensor(name, {(uint64_t)h.size()}, GgufTensorType::F32, norms.back().data(), h.size() * 4);
+    };
     const model::QwenConfig& c = s.cfg;
     o.str("general.architecture", "qwen3");
-    o.tokens("tokenizer.ggml.tokens", (int)c.vocab_size);
+    o.strings("tokenizer.ggml.tokens", (int)c.vocab_size);
     o.u32("qwen3.context_length", c.context_length);
     o.u32("qwen3.embedding_length", c.embedding_length);
     o.u32("qwen3.block_count", c.block_count);
@@ -749,23 +693,23 @@ void write_synth_gguf(const SynthModel& s, const std::string& path) {
     o.u32("qwen3.attention.value_length", c.head_dim);
     o.f32("qwen3.attention.layer_norm_rms_epsilon", c.rms_norm_eps);
     o.f32("qwen3.rope.freq_base", c.rope_theta);
-    o.matrix("token_embd.weight", s.embd);
-    o.norm("output_norm.weight", s.output_norm);
-    o.matrix("output.weight", s.output);
+    matrix("token_embd.weight", s.embd);
+    norm("output_norm.weight", s.output_norm);
+    matrix("output.weight", s.output);
     for (size_t l = 0; l < s.layers.size(); ++l) {
         const auto& L = s.layers[l];
         const std::string b = "blk." + std::to_string(l) + ".";
-        o.norm(b + "attn_norm.weight", L.attn_norm);
-        o.matrix(b + "attn_q.weight", L.q);
-        o.matrix(b + "attn_k.weight", L.k);
-        o.matrix(b + "attn_v.weight", L.v);
-        o.matrix(b + "attn_output.weight", L.o);
-        o.norm(b + "attn_q_norm.weight", L.q_norm);
-        o.norm(b + "attn_k_norm.weight", L.k_norm);
-        o.norm(b + "ffn_norm.weight", L.ffn_norm);
-        o.matrix(b + "ffn_gate.weight", L.gate);
-        o.matrix(b + "ffn_up.weight", L.up);
-        o.matrix(b + "ffn_down.weight", L.down);
+        norm(b + "attn_norm.weight", L.attn_norm);
+        matrix(b + "attn_q.weight", L.q);
+        matrix(b + "attn_k.weight", L.k);
+        matrix(b + "attn_v.weight", L.v);
+        matrix(b + "attn_output.weight", L.o);
+        norm(b + "attn_q_norm.weight", L.q_norm);
+        norm(b + "attn_k_norm.weight", L.k_norm);
+        norm(b + "ffn_norm.weight", L.ffn_norm);
+        matrix(b + "ffn_gate.weight", L.gate);
+        matrix(b + "ffn_up.weight", L.up);
+        matrix(b + "ffn_down.weight", L.down);
     }
     o.write(path);
 }
