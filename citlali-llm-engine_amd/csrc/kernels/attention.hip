@@ -671,11 +671,12 @@ int attention_plan_length(int length, int max_context) {
 
 // Work split: enough chunks for about `target_blocks` workgroups over all
 // (sequence, kv head) units, within a range of chunk lengths that keeps the
-// per-workgroup set-up and the partial write amortised -- 64..256 positions
-// for the matrix-core kernel (head_dim 128, group >= 2), 256..512 for the
-// other (measured on MI355X at 512..8192 positions); the chunk a multiple of
-// 4 tiles, and at most kMaxSplits chunks (bounds the merge's per-thread loop
-// and the partials workspace).
+// per-workgroup set-up and the partial write amortised -- for the
+// matrix-core kernel (head_dim 128, group >= 2) 64 positions up to 1024 with
+// at most 16 units, 512 with more; 256..512 for the other kernel (measured
+// on MI355X: one sequence at 512..32768 positions, 16 sequences of
+// 4096..32768); the chunk a multiple of 4 tiles, and at most kMaxSplits
+// chunks (bounds the merge's per-thread loop and the partials workspace).
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
     AttnPlan p{};
     const int group = heads / kv_heads;
@@ -684,7 +685,7 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     const int tp = mfma ? kMTile : (64 / p.gp) < 32 ? 64 / p.gp : 32;
     const int quantum = tp * kWaves;
     const long long units = (long long)nseq * kv_heads;
-    const long long lo = mfma ? 64 : 256, hi = mfma ? 256 : 512;
+    const long long lo = mfma ? 64 : 256, hi = mfma ? (units <= 16 ? 1024 : 512) : 512;
     long long chunk = ((long long)max_len * units + target_blocks - 1) / target_blocks;
     chunk = chunk < lo ? lo : chunk > hi ? hi : chunk;
     const long long min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;
