@@ -493,6 +493,58 @@ CITLALI_EXPORT int citlali_hip_qk_norm_rope_store_at(uint16_t* q, const uint16_t
     return CITLALI_OK;
 }
 
+CITLALI_EXPORT int citlali_hip_qk_norm_rope_store_attention(
+    const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm, const uint16_t* k_norm,
+    int heads, int kv_heads, int head_dim, int position, const int32_t* position_at, int plan_length,
+    int max_context, float theta, float eps, uint16_t* k_cache, uint16_t* v_cache, void* workspace,
+    size_t workspace_bytes, uint16_t* out) {
+    REQUIRE(q && k && v && k_cache && v_cache && out, "qk_norm_rope_store_attention received a null buffer");
+    const int st = check_attn_shape(heads, kv_heads, head_dim);
+    if (st) return st;
+    const int group = heads / kv_heads;
+    if (head_dim != 128 || group < 2 || group > 8)
+        return fail(CITLALI_ERR_UNSUPPORTED,
+                    "qk_norm_rope_store_attention: no fused kernel for head_dim %d with %d query heads per kv head",
+                    head_dim, group);
+    REQUIRE(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16),
+            "qk_norm_rope_store_attention: q and caches must be 16-byte aligned");
+    REQUIRE(max_context > 0, "qk_norm_rope_store_attention: max_context must be positive");
+    AttnArgs a{};
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.seq_stride = 0;
+    a.nseq = 1;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.out = out;
+    AttnPlan p{};
+    if (position_at != nullptr) {
+        // as qk_norm_rope_store_at + attention_batched(nseq 1, plan_length)
+        REQUIRE(plan_length > 0 && plan_length <= max_context,
+                "qk_norm_rope_store_attention: plan_length %d outside (0, max_context]", plan_length);
+        a.positions = position_at;
+        a.max_len = plan_length;
+        p = plan_attention(plan_length, 1, kv_heads, heads, head_dim, kAttnTargetBlocks);
+    } else {
+        // as qk_norm_rope_store + attention at `position`
+        REQUIRE(position >= 0 && position < max_context, "position exceeds max_context");
+        a.position = position;
+        a.max_len = position + 1;
+        p = plan_attention(attention_plan_length(position + 1, max_context), 1, kv_heads, heads, head_dim,
+                           kAttnTargetBlocks);
+    }
+    const size_t need = attention_workspace_bytes(p, 1, heads, head_dim);
+    REQUIRE(workspace_bytes >= need && (need == 0 || (workspace && aligned(workspace, 16))),
+            "qk_norm_rope_store_attention: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    a.workspace = static_cast<float*>(workspace);
+    const QkPrep prep{k, v, q_norm, k_norm, k_cache, v_cache, theta, eps};
+    a.prep = &prep;
+    HIP_TRY(launch_attention(a, p, g_stream));
+    return CITLALI_OK;
+}
+
 // ---------------------------------------------------------------- streams and graphs
 CITLALI_EXPORT int citlali_hip_stream_create(void** stream) {
     REQUIRE(stream, "null output pointer");

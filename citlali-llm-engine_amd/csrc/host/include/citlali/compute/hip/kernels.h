@@ -85,6 +85,17 @@ bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, co
 // the logits to the host, qwen_model.cpp:448-465): the first largest finite
 // value of logits[0..n) is written to *out_index (0 when none is finite).
 void launch_argmax(const float* logits, int n, int32_t* out_index);
+// launch_qk_norm_rope_store(_at) followed by launch_attention(_at) in one
+// launch, the same results bit for bit (q is only read); position_at (device)
+// replaces `position` when not null, with plan_length the bucket.  Returns
+// false, launching nothing, when no fused kernel covers the shape (head_dim
+// 128 with 2..8 query heads per kv head).
+bool launch_qk_norm_rope_store_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                         const uint16_t* q_norm, const uint16_t* k_norm, int heads, int kv_heads,
+                                         int head_dim, int position, const int32_t* position_at, int plan_length,
+                                         int max_context, float theta, float eps, uint16_t* k_cache,
+                                         uint16_t* v_cache, float* workspace, std::size_t workspace_bytes,
+                                         uint16_t* output);
 // Waits for every launch queued on the library stream.
 void synchronize();
 // Load-time dequantisation on the device (no reference launcher: the

@@ -163,6 +163,20 @@ void launch_argmax(const float* logits, int n, int32_t* out_index) {
     CITLALI_HIP_CHECK(citlali_hip_argmax(logits, n, out_index));
 }
 
+bool launch_qk_norm_rope_store_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                         const uint16_t* q_norm, const uint16_t* k_norm, int heads, int kv_heads,
+                                         int head_dim, int position, const int32_t* position_at, int plan_length,
+                                         int max_context, float theta, float eps, uint16_t* k_cache,
+                                         uint16_t* v_cache, float* workspace, std::size_t workspace_bytes,
+                                         uint16_t* output) {
+    const int st = citlali_hip_qk_norm_rope_store_attention(q, k, v, q_norm, k_norm, heads, kv_heads, head_dim,
+                                                            position, position_at, plan_length, max_context, theta,
+                                                            eps, k_cache, v_cache, workspace, workspace_bytes, output);
+    if (st == CITLALI_ERR_UNSUPPORTED) return false;
+    CITLALI_HIP_CHECK(st);
+    return true;
+}
+
 void synchronize() { CITLALI_HIP_CHECK(citlali_hip_synchronize()); }
 
 void launch_dequant_q4k_f16(const uint8_t* blocks, uint64_t count, uint16_t* output) {

@@ -257,7 +257,15 @@ void QwenModel::enqueue_token(int32_t token_id, int pos, int32_t* state, int pla
         add_bias_if_present(layer.attn_v_bias, v_, static_cast<uint64_t>(kv_heads) * head_dim);
         const uint16_t* q_norm = layer.attn_q_norm.buffer ? layer.attn_q_norm.device_half_data() : nullptr;
         const uint16_t* k_norm = layer.attn_k_norm.buffer ? layer.attn_k_norm.device_half_data() : nullptr;
-        if (state) {
+        // q/k norm + RoPE + KV store inside the attention launch where a
+        // fused kernel covers the shape (the same bits as the two launches)
+        if (compute::launch_qk_norm_rope_store_attention(
+                q_->half_data(), k_->half_data(), v_->half_data(), q_norm, k_norm, heads, kv_heads, head_dim,
+                state ? 0 : pos, state ? state_position : nullptr, state ? plan_length : 0,
+                static_cast<int>(max_context_), config_.rope_theta, eps, layer.k_cache->half_data(),
+                layer.v_cache->half_data(), static_cast<float*>(scores_->data()), scores_->bytes(),
+                attn_out_->half_data())) {
+        } else if (state) {
             compute::launch_qk_norm_rope_store_at(q_->half_data(), k_->half_data(), v_->half_data(), q_norm, k_norm,
                                                   heads, kv_heads, head_dim, state_position,
                                                   static_cast<int>(max_context_), config_.rope_theta, eps,

@@ -327,6 +327,10 @@ struct MfmaLds {
     static constexpr size_t kMlFloats = (size_t)NW * 8 * 2;
     static constexpr size_t kMerge = (kMlFloats + (size_t)NW * 2 * 8 * 16 * 4) * sizeof(float);
     static constexpr size_t kBytes = kMerge > kMWaveLds * NW ? kMerge : kMWaveLds * NW;
+    // with the q/k prologue: q' of up to 8 heads, then per wave k' and v of the step
+    static constexpr size_t kQs = kBytes;
+    static constexpr size_t kKv = kQs + 8 * 128 * 2;
+    static constexpr size_t kPrepBytes = kKv + (size_t)NW * 2 * 128 * 2;
 };
 
 __device__ __forceinline__ f32x4 mfma16(half4 a, half4 b, f32x4 c) {
@@ -337,12 +341,19 @@ __device__ __forceinline__ half4 as_half4(uint32_t lo, uint32_t hi) {
     return __builtin_bit_cast(half4, u32x2{lo, hi});
 }
 
-template <int GP, int kDepth, int NW>
+// kPrep: the launch also does the step's q/k head RMSNorm + RoPE and KV
+// store (QkPrep).  Every workgroup forms q' of its group's heads (one wave
+// per head, the arithmetic of the standalone kernel) while its first tiles
+// load; the one wave whose positions end at the step's position forms k',
+// stores k' and v into the caches and puts them in place of the cache row it
+// loaded for that position (all lanes that load the row, clamped duplicates
+// included), so nothing reads the row before it is written.
+template <int GP, int kDepth, int NW, bool kPrep>
 __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     long long seq_stride, const int32_t* __restrict__ positions, int position, int max_len, int heads,
     int kv_heads, int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, QkPrep prep) {
     constexpr int HD = 128;
     static_assert(GP >= 2 && GP <= 8, "group");
     extern __shared__ __align__(16) uint8_t smem[];
@@ -361,6 +372,12 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     const int w0 = min(b1, b0 + wave * sub);
     const int w1 = min(b1, w0 + sub);
 
+    // the step's position (kPrep): within the planned range it is the last
+    // position L - 1 and lies in exactly one wave's range
+    const int p_raw = positions ? positions[seq] : position;
+    const int pos_row = L - 1;
+    const bool has_pos = kPrep && p_raw >= 0 && p_raw < max_len && w0 <= pos_row && pos_row < w1;
+
     uint16_t* vt = reinterpret_cast<uint16_t*>(smem + (size_t)wave * kMWaveLds);
     const uint16_t* kbase = k_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + 8 * grp;
     const uint16_t* vbase = v_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + 8 * grp;
@@ -371,7 +388,31 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     // issued, so that q's round trip overlaps theirs
     const bool q_ok = col < group;
     u32x4 q_raw[4];
-    {
+    // kPrep: raw q of the heads this wave forms (dims lane, lane + 64), the
+    // step's k and v of this kv head, the norm weights; all loads
+    // unconditional (a missing weight reads q and is not used)
+    constexpr int kHeadsPerWave = (GP + NW - 1) / NW;
+    uint16_t pq[kHeadsPerWave][2], pk[2], pv[2], pqw[2], pkw[2];
+    if constexpr (kPrep) {
+#pragma unroll
+        for (int j = 0; j < kHeadsPerWave; ++j) {
+            const int h = min(wave + j * NW, group - 1);
+            const uint16_t* qh = q + ((size_t)seq * heads + kvh * group + h) * HD;
+            pq[j][0] = qh[lane];
+            pq[j][1] = qh[64 + lane];
+        }
+        const size_t kv_off = ((size_t)seq * kv_heads + kvh) * HD;
+        const uint16_t* qw = prep.q_norm ? prep.q_norm : q;
+        const uint16_t* kw = prep.k_norm ? prep.k_norm : q;
+        pk[0] = prep.k[kv_off + lane];
+        pk[1] = prep.k[kv_off + 64 + lane];
+        pv[0] = prep.v[kv_off + lane];
+        pv[1] = prep.v[kv_off + 64 + lane];
+        pqw[0] = qw[lane];
+        pqw[1] = qw[64 + lane];
+        pkw[0] = kw[lane];
+        pkw[1] = kw[64 + lane];
+    } else {
         const uint16_t* qh = q + ((size_t)seq * heads + kvh * group + (q_ok ? col : group - 1)) * HD + 8 * grp;
 #pragma unroll
         for (int t = 0; t < 4; ++t) q_raw[t] = *reinterpret_cast<const u32x4*>(qh + 32 * t);
@@ -394,7 +435,17 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
         }
     };
 
+    const uint16_t* kv_new = reinterpret_cast<const uint16_t*>(smem + MfmaLds<NW>::kKv) + (size_t)wave * 2 * HD;
     auto process = [&](int d, int t0) {
+        if constexpr (kPrep) {
+            if (has_pos && min(t0 + col, w1 - 1) == pos_row) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    kr[d][t] = *reinterpret_cast<const u32x4*>(kv_new + 32 * t + 8 * grp);
+                    vr[d][t] = *reinterpret_cast<const u32x4*>(kv_new + HD + 32 * t + 8 * grp);
+                }
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t) *reinterpret_cast<u32x4*>(vt + col * kMStride + 32 * t + 8 * grp) = vr[d][t];
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -467,7 +518,57 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
         load_tile(d, w0 + d * kMTile);
         __builtin_amdgcn_sched_barrier(0);
     }
-    {
+    if constexpr (kPrep) {
+        uint16_t* qs = reinterpret_cast<uint16_t*>(smem + MfmaLds<NW>::kQs);   // [GP][HD]
+#pragma unroll
+        for (int j = 0; j < kHeadsPerWave; ++j) {
+            const int h = wave + j * NW;
+            if (h < GP) {   // wave-uniform
+                uint16_t y0 = pq[j][0], y1 = pq[j][1];
+                if (prep.q_norm != nullptr) {
+                    const float x0 = h2f(y0), x1 = h2f(y1);
+                    const float inv = head_inv_rms(x0, x1, HD, prep.eps);
+                    y0 = f2h_rne(x0 * inv * h2f(pqw[0]));
+                    y1 = f2h_rne(x1 * inv * h2f(pqw[1]));
+                }
+                uint16_t r0, r1;
+                rope_pair(h2f(y0), h2f(y1), lane, HD, p_raw, prep.theta, r0, r1);
+                const bool real = h < group;   // padding heads: q = 0
+                qs[h * HD + lane] = real ? r0 : (uint16_t)0;
+                qs[h * HD + 64 + lane] = real ? r1 : (uint16_t)0;
+            }
+        }
+        if (has_pos) {   // wave-uniform
+            uint16_t y0 = pk[0], y1 = pk[1];
+            if (prep.k_norm != nullptr) {
+                const float x0 = h2f(y0), x1 = h2f(y1);
+                const float inv = head_inv_rms(x0, x1, HD, prep.eps);
+                y0 = f2h_rne(x0 * inv * h2f(pkw[0]));
+                y1 = f2h_rne(x1 * inv * h2f(pkw[1]));
+            }
+            uint16_t r0, r1;
+            rope_pair(h2f(y0), h2f(y1), lane, HD, p_raw, prep.theta, r0, r1);
+            const size_t row = (size_t)seq * seq_stride + (size_t)pos_row * row_step + (size_t)kvh * HD;
+            prep.k_cache[row + lane] = r0;
+            prep.k_cache[row + 64 + lane] = r1;
+            prep.v_cache[row + lane] = pv[0];
+            prep.v_cache[row + 64 + lane] = pv[1];
+            uint16_t* kvw = reinterpret_cast<uint16_t*>(smem + MfmaLds<NW>::kKv) + (size_t)wave * 2 * HD;
+            kvw[lane] = r0;
+            kvw[64 + lane] = r1;
+            kvw[HD + lane] = pv[0];
+            kvw[HD + 64 + lane] = pv[1];
+        }
+        lds_barrier();   // q' of every head, and this wave's k' / v (tile loads stay in flight)
+        const uint16_t* qh = qs + (q_ok ? col : 0) * HD + 8 * grp;
+        const uint32_t keep = q_ok ? 0xffffffffu : 0u;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(qh + 32 * t);
+            qb[t][0] = as_half4(v.x & keep, v.y & keep);
+            qb[t][1] = as_half4(v.z & keep, v.w & keep);
+        }
+    } else {
         const uint32_t keep = q_ok ? 0xffffffffu : 0u;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -619,10 +720,18 @@ hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream
 template <int GP, int kDepth, int NW = kWaves>
 hipError_t launch_mfma(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
     const float scale_log2 = (float)(1.4426950408889634 / sqrt(128.0));
-    launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth, NW>), dim3(p.n_splits, a.kv_heads, a.nseq),
-                          dim3(NW * kWave), MfmaLds<NW>::kBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
-                          a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
-                          a.workspace, p.n_splits, a.out);
+    const dim3 grid(p.n_splits, a.kv_heads, a.nseq);
+    if (a.prep != nullptr) {
+        launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth, NW, true>), grid, dim3(NW * kWave),
+                              MfmaLds<NW>::kPrepBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
+                              a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
+                              a.workspace, p.n_splits, a.out, *a.prep);
+    } else {
+        launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth, NW, false>), grid, dim3(NW * kWave),
+                              MfmaLds<NW>::kBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
+                              a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
+                              a.workspace, p.n_splits, a.out, QkPrep{});
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_splits <= 1) return e;
     launch_kernel((attn_merge_kernel<128>), dim3(a.heads, a.nseq), dim3(kBlock), kMergeLds, stream, a.workspace,
@@ -639,6 +748,7 @@ hipError_t launch_depth(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
             default: return hipErrorInvalidValue;
         }
     }
+    if (a.prep != nullptr) return hipErrorInvalidValue;   // the q/k prologue exists only in the MFMA kernel
     switch (p.depth) {
         case 1: return launch_split<HD, GP, 1>(a, p, s);
         case 2: return launch_split<HD, GP, 2>(a, p, s);

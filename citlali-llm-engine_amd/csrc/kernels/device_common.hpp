@@ -179,6 +179,28 @@ __device__ __forceinline__ float norm_block_sum(float s, float* red) {
     return ((red[0] + red[1]) + red[2]) + red[3];
 }
 
+// Head RMSNorm and NeoX RoPE pieces shared by the q/k norm + RoPE + store
+// kernel and the attention launch that does the same work in its prologue,
+// so both give the same bits.  rsqrt(mean(x^2) + eps) of a 128-dim head whose
+// values lie two per lane of a wave (dims l and l + 64): the two 64-lane sums
+// added, as a 128-thread block sums them (wave 0 holds dims 0..63).
+__device__ __forceinline__ float head_inv_rms(float x_lo, float x_hi, int head_dim, float eps) {
+    const float s0 = wave_sum(x_lo * x_lo), s1 = wave_sum(x_hi * x_hi);
+    return rsqrtf((s0 + s1) / (float)head_dim + eps);
+}
+
+// Pair (i, i + head_dim/2) rotated by position * theta^(-2i/head_dim), each
+// result rounded to fp16 (kernels.cu:485-521).
+__device__ __forceinline__ void rope_pair(float x0, float x1, int i, int head_dim, int position, float theta,
+                                          uint16_t& y0, uint16_t& y1) {
+    const float inv_freq = powf(theta, -(float)(2 * i) / (float)head_dim);
+    const float angle = (float)position * inv_freq;
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    y0 = f2h_rne(x0 * cs - x1 * sn);
+    y1 = f2h_rne(x0 * sn + x1 * cs);
+}
+
 // Orders LDS traffic between lanes of one wave (no workgroup barrier): the
 // fence makes earlier LDS writes visible, the wave barrier stops the compiler
 // from moving memory operations across this point.

@@ -176,13 +176,10 @@ __global__ void qk_norm_rope_store_kernel(uint16_t* __restrict__ q, const uint16
     uint16_t* dst = is_q ? q + (size_t)head * head_dim
                          : k_cache + (size_t)position * kv_size + (size_t)head * head_dim;
     if (i < half) {
-        const float inv_freq = powf(theta, -(float)(2 * i) / (float)head_dim);
-        const float angle = (float)position * inv_freq;
-        float sn, cs;
-        sincosf(angle, &sn, &cs);
-        const float x0 = h2f(vals[i]), x1 = h2f(vals[half + i]);
-        dst[i] = f2h_rne(x0 * cs - x1 * sn);
-        dst[half + i] = f2h_rne(x0 * sn + x1 * cs);
+        uint16_t y0, y1;
+        rope_pair(h2f(vals[i]), h2f(vals[half + i]), i, head_dim, position, theta, y0, y1);
+        dst[i] = y0;
+        dst[half + i] = y1;
     }
     if (!is_q && i < head_dim)
         v_cache[(size_t)position * kv_size + (size_t)head * head_dim + i] = v[(size_t)head * head_dim + i];
@@ -193,13 +190,10 @@ __global__ void rope_kernel(uint16_t* __restrict__ data, int head_dim, int posit
     const int head = blockIdx.x, i = threadIdx.x, half = head_dim / 2;
     if (i >= half) return;
     const size_t base = (size_t)head * head_dim;
-    const float inv_freq = powf(theta, -(float)(2 * i) / (float)head_dim);
-    const float angle = (float)position * inv_freq;
-    float s, c;
-    sincosf(angle, &s, &c);
-    const float x0 = h2f(data[base + i]), x1 = h2f(data[base + half + i]);
-    data[base + i] = f2h_rne(x0 * c - x1 * s);
-    data[base + half + i] = f2h_rne(x0 * s + x1 * c);
+    uint16_t y0, y1;
+    rope_pair(h2f(data[base + i]), h2f(data[base + half + i]), i, head_dim, position, theta, y0, y1);
+    data[base + i] = y0;
+    data[base + half + i] = y1;
 }
 
 __global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __restrict__ u,

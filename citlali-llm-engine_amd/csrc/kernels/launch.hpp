@@ -49,6 +49,19 @@ hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool 
                              hipStream_t s);
 
 // ---- decode attention (attention.hip) ----
+// The step's q/k head RMSNorm + RoPE and KV store done inside the attention
+// launch (head_dim 128, GQA group 2..8): k and v of this step before the
+// norm ([nseq][kv_heads][128]), the norm weights (null: no norm), writable
+// views of the caches.  Attention then reads q as it comes from the q GEMV.
+struct QkPrep {
+    const uint16_t* k;
+    const uint16_t* v;
+    const uint16_t* q_norm;
+    const uint16_t* k_norm;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    float theta, eps;
+};
 struct AttnArgs {
     const uint16_t* q;         // [nseq][heads][head_dim]
     const uint16_t* k_cache;   // sequence s at k_cache + s*seq_stride: [pos][kv_heads][head_dim]
@@ -60,6 +73,7 @@ struct AttnArgs {
     int nseq, heads, kv_heads, head_dim;
     float* workspace;          // chunk partials, attention_workspace_bytes()
     uint16_t* out;             // [nseq][heads][head_dim]
+    const QkPrep* prep;        // null: q already normed and roped, the step's k/v already stored
 };
 struct AttnPlan {
     int gp;        // padded GQA group (1, 2, 4, 8)

@@ -84,6 +84,8 @@ SIGNATURES = [
     ("citlali_hip_embed_at", c_int, [_P, _P, c_int, _P, c_int]),
     ("citlali_hip_qk_norm_rope_store_at", c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, _P, c_int, c_float,
                                                   c_float, _P, _P]),
+    ("citlali_hip_qk_norm_rope_store_attention", c_int, [_P, _P, _P, _P, _P, c_int, c_int, c_int, c_int, _P, c_int,
+                                                         c_int, c_float, c_float, _P, _P, _P, c_size_t, _P]),
     ("citlali_hip_stream_create", c_int, [POINTER(c_void_p)]),
     ("citlali_hip_stream_destroy", c_int, [_P]),
     ("citlali_hip_graph_begin", c_int, []),

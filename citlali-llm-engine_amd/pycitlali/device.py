@@ -263,6 +263,22 @@ def qk_norm_rope_store_at(q, k, v, q_norm, k_norm, heads: int, kv_heads: int, he
               ctypes.c_float(eps), _vp(k_cache), _vp(v_cache))
 
 
+def qk_norm_rope_store_attention(q, k, v, q_norm, k_norm, heads: int, kv_heads: int, head_dim: int, position,
+                                 plan_length: int, max_context: int, theta: float, eps: float, k_cache, v_cache,
+                                 workspace, workspace_bytes: int, out) -> None:
+    """qk_norm_rope_store(_at) + attention(_batched) in one launch; `position`
+    is an int (scalar form) or a device int32 (then plan_length is the
+    bucket)."""
+    null = ctypes.c_void_p(0)
+    scalar = isinstance(position, int)
+    _lib.call("citlali_hip_qk_norm_rope_store_attention", _vp(q), _vp(k), _vp(v),
+              _vp(q_norm) if q_norm is not None else null, _vp(k_norm) if k_norm is not None else null, int(heads),
+              int(kv_heads), int(head_dim), int(position) if scalar else 0, null if scalar else _vp(position),
+              int(plan_length), int(max_context), ctypes.c_float(theta), ctypes.c_float(eps), _vp(k_cache),
+              _vp(v_cache), _vp(workspace) if workspace is not None else null, ctypes.c_size_t(workspace_bytes),
+              _vp(out))
+
+
 class Stream:
     """A HIP stream of the library (citlali_hip_stream_create)."""
 

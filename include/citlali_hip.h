@@ -130,6 +130,25 @@ size_t citlali_hip_attention_workspace_bytes(int max_positions_bound, int nseq, 
                                              int head_dim);
 int citlali_hip_release_workspace(void);
 
+/* citlali_hip_qk_norm_rope_store (or its _at form) followed by
+ * citlali_hip_attention (or citlali_hip_attention_batched with nseq 1 and
+ * max_positions_bound plan_length) in one launch, with the same results bit
+ * for bit: q is the q GEMV's output (read only, not updated), k / v the
+ * step's k and v; the step's k (normed, roped) and v are stored into the
+ * caches at the position and attention reads them.  The position is
+ * *position_at when that is not NULL (then plan_length is the bucket, and a
+ * position at or beyond it writes nothing), else `position`.  workspace:
+ * citlali_hip_attention_workspace_bytes(plan length) bytes.  No reference
+ * counterpart (qwen_model.cpp:315-338 makes these separate launches);
+ * CITLALI_ERR_UNSUPPORTED unless head_dim is 128 with 2..8 query heads per
+ * kv head. */
+int citlali_hip_qk_norm_rope_store_attention(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                             const uint16_t* q_norm, const uint16_t* k_norm, int heads,
+                                             int kv_heads, int head_dim, int position, const int32_t* position_at,
+                                             int plan_length, int max_context, float theta, float eps,
+                                             uint16_t* k_cache, uint16_t* v_cache, void* workspace,
+                                             size_t workspace_bytes, uint16_t* out);
+
 /* launch_store_kv (kernels.h:36, kernels.cu:829-843): the cache layout
  * contract, cache[position*kv_size + i] = k[i]. */
 int citlali_hip_store_kv(const uint16_t* k, const uint16_t* v, uint16_t* k_cache, uint16_t* v_cache, int position,
