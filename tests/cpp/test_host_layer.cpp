@@ -333,7 +333,8 @@ struct SynthModel {
     HostMatrix embd, output;
     std::vector<uint16_t> output_norm;
     struct Layer {
-        std::vector<uint16_t> attn_norm, q_norm, k_norm, ffn_norm;
+        std::vector<uint16_t> attn_norm, q_norm, k_norm, ffn_norm;   // q_norm / k_norm empty: absent
+        std::vector<uint16_t> q_bias, k_bias, v_bias, o_bias, gate_bias, up_bias, down_bias;   // empty: absent
         HostMatrix q, k, v, o, gate, up, down;
     };
     std::vector<Layer> layers;
@@ -363,6 +364,7 @@ SynthModel make_model(uint64_t seed, int hidden, int heads, int kv_heads, int ff
     m.cfg.head_count = heads;
     m.cfg.head_count_kv = kv_heads;
     m.cfg.head_dim = 128;
+    m.cfg.architecture = "qwen3";
     m.embd = make_matrix(r, GgufTensorType::Q6_K, vocab, hidden, std::sqrt((double)hidden));   // rows of rms ~1
     m.output = make_matrix(r, GgufTensorType::Q6_K, vocab, hidden, 3.0);
     m.output_norm = make_norm(r, hidden);
@@ -385,6 +387,36 @@ SynthModel make_model(uint64_t seed, int hidden, int heads, int kv_heads, int ff
     return m;
 }
 
+std::vector<uint16_t> make_bias(Rng& r, int n, double scale) {
+    std::vector<uint16_t> v(n);
+    for (auto& h : v) h = orc_f2h_rne((float)(scale * r.normal()));
+    return v;
+}
+
+// Qwen2-style: biases on q/k/v (the Qwen2 checkpoints), and here on o and
+// the FFN matrices too (so every bias add and the unfused gate/up path run);
+// no q/k head norms.
+SynthModel make_model_biased(uint64_t seed, int hidden, int heads, int kv_heads, int ff, int layers, int vocab) {
+    SynthModel m = make_model(seed, hidden, heads, kv_heads, ff, layers, vocab);
+    m.cfg.architecture = "qwen2";
+    Rng r{seed * 7 + 5};
+    const int nq = heads * 128, nkv = kv_heads * 128;
+    for (auto& L : m.layers) {
+        L.q_norm.clear();
+        L.k_norm.clear();
+        L.q_bias = make_bias(r, nq, 0.5);
+        L.k_bias = make_bias(r, nkv, 0.5);
+        L.v_bias = make_bias(r, nkv, 0.5);
+        L.o_bias = make_bias(r, hidden, 0.1);
+        L.gate_bias = make_bias(r, ff, 0.2);
+        L.up_bias = make_bias(r, ff, 0.2);
+        L.down_bias = make_bias(r, hidden, 0.1);
+    }
+    return m;
+}
+
+const uint16_t* opt(const std::vector<uint16_t>& v) { return v.empty() ? nullptr : v.data(); }
+
 OrcMatrix orc_of(const HostMatrix& m) { return {m.type == GgufTensorType::Q4_K ? ORC_Q4K : ORC_Q6K, m.bytes.data()}; }
 
 // The oracle's model view; `drop` zeroes nothing, it only selects layers.
@@ -399,7 +431,9 @@ struct OracleModel {
             OrcLayer o{};
             o.attn_norm = L.attn_norm.data();
             o.q = orc_of(L.q); o.k = orc_of(L.k); o.v = orc_of(L.v); o.o = orc_of(L.o);
-            o.q_norm = L.q_norm.data(); o.k_norm = L.k_norm.data();
+            o.q_norm = opt(L.q_norm); o.k_norm = opt(L.k_norm);
+            o.q_bias = opt(L.q_bias); o.k_bias = opt(L.k_bias); o.v_bias = opt(L.v_bias); o.o_bias = opt(L.o_bias);
+            o.gate_bias = opt(L.gate_bias); o.up_bias = opt(L.up_bias); o.down_bias = opt(L.down_bias);
             o.ffn_norm = L.ffn_norm.data();
             o.gate = orc_of(L.gate); o.up = orc_of(L.up); o.down = orc_of(L.down);
             layers.push_back(o);
@@ -451,8 +485,18 @@ model::QwenWeights device_weights(const SynthModel& s) {
         d.attn_k = handle_of(L.k, b + "attn_k.weight");
         d.attn_v = handle_of(L.v, b + "attn_v.weight");
         d.attn_o = handle_of(L.o, b + "attn_output.weight");
-        d.attn_q_norm = handle_of_norm(L.q_norm, b + "attn_q_norm.weight");
-        d.attn_k_norm = handle_of_norm(L.k_norm, b + "attn_k_norm.weight");
+        const auto vec = [&](const std::vector<uint16_t>& v, const std::string& name) {
+            return v.empty() ? model::WeightHandle{} : handle_of_norm(v, b + name);
+        };
+        d.attn_q_norm = vec(L.q_norm, "attn_q_norm.weight");
+        d.attn_k_norm = vec(L.k_norm, "attn_k_norm.weight");
+        d.attn_q_bias = vec(L.q_bias, "attn_q.bias");
+        d.attn_k_bias = vec(L.k_bias, "attn_k.bias");
+        d.attn_v_bias = vec(L.v_bias, "attn_v.bias");
+        d.attn_o_bias = vec(L.o_bias, "attn_output.bias");
+        d.ffn_gate_bias = vec(L.gate_bias, "ffn_gate.bias");
+        d.ffn_up_bias = vec(L.up_bias, "ffn_up.bias");
+        d.ffn_down_bias = vec(L.down_bias, "ffn_down.bias");
         d.ffn_norm = handle_of_norm(L.ffn_norm, b + "ffn_norm.weight");
         d.ffn_gate = handle_of(L.gate, b + "ffn_gate.weight");
         d.ffn_up = handle_of(L.up, b + "ffn_up.weight");
@@ -539,8 +583,9 @@ void test_model_load_errors() {
 // lockstep, and the GPU must stay within the spread that this 1-ulp input
 // noise produces in the oracle.
 void greedy_run(uint64_t seed, int prompt, int steps, int* identical, int* ties, int hidden = 2048,
-                int heads = 16) {
-    SynthModel s = make_model(seed, hidden, heads, 8, 4096, 2, 8192);
+                int heads = 16, bool biased = false) {
+    SynthModel s = biased ? make_model_biased(seed, hidden, heads, 8, 4096, 2, 8192)
+                          : make_model(seed, hidden, heads, 8, 4096, 2, 8192);
     const int ctx = 128;
     model::QwenModel gpu;
     gpu.load(s.cfg, device_weights(s), ctx);
@@ -603,10 +648,10 @@ void greedy_run(uint64_t seed, int prompt, int steps, int* identical, int* ties,
                                              " exceeds twice the logit error " + std::to_string(step_err));
         }
     }
-    std::printf("greedy decode seed %llu (hidden %d): %d prompt tokens, %d greedy steps: %d identical, %d numerical ties; "
+    std::printf("greedy decode seed %llu (hidden %d%s): %d prompt tokens, %d greedy steps: %d identical, %d numerical ties; "
                 "max |logit diff| / rms(logits) = %.2e (rms %.2f; by position%s); oracle under 1-ulp embedding "
                 "noise: %.2e; min oracle top-2 margin %.2e\n",
-                (unsigned long long)seed, hidden, prompt, steps, *identical, *ties, worst, rms_sum / (prompt + steps),
+                (unsigned long long)seed, hidden, biased ? ", Qwen2-style biases, no q/k norm" : "", prompt, steps, *identical, *ties, worst, rms_sum / (prompt + steps),
                 profile.c_str(), ctl_worst, min_margin);
     check(worst <= ctl_worst, "GPU logits within the oracle's own 1-ulp sensitivity");
 }
@@ -621,7 +666,11 @@ void test_forward_greedy() {
     // their own launch (hidden 2048 above uses the separate launches)
     greedy_run(10, 8, 64, &identical, &ties, 4096, 32);
     all_ties += ties;
-    check(all_ties <= 4, "at most one numerical tie per 64-step run on average");
+    // biases on every matrix, no q/k head norms (the unfused gate/up path and
+    // the attention prologue without norm weights)
+    greedy_run(12, 8, 64, &identical, &ties, 2048, 16, /*biased=*/true);
+    all_ties += ties;
+    check(all_ties <= 5, "at most one numerical tie per 64-step run on average");
 }
 
 // QwenModel::decode_greedy (captured steps replayed per token) against the
@@ -671,7 +720,7 @@ void test_decode_greedy_graph(int hidden, int heads) {
 void write_synth_gguf(const SynthModel& s, const std::string& path) {
     bench::GgufOut o;
     std::vector<std::vector<float>> norms;   // borrowed by `o` until write()
-    norms.reserve(1 + 4 * s.layers.size());
+    norms.reserve(1 + 11 * s.layers.size());
     const auto matrix = [&](const std::string& name, const HostMatrix& m) {
         o.tensor(name, {(uint64_t)m.cols, (uint64_t)m.rows}, m.type, m.bytes.data(), m.bytes.size());
     };
@@ -681,18 +730,19 @@ void write_synth_gguf(const SynthModel& s, const std::string& path) {
         o.tensor(name, {(uint64_t)h.size()}, GgufTensorType::F32, norms.back().data(), h.size() * 4);
     };
     const model::QwenConfig& c = s.cfg;
-    o.str("general.architecture", "qwen3");
+    const std::string a = c.architecture;
+    o.str("general.architecture", a);
     o.strings("tokenizer.ggml.tokens", (int)c.vocab_size);
-    o.u32("qwen3.context_length", c.context_length);
-    o.u32("qwen3.embedding_length", c.embedding_length);
-    o.u32("qwen3.block_count", c.block_count);
-    o.u32("qwen3.feed_forward_length", c.feed_forward_length);
-    o.u32("qwen3.attention.head_count", c.head_count);
-    o.u32("qwen3.attention.head_count_kv", c.head_count_kv);
-    o.u32("qwen3.attention.key_length", c.head_dim);
-    o.u32("qwen3.attention.value_length", c.head_dim);
-    o.f32("qwen3.attention.layer_norm_rms_epsilon", c.rms_norm_eps);
-    o.f32("qwen3.rope.freq_base", c.rope_theta);
+    o.u32(a + ".context_length", c.context_length);
+    o.u32(a + ".embedding_length", c.embedding_length);
+    o.u32(a + ".block_count", c.block_count);
+    o.u32(a + ".feed_forward_length", c.feed_forward_length);
+    o.u32(a + ".attention.head_count", c.head_count);
+    o.u32(a + ".attention.head_count_kv", c.head_count_kv);
+    o.u32(a + ".attention.key_length", c.head_dim);
+    o.u32(a + ".attention.value_length", c.head_dim);
+    o.f32(a + ".attention.layer_norm_rms_epsilon", c.rms_norm_eps);
+    o.f32(a + ".rope.freq_base", c.rope_theta);
     matrix("token_embd.weight", s.embd);
     norm("output_norm.weight", s.output_norm);
     matrix("output.weight", s.output);
@@ -704,8 +754,18 @@ void write_synth_gguf(const SynthModel& s, const std::string& path) {
         matrix(b + "attn_k.weight", L.k);
         matrix(b + "attn_v.weight", L.v);
         matrix(b + "attn_output.weight", L.o);
-        norm(b + "attn_q_norm.weight", L.q_norm);
-        norm(b + "attn_k_norm.weight", L.k_norm);
+        const auto opt_vec = [&](const std::string& name, const std::vector<uint16_t>& v) {
+            if (!v.empty()) norm(b + name, v);
+        };
+        opt_vec("attn_q_norm.weight", L.q_norm);
+        opt_vec("attn_k_norm.weight", L.k_norm);
+        opt_vec("attn_q.bias", L.q_bias);
+        opt_vec("attn_k.bias", L.k_bias);
+        opt_vec("attn_v.bias", L.v_bias);
+        opt_vec("attn_output.bias", L.o_bias);
+        opt_vec("ffn_gate.bias", L.gate_bias);
+        opt_vec("ffn_up.bias", L.up_bias);
+        opt_vec("ffn_down.bias", L.down_bias);
         norm(b + "ffn_norm.weight", L.ffn_norm);
         matrix(b + "ffn_gate.weight", L.gate);
         matrix(b + "ffn_up.weight", L.up);
@@ -736,15 +796,15 @@ std::vector<uint16_t> dequant_f16(const HostMatrix& m) {
 // (bound as greedy_run: within the oracle's own spread under 1-ulp input
 // noise; a differing token only where the oracle's gap is within twice the
 // logit error).
-void test_load_from_gguf() {
-    SynthModel s = make_model(23, 1024, 8, 4, 2048, 2, 512);
+void test_load_from_gguf(bool biased) {
+    SynthModel s = biased ? make_model_biased(24, 1024, 8, 4, 2048, 2, 512) : make_model(23, 1024, 8, 4, 2048, 2, 512);
     const int ctx = 64, vocab = 512, prompt = 8, steps = 40;
-    const std::string path = temp_path("synth_qwen3.gguf");
+    const std::string path = temp_path(biased ? "synth_qwen2.gguf" : "synth_qwen3.gguf");
     write_synth_gguf(s, path);
     io::GgufFile g;
     g.load(path);
     const model::QwenConfig c = model::QwenConfig::from_gguf(g);
-    check(c.architecture == "qwen3" && c.vocab_size == 512 && c.embedding_length == 1024 && c.block_count == 2 &&
+    check(c.architecture == s.cfg.architecture && c.vocab_size == 512 && c.embedding_length == 1024 && c.block_count == 2 &&
               c.feed_forward_length == 2048 && c.head_count == 8 && c.head_count_kv == 4 && c.head_dim == 128 &&
               c.value_dim == 128 && c.context_length == s.cfg.context_length && c.rms_norm_eps == s.cfg.rms_norm_eps &&
               c.rope_theta == s.cfg.rope_theta,
@@ -813,9 +873,9 @@ void test_load_from_gguf() {
         }
         tok = ta;
     }
-    std::printf("GGUF load: KeepQuantized = WeightHandles over %d positions; DequantizeToFp16 vs fp16 oracle: "
+    std::printf("GGUF load (%s): KeepQuantized = WeightHandles over %d positions; DequantizeToFp16 vs fp16 oracle: "
                 "max |logit diff| / rms = %.2e (oracle under 1-ulp embedding noise %.2e), %d/%d greedy tokens differ\n",
-                prompt + steps, worst, ctl_worst, mismatched, steps);
+                biased ? "qwen2, biases, no q/k norm" : "qwen3", prompt + steps, worst, ctl_worst, mismatched, steps);
     check(worst <= std::max(ctl_worst, 1e-3), "fp16-path logits within the oracle's own 1-ulp sensitivity");
     check(mismatched <= 2, "fp16-path greedy tokens");
 }
@@ -847,7 +907,8 @@ int main(int argc, char** argv) {
             test_forward_greedy();
             test_decode_greedy_graph(2048, 16);
             test_decode_greedy_graph(4096, 32);
-            test_load_from_gguf();
+            test_load_from_gguf(false);
+            test_load_from_gguf(true);
             compute::synchronize();
         } else {
             std::printf("usage: %s cpu|gpu\n", argv[0]);
