@@ -154,6 +154,7 @@ __device__ __forceinline__ u32x4 add_run(u32x4 x, u32x4 d, bool has_d) {
     return u32x4{add_pair(x.x, d.x), add_pair(x.y, d.y), add_pair(x.z, d.z), add_pair(x.w, d.w)};
 }
 __device__ __forceinline__ float sq_pair(uint32_t v, float s) {
+#pragma clang fp contract(off)   // the same bits in every kernel that inlines it
     const float a = h2f(v & 0xffffu), b = h2f(v >> 16);
     s += a * a;
     return s + b * b;
@@ -185,6 +186,7 @@ __device__ __forceinline__ float norm_block_sum(float s, float* red) {
 // values lie two per lane of a wave (dims l and l + 64): the two 64-lane sums
 // added, as a 128-thread block sums them (wave 0 holds dims 0..63).
 __device__ __forceinline__ float head_inv_rms(float x_lo, float x_hi, int head_dim, float eps) {
+#pragma clang fp contract(off)   // the same bits in every kernel that inlines it
     const float s0 = wave_sum(x_lo * x_lo), s1 = wave_sum(x_hi * x_hi);
     return rsqrtf((s0 + s1) / (float)head_dim + eps);
 }
@@ -193,6 +195,7 @@ __device__ __forceinline__ float head_inv_rms(float x_lo, float x_hi, int head_d
 // result rounded to fp16 (kernels.cu:485-521).
 __device__ __forceinline__ void rope_pair(float x0, float x1, int i, int head_dim, int position, float theta,
                                           uint16_t& y0, uint16_t& y1) {
+#pragma clang fp contract(off)   // the same bits in every kernel that inlines it
     const float inv_freq = powf(theta, -(float)(2 * i) / (float)head_dim);
     const float angle = (float)position * inv_freq;
     float sn, cs;

@@ -155,8 +155,30 @@ struct Q4K {
         return f;
     }
 
-    // Contribution of lane j (group pair 2j, 2j+1) of super-block b.
+    // The x values lane j needs for super-block b (its 64 staged values and
+    // the two 32-value sums); loop-invariant across rows, so the streaming
+    // loops load them into registers once.
+    struct XRegs { u32x4 l[4], h[4]; f32x2 s; };
+    __device__ static __forceinline__ XRegs xload(const uint32_t* xp, const float* sx, int j, int b) {
+        const uint32_t* xl = xp + ((b * kQK + 64 * j) >> 1);
+        XRegs r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            r.l[i] = *reinterpret_cast<const u32x4*>(xl + 4 * i);
+            r.h[i] = *reinterpret_cast<const u32x4*>(xl + 16 + 4 * i);
+        }
+        r.s = *reinterpret_cast<const f32x2*>(sx + b * 8 + 2 * j);
+        return r;
+    }
     __device__ static __forceinline__ float dot(const Frag& f, int j, const uint32_t* xp, const float* sx, int b) {
+        return dot(f, j, xload(xp, sx, j, b));
+    }
+
+    // Contribution of lane j (group pair 2j, 2j+1) of a super-block.
+    __device__ static __forceinline__ float dot(const Frag& f, int j, const XRegs& x) {
+        // no fused multiply-adds: every kernel that inlines this computes the
+        // same bits (the fused launches equal the plain ones)
+#pragma clang fp contract(off)
         // 6-bit (scale, min) codes of groups 2j, 2j+1 (kernels.cu:174-186):
         // work on the two bytes k, k+1 of each 4-byte scale word at once.
         const uint32_t sh = (uint32_t)((2 * j) & 3) * 8u;
@@ -174,15 +196,8 @@ struct Q4K {
         const float d = h2f(f.hdr.x & 0xffffu);
         const float dmin = h2f(f.hdr.x >> 16);
 
-        const uint32_t* xl = xp + ((b * kQK + 64 * j) >> 1);
-        const u32x4 xl0 = *reinterpret_cast<const u32x4*>(xl + 0);
-        const u32x4 xl1 = *reinterpret_cast<const u32x4*>(xl + 4);
-        const u32x4 xl2 = *reinterpret_cast<const u32x4*>(xl + 8);
-        const u32x4 xl3 = *reinterpret_cast<const u32x4*>(xl + 12);
-        const u32x4 xh0 = *reinterpret_cast<const u32x4*>(xl + 16);
-        const u32x4 xh1 = *reinterpret_cast<const u32x4*>(xl + 20);
-        const u32x4 xh2 = *reinterpret_cast<const u32x4*>(xl + 24);
-        const u32x4 xh3 = *reinterpret_cast<const u32x4*>(xl + 28);
+        const u32x4 xl0 = x.l[0], xl1 = x.l[1], xl2 = x.l[2], xl3 = x.l[3];
+        const u32x4 xh0 = x.h[0], xh1 = x.h[1], xh2 = x.h[2], xh3 = x.h[3];
         const uint32_t q[8] = {f.q0.x, f.q0.y, f.q0.z, f.q0.w, f.q1.x, f.q1.y, f.q1.z, f.q1.w};
         const uint32_t XL[16] = {xl0.x, xl0.y, xl0.z, xl0.w, xl1.x, xl1.y, xl1.z, xl1.w,
                                  xl2.x, xl2.y, xl2.z, xl2.w, xl3.x, xl3.y, xl3.z, xl3.w};
@@ -198,7 +213,7 @@ struct Q4K {
             phi = dot2(w & 0x00f000f0u, XH[2 * t], phi);       // q * 2^-20
             phi = dot2(w8 & 0x00f000f0u, XH[2 * t + 1], phi);
         }
-        const f32x2 s = *reinterpret_cast<const f32x2*>(sx + b * 8 + 2 * j);
+        const f32x2 s = x.s;
         const float a_lo = d * (float)(sc & 0xffu) * 16777216.0f;
         const float a_hi = d * (float)(sc >> 8) * 1048576.0f;
         const float m_lo = dmin * (float)(mn & 0xffu);
@@ -238,8 +253,28 @@ struct Q6K {
         return f;
     }
 
-    __device__ static __forceinline__ float dot(const Frag& f, int l4, const uint32_t* xp, const float* sx, int b) {
+    // The x values lane l4 needs for super-block b: slice k, pair t of its
+    // 16 positions per slice, and the four slice sums (loop-invariant).
+    struct XRegs { u32x2 v[4][4]; f32x4 s; };
+    __device__ static __forceinline__ XRegs xload(const uint32_t* xp, const float* sx, int l4, int b) {
         const int h = l4 >> 1, ih = l4 & 1;
+        // x pairs of slice k: values 128h + 32k + 16ih + [0,16)
+        const uint32_t* xb = xp + ((b * kQK + 128 * h + 16 * ih) >> 1);
+        XRegs r;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) r.v[k][t] = *reinterpret_cast<const u32x2*>(xb + k * 16 + 2 * t);
+        r.s = *reinterpret_cast<const f32x4*>(sx + b * 16 + h * 8 + ih * 4);
+        return r;
+    }
+    __device__ static __forceinline__ float dot(const Frag& f, int l4, const uint32_t* xp, const float* sx, int b) {
+        return dot(f, l4, xload(xp, sx, l4, b));
+    }
+
+    __device__ static __forceinline__ float dot(const Frag& f, int l4, const XRegs& x) {
+#pragma clang fp contract(off)   // the same bits in every kernel that inlines it
+        const int ih = l4 & 1;
         const float d = h2f((uint16_t)f.dbits);
         // int8 scales sc[8h + ih + 2k], k = 0..3 (kernels.cu:166-167)
         // (int8_t casts: the result must be converted as a signed value)
@@ -249,33 +284,30 @@ struct Q6K {
         const float sc2 = (float)(int8_t)(f.s1 >> sh);
         const float sc3 = (float)(int8_t)(f.s1 >> (sh + 16u));
 
-        // x pairs of slice k: values 128h + 32k + 16ih + [0,16)
-        const uint32_t* xb = xp + ((b * kQK + 128 * h + 16 * ih) >> 1);
         float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
             const uint32_t wa = f.wa[t], wb = f.wb[t], u = f.u[t];
-            const uint32_t wa8 = wa >> 8, wb8 = wb >> 8, u8 = u >> 8;
-            // 6-bit code = low nibble (ql) | two qh bits << 4, in bits 0..5
-            // of each fp16 half (bytes 0/2 of the word, then bytes 1/3).
-            const uint32_t c0a = (wa & 0x000f000fu) | ((u << 4) & 0x00300030u);
-            const uint32_t c0b = (wa8 & 0x000f000fu) | ((u8 << 4) & 0x00300030u);
-            const uint32_t c1a = (wb & 0x000f000fu) | ((u << 2) & 0x00300030u);
-            const uint32_t c1b = (wb8 & 0x000f000fu) | ((u8 << 2) & 0x00300030u);
-            const uint32_t c2a = ((wa >> 4) & 0x000f000fu) | (u & 0x00300030u);
-            const uint32_t c2b = ((wa8 >> 4) & 0x000f000fu) | (u8 & 0x00300030u);
-            const uint32_t c3a = ((wb >> 4) & 0x000f000fu) | ((u >> 2) & 0x00300030u);
-            const uint32_t c3b = ((wb8 >> 4) & 0x000f000fu) | ((u8 >> 2) & 0x00300030u);
-            const u32x2 x0 = *reinterpret_cast<const u32x2*>(xb + 0 * 16 + 2 * t);
-            const u32x2 x1 = *reinterpret_cast<const u32x2*>(xb + 1 * 16 + 2 * t);
-            const u32x2 x2 = *reinterpret_cast<const u32x2*>(xb + 2 * 16 + 2 * t);
-            const u32x2 x3 = *reinterpret_cast<const u32x2*>(xb + 3 * 16 + 2 * t);
+            // 6-bit codes of the word's four bytes for each slice k: low
+            // nibble (ql) | the slice's two qh bits << 4, one byte each;
+            // then bytes 0/2 and bytes 1/3 go to the two fp16 halves of a
+            // dot2 operand (one byte permute each, the other bytes zero).
+            const uint32_t k0 = (wa & 0x0f0f0f0fu) | ((u << 4) & 0x30303030u);
+            const uint32_t k1 = (wb & 0x0f0f0f0fu) | ((u << 2) & 0x30303030u);
+            const uint32_t k2 = ((wa >> 4) & 0x0f0f0f0fu) | (u & 0x30303030u);
+            const uint32_t k3 = ((wb >> 4) & 0x0f0f0f0fu) | ((u >> 2) & 0x30303030u);
+            constexpr uint32_t kEven = 0x0c020c00u, kOdd = 0x0c030c01u;   // 0x0c selects a zero byte
+            const uint32_t c0a = __builtin_amdgcn_perm(0u, k0, kEven), c0b = __builtin_amdgcn_perm(0u, k0, kOdd);
+            const uint32_t c1a = __builtin_amdgcn_perm(0u, k1, kEven), c1b = __builtin_amdgcn_perm(0u, k1, kOdd);
+            const uint32_t c2a = __builtin_amdgcn_perm(0u, k2, kEven), c2b = __builtin_amdgcn_perm(0u, k2, kOdd);
+            const uint32_t c3a = __builtin_amdgcn_perm(0u, k3, kEven), c3b = __builtin_amdgcn_perm(0u, k3, kOdd);
+            const u32x2 x0 = x.v[0][t], x1 = x.v[1][t], x2 = x.v[2][t], x3 = x.v[3][t];
             p0 = dot2(c0b, x0.y, dot2(c0a, x0.x, p0));
             p1 = dot2(c1b, x1.y, dot2(c1a, x1.x, p1));
             p2 = dot2(c2b, x2.y, dot2(c2a, x2.x, p2));
             p3 = dot2(c3b, x3.y, dot2(c3a, x3.x, p3));
         }
-        const f32x4 s = *reinterpret_cast<const f32x4*>(sx + b * 16 + h * 8 + ih * 4);
+        const f32x4 s = x.s;
         // sum (q6 - 32) x = 2^24 P - 32 S
         const float t0 = sc0 * (p0 * 16777216.0f - 32.0f * s.x);
         const float t1 = sc1 * (p1 * 16777216.0f - 32.0f * s.y);
@@ -348,6 +380,9 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
             __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
         }
     xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
+    typename QT::XRegs xr[S];   // this lane's x, the same for every row
+#pragma unroll
+    for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, t * QT::kSbPerStep + sub);
 
     for (int row = gw; row < N; row += M * W) {
 #pragma unroll
@@ -356,7 +391,7 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
             float acc = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
-                const float c = QT::dot(fr[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
+                const float c = QT::dot(fr[m * S + t], l4, xr[t]);
                 acc += c;
                 // Refill after the dot has read the slot (issue_after), in
                 // slot order (vmcnt retires loads in issue order: a reordered
@@ -443,6 +478,9 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
             __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
         }
     xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
+    typename QT::XRegs xr[S];   // this lane's x, the same for every row
+#pragma unroll
+    for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, t * QT::kSbPerStep + sub);
 
     for (int row = gw; row < N; row += M * W) {
 #pragma unroll
@@ -451,8 +489,8 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
             float ag = 0.f, au = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
-                const float cg = QT::dot(fg[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
-                const float cu = QT::dot(fu[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
+                const float cg = QT::dot(fg[m * S + t], l4, xr[t]);
+                const float cu = QT::dot(fu[m * S + t], l4, xr[t]);
                 ag += cg;
                 au += cu;
                 const int nr = issue_after(r + M * W, cg, cu);   // refill after the dots, in slot order
