@@ -27,7 +27,9 @@ layer, on this machine's host cores.  attention_cfg4
 (16 sequences in one batched attention launch).  decode_cfg5: BASELINE
 config 5 (the whole synthetic Qwen3-8B, greedy decode tok/s) from
 bin/decode_qwen3, its weights written to a GGUF file in the temp directory
-and loaded by QwenModel::load(GgufFile) (load time and GB/s reported).
+and loaded by QwenModel::load(GgufFile) (load time and GB/s reported);
+decode_cfg5_fp16: the same file loaded with DequantizeToFp16 (fp16 weights,
+the fp16 GEMVs), 64-token prompt then 128 greedy steps.
 """
 from __future__ import annotations
 
@@ -275,18 +277,20 @@ PMC_SUMMARY = os.path.join(ROOT, "profiles", "cfg3_layer_hbm_traffic_pmc.md")
 DECODE_BIN = os.path.join(ROOT, "citlali-llm-engine_amd", "bin", "decode_qwen3")
 
 
-def decode_cfg5():
+def decode_cfg5(fp16=False):
     """BASELINE config 5 beside the headline: the synthetic Qwen3-8B greedy
     decode through QwenModel (bin/decode_qwen3, a child process), loaded from
     a GGUF file of its weights (written to the temp directory, removed after
-    loading), 512-token prompt then 256 greedy steps; decode tok/s."""
+    loading), 512-token prompt then 256 greedy steps; decode tok/s.  fp16:
+    loaded with DequantizeToFp16, 64-token prompt then 128 steps."""
     import subprocess
     import tempfile
     if not os.path.exists(DECODE_BIN):
         return {"error": "citlali-llm-engine_amd/bin/decode_qwen3 is not built"}
     path = os.path.join(tempfile.gettempdir(), f"citlali_cfg5_{os.getpid()}.gguf")
+    cmd = [DECODE_BIN, "--gguf", path] + (["--fp16", "--prompt", "64", "--steps", "128"] if fp16 else [])
     try:
-        p = subprocess.run([DECODE_BIN, "--gguf", path], capture_output=True, text=True, timeout=600)
+        p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     finally:
         if os.path.exists(path):
             os.remove(path)
@@ -360,6 +364,7 @@ def main():
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
     line["decode_cfg5"] = None if args.no_decode else decode_cfg5()
+    line["decode_cfg5_fp16"] = None if args.no_decode else decode_cfg5(fp16=True)
     print(json.dumps(line), flush=True)
 
 

@@ -594,17 +594,24 @@ CITLALI_EXPORT int citlali_hip_graph_destroy(void* graph) {
     return CITLALI_OK;
 }
 
+namespace {
+// GEMV weight types of the grouped / fused entry points: GGUF Q4_K (12),
+// Q6_K (14) and F16 (1, fp16 rows), as the kernels' kinds 4, 6, 1
+bool fused_type_ok(int t) { return t == 12 || t == 14 || t == 1; }
+int fused_kind(int t) { return t == 14 ? 6 : t == 1 ? 1 : 4; }
+uintptr_t fused_walign(int t) { return t == 14 ? 4 : 16; }
+}  // namespace
+
 CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up,
                                                      const uint16_t* x, uint16_t* act, int in_f, int out_f) {
-    REQUIRE(gguf_type == 12 || gguf_type == 14, "matvec_gate_up_swiglu: GGUF type %d is not Q4_K or Q6_K",
-            gguf_type);
-    const uintptr_t walign = gguf_type == 12 ? 16 : 4;
+    REQUIRE(fused_type_ok(gguf_type), "matvec_gate_up_swiglu: GGUF type %d is not Q4_K, Q6_K or F16", gguf_type);
+    const uintptr_t walign = fused_walign(gguf_type);
     int st = check_matvec("matvec_gate_up_swiglu", w_gate, x, act, in_f, out_f, walign, 2);
     if (st) return st;
     REQUIRE(w_up && aligned(w_up, walign), "matvec_gate_up_swiglu: bad up weight");
     if (in_f != 4096 && in_f != 8192)
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_gate_up_swiglu: in_features %d has no fused kernel", in_f);
-    HIP_TRY(launch_matvec_gate_up_swiglu(gguf_type == 14 ? 6 : 4, w_gate, w_up, x, act, in_f, out_f, nullptr,
+    HIP_TRY(launch_matvec_gate_up_swiglu(fused_kind(gguf_type), w_gate, w_up, x, act, in_f, out_f, nullptr,
                                          g_stream));
     return CITLALI_OK;
 }
@@ -616,16 +623,19 @@ CITLALI_EXPORT int citlali_hip_matvec_group(int count, const int* gguf_types, co
     REQUIRE(gguf_types && weights && outputs && out_features, "matvec_group received a null array");
     int kinds[3];
     long long rows = 0;
+    int f16 = 0;
     for (int i = 0; i < count; ++i) {
-        REQUIRE(gguf_types[i] == 12 || gguf_types[i] == 14, "matvec_group: GGUF type %d is not Q4_K or Q6_K",
-                gguf_types[i]);
+        REQUIRE(fused_type_ok(gguf_types[i]), "matvec_group: GGUF type %d is not Q4_K, Q6_K or F16", gguf_types[i]);
         const int st = check_matvec("matvec_group", weights[i], x, outputs[i], in_f, out_features[i],
-                                    gguf_types[i] == 12 ? 16 : 4, 2);
+                                    fused_walign(gguf_types[i]), 2);
         if (st) return st;
-        kinds[i] = gguf_types[i] == 14 ? 6 : 4;
+        kinds[i] = fused_kind(gguf_types[i]);
+        f16 += kinds[i] == 1;
         rows += out_features[i];
     }
     REQUIRE(rows <= INT_MAX, "matvec_group: %lld rows in total exceed INT_MAX", rows);
+    if (f16 != 0 && f16 != count)
+        return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: F16 and quantized weights have no grouped kernel");
     if (in_f % 4096 != 0 || in_f > 16384)
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: in_features %d has no grouped kernel", in_f);
     HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, nullptr, g_stream));
@@ -658,16 +668,20 @@ CITLALI_EXPORT int citlali_hip_matvec_group_norm(int count, const int* gguf_type
     if (st) return st;
     int kinds[3];
     long long rows = 0;
+    int f16 = 0;
     for (int i = 0; i < count; ++i) {
-        REQUIRE(gguf_types[i] == 12 || gguf_types[i] == 14, "matvec_group_norm: GGUF type %d is not Q4_K or Q6_K",
+        REQUIRE(fused_type_ok(gguf_types[i]), "matvec_group_norm: GGUF type %d is not Q4_K, Q6_K or F16",
                 gguf_types[i]);
         st = check_matvec("matvec_group_norm", weights[i], x, outputs[i], in_f, out_features[i],
-                          gguf_types[i] == 12 ? 16 : 4, 2);
+                          fused_walign(gguf_types[i]), 2);
         if (st) return st;
-        kinds[i] = gguf_types[i] == 14 ? 6 : 4;
+        kinds[i] = fused_kind(gguf_types[i]);
+        f16 += kinds[i] == 1;
         rows += out_features[i];
     }
     REQUIRE(rows <= INT_MAX, "matvec_group_norm: %lld rows in total exceed INT_MAX", rows);
+    if (f16 != 0 && f16 != count)
+        return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group_norm: F16 and quantized weights have no grouped kernel");
     if (!norm_length_ok(in_f))
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group_norm: in_features %d has no grouped kernel", in_f);
     HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, &nrm, g_stream));
@@ -677,33 +691,33 @@ CITLALI_EXPORT int citlali_hip_matvec_group_norm(int count, const int* gguf_type
 CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu_norm(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up,
                                                           const uint16_t* x, const citlali_hip_norm* norm,
                                                           uint16_t* act, int in_f, int out_f) {
-    REQUIRE(gguf_type == 12 || gguf_type == 14, "matvec_gate_up_swiglu_norm: GGUF type %d is not Q4_K or Q6_K",
+    REQUIRE(fused_type_ok(gguf_type), "matvec_gate_up_swiglu_norm: GGUF type %d is not Q4_K, Q6_K or F16",
             gguf_type);
     NormIn nrm;
     int st = check_norm("matvec_gate_up_swiglu_norm", x, norm, in_f, &nrm);
     if (st) return st;
-    const uintptr_t walign = gguf_type == 12 ? 16 : 4;
+    const uintptr_t walign = fused_walign(gguf_type);
     st = check_matvec("matvec_gate_up_swiglu_norm", w_gate, x, act, in_f, out_f, walign, 2);
     if (st) return st;
     REQUIRE(w_up && aligned(w_up, walign), "matvec_gate_up_swiglu_norm: bad up weight");
     if (in_f != 4096 && in_f != 8192)
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_gate_up_swiglu_norm: in_features %d has no fused kernel", in_f);
-    HIP_TRY(launch_matvec_gate_up_swiglu(gguf_type == 14 ? 6 : 4, w_gate, w_up, x, act, in_f, out_f, &nrm,
+    HIP_TRY(launch_matvec_gate_up_swiglu(fused_kind(gguf_type), w_gate, w_up, x, act, in_f, out_f, &nrm,
                                          g_stream));
     return CITLALI_OK;
 }
 
 CITLALI_EXPORT int citlali_hip_matvec_norm(int gguf_type, const uint8_t* w, const uint16_t* x,
                                            const citlali_hip_norm* norm, void* y, int f32_out, int in_f, int out_f) {
-    REQUIRE(gguf_type == 12 || gguf_type == 14, "matvec_norm: GGUF type %d is not Q4_K or Q6_K", gguf_type);
+    REQUIRE(fused_type_ok(gguf_type), "matvec_norm: GGUF type %d is not Q4_K, Q6_K or F16", gguf_type);
     NormIn nrm;
     int st = check_norm("matvec_norm", x, norm, in_f, &nrm);
     if (st) return st;
-    st = check_matvec("matvec_norm", w, x, y, in_f, out_f, gguf_type == 12 ? 16 : 4, f32_out ? 4 : 2);
+    st = check_matvec("matvec_norm", w, x, y, in_f, out_f, fused_walign(gguf_type), f32_out ? 4 : 2);
     if (st) return st;
     if (!norm_length_ok(in_f))
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_norm: in_features %d has no prologue kernel", in_f);
-    HIP_TRY(launch_matvec_norm(gguf_type == 14 ? 6 : 4, w, x, nrm, y, f32_out != 0, in_f, out_f, g_stream));
+    HIP_TRY(launch_matvec_norm(fused_kind(gguf_type), w, x, nrm, y, f32_out != 0, in_f, out_f, g_stream));
     return CITLALI_OK;
 }
 

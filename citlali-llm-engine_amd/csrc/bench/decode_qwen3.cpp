@@ -17,11 +17,14 @@
 // PATH (layers of one byte set share their data in the file; the norms are
 // F32 ones) and the model is loaded from it by QwenModel::load(GgufFile)
 // with KeepQuantized, the reference's load path (qwen_model.cpp:45-186); the
-// file is removed after loading and the load time is reported.
+// file is removed after loading and the load time is reported.  `--fp16`
+// (with --gguf) loads it with DequantizeToFp16 instead, the reference's
+// default policy: every matrix becomes fp16 in device memory and the fp16
+// GEMVs run.
 // Prints one JSON line.
 //
 // usage: decode_qwen3 [--layers 36] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1] [--no-graph]
-//                     [--gguf PATH]
+//                     [--gguf PATH [--fp16]]
 #include "citlali/common.h"
 #include "citlali/compute/hip/kernels.h"
 #include "citlali/io/gguf_reader.h"
@@ -124,8 +127,11 @@ int main(int argc, char** argv) {
     const int distinct = arg(argc, argv, "--distinct", 4);
     const uint64_t seed = (uint64_t)arg(argc, argv, "--seed", 1);
     bool graph_pass = true;   // --no-graph: forward_token loop only (for tracing tools)
-    for (int i = 1; i < argc; ++i)
+    bool fp16_weights = false;
+    for (int i = 1; i < argc; ++i) {
         if (std::strcmp(argv[i], "--no-graph") == 0) graph_pass = false;
+        if (std::strcmp(argv[i], "--fp16") == 0) fp16_weights = true;
+    }
     try {
         if (citlali_hip_init(0) != CITLALI_OK) throw Error(citlali_hip_last_error());
         model::QwenConfig cfg;
@@ -217,7 +223,7 @@ int main(int argc, char** argv) {
             gguf_write_s = std::chrono::duration<double>(w1 - w0).count();
             io::GgufFile g;
             g.load(gguf_path);
-            m.load(g, (uint32_t)ctx, /*quantized=*/true);
+            m.load(g, (uint32_t)ctx, /*quantized=*/!fp16_weights);
             m.synchronize();
             load_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - w1).count();
             for (const auto& t : g.tensors()) loaded_bytes += (double)t.nbytes;
@@ -300,9 +306,12 @@ int main(int argc, char** argv) {
         const double decode_ms = graph_wall * 1e3;
         // bytes one decode step must read: every weight once, the KV cache
         // up to the position, the embedding row and the logits
-        const double layer_bytes = 9437184.0 * 2 + 2359296 + 3440640 + 28311552.0 * 2 + 41287680;
+        // (fp16 weights: every matrix as 2-byte values)
+        const double layer_bytes = fp16_weights ? 2.0 * ((double)NQ * H * 2 + (double)NKV * H * 2 + 3.0 * F * H)
+                                                : 9437184.0 * 2 + 2359296 + 3440640 + 28311552.0 * 2 + 41287680;
         const double mean_len = prompt + (steps + 1) / 2.0;
-        const double step_bytes = layer_bytes * layers + 510504960.0 + 3360 + V * 4.0 +
+        const double out_bytes = fp16_weights ? 2.0 * V * H : 510504960.0;
+        const double step_bytes = layer_bytes * layers + out_bytes + 3360 + V * 4.0 +
                                   (double)layers * 2 * 2 * NKV * mean_len;
         std::printf("{\"workload\": \"BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode\", \"layers\": %d, "
                     "\"distinct_layer_weight_sets\": %d, \"prompt\": %d, \"steps\": %d, \"decode_tok_per_s\": %.2f, "
@@ -319,7 +328,9 @@ int main(int argc, char** argv) {
                     step_bytes / (decode_ms * 1e-3 / steps) / 1e9, steps / (eager_ms * 1e-3), eager_ms / steps,
                     eager_wall * 1e3 / steps, match ? "true" : "false", prompt / (prompt_ms * 1e-3),
                     prompt_wall * 1e3 / prompt, setup_s, (unsigned long long)checksum,
-                    gguf_path ? "GGUF file, QwenModel::load(GgufFile) KeepQuantized" : "WeightHandles",
+                    gguf_path ? (fp16_weights ? "GGUF file, QwenModel::load(GgufFile) DequantizeToFp16"
+                                              : "GGUF file, QwenModel::load(GgufFile) KeepQuantized")
+                              : "WeightHandles",
                     file_bytes, gguf_write_s, load_s, load_s > 0 ? loaded_bytes / load_s / 1e9 : 0.0);
         if (!match) {
             std::fprintf(stderr, "decode_qwen3: decode_greedy tokens differ from the forward_token loop\n");

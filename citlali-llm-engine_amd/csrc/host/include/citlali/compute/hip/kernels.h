@@ -51,9 +51,11 @@ void launch_add_rms_norm(uint16_t* x, const uint16_t* delta, const uint16_t* wei
 void launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
                                const uint16_t* k_norm, int heads, int kv_heads, int head_dim, int position,
                                float theta, float eps, uint16_t* k_cache, uint16_t* v_cache);
-// launch_matvec_q4k / _q6k for `count` (1..3) weights that read the same
+// launch_matvec_q4k / _q6k (or launch_matvec_fp16, type F16, the weight
+// pointer to its fp16 rows) for `count` (1..3) weights that read the same
 // input (attn_q, attn_k, attn_v); returns false, launching nothing, when a
-// type is not Q4_K/Q6_K or no grouped kernel covers in_features.
+// type is not Q4_K/Q6_K/F16, F16 is mixed with quantized types, or no
+// grouped kernel covers in_features.
 bool launch_matvec_group(int count, const GgufTensorType* types, const uint8_t* const* weights,
                          const uint16_t* input, uint16_t* const* outputs, const int* out_features, int in_features);
 // GEMVs whose input is the residual add + RMSNorm of `input` (see
@@ -77,7 +79,8 @@ bool launch_matvec_gate_up_swiglu_norm(GgufTensorType type, const uint8_t* w_gat
                                        int in_features, int out_features);
 bool launch_matvec_norm(GgufTensorType type, const uint8_t* weight, const uint16_t* input, const NormInput& norm,
                         void* output, bool f32_out, int in_features, int out_features);
-// The ffn_gate and ffn_up GEMVs (both of `type`) then launch_swiglu; returns
+// The ffn_gate and ffn_up GEMVs (both of `type`: Q4_K, Q6_K or F16) then
+// launch_swiglu; returns
 // false, launching nothing, when no fused kernel covers the shape.
 bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
                                   const uint16_t* input, uint16_t* output, int in_features, int out_features);

@@ -94,23 +94,12 @@ void launch_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v
                                                      theta, eps, k_cache, v_cache));
 }
 
-bool launch_matvec_group(int count, const GgufTensorType* types, const uint8_t* const* weights,
-                         const uint16_t* input, uint16_t* const* outputs, const int* out_features, int in_features) {
-    require(count >= 1 && count <= 3, "launch_matvec_group: count must be 1, 2 or 3");
-    int codes[3];
-    for (int i = 0; i < count; ++i) {
-        if (types[i] != GgufTensorType::Q4_K && types[i] != GgufTensorType::Q6_K) return false;
-        codes[i] = static_cast<int>(types[i]);
-    }
-    const int st = citlali_hip_matvec_group(count, codes, weights, input, outputs, out_features, in_features);
-    if (st == CITLALI_ERR_UNSUPPORTED) return false;
-    CITLALI_HIP_CHECK(st);
-    return true;
-}
-
 namespace {
 citlali_hip_norm to_abi(const NormInput& n) { return citlali_hip_norm{n.delta, n.weight, n.sum_out, n.eps}; }
-bool kquant(GgufTensorType t) { return t == GgufTensorType::Q4_K || t == GgufTensorType::Q6_K; }
+// weight types the grouped / fused GEMV kernels read
+bool fusable(GgufTensorType t) {
+    return t == GgufTensorType::Q4_K || t == GgufTensorType::Q6_K || t == GgufTensorType::F16;
+}
 bool launched(int st) {
     if (st == CITLALI_ERR_UNSUPPORTED) return false;
     CITLALI_HIP_CHECK(st);
@@ -118,13 +107,24 @@ bool launched(int st) {
 }
 }  // namespace
 
+bool launch_matvec_group(int count, const GgufTensorType* types, const uint8_t* const* weights,
+                         const uint16_t* input, uint16_t* const* outputs, const int* out_features, int in_features) {
+    require(count >= 1 && count <= 3, "launch_matvec_group: count must be 1, 2 or 3");
+    int codes[3];
+    for (int i = 0; i < count; ++i) {
+        if (!fusable(types[i])) return false;
+        codes[i] = static_cast<int>(types[i]);
+    }
+    return launched(citlali_hip_matvec_group(count, codes, weights, input, outputs, out_features, in_features));
+}
+
 bool launch_matvec_group_norm(int count, const GgufTensorType* types, const uint8_t* const* weights,
                               const uint16_t* input, const NormInput& norm, uint16_t* const* outputs,
                               const int* out_features, int in_features) {
     require(count >= 1 && count <= 3, "launch_matvec_group_norm: count must be 1, 2 or 3");
     int codes[3];
     for (int i = 0; i < count; ++i) {
-        if (!kquant(types[i])) return false;
+        if (!fusable(types[i])) return false;
         codes[i] = static_cast<int>(types[i]);
     }
     const citlali_hip_norm n = to_abi(norm);
@@ -135,7 +135,7 @@ bool launch_matvec_group_norm(int count, const GgufTensorType* types, const uint
 bool launch_matvec_gate_up_swiglu_norm(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
                                        const uint16_t* input, const NormInput& norm, uint16_t* output,
                                        int in_features, int out_features) {
-    if (!kquant(type)) return false;
+    if (!fusable(type)) return false;
     const citlali_hip_norm n = to_abi(norm);
     return launched(citlali_hip_matvec_gate_up_swiglu_norm(static_cast<int>(type), w_gate, w_up, input, &n, output,
                                                            in_features, out_features));
@@ -143,7 +143,7 @@ bool launch_matvec_gate_up_swiglu_norm(GgufTensorType type, const uint8_t* w_gat
 
 bool launch_matvec_norm(GgufTensorType type, const uint8_t* weight, const uint16_t* input, const NormInput& norm,
                         void* output, bool f32_out, int in_features, int out_features) {
-    if (!kquant(type)) return false;
+    if (!fusable(type)) return false;
     const citlali_hip_norm n = to_abi(norm);
     return launched(citlali_hip_matvec_norm(static_cast<int>(type), weight, input, &n, output, f32_out ? 1 : 0,
                                             in_features, out_features));
@@ -151,12 +151,9 @@ bool launch_matvec_norm(GgufTensorType type, const uint8_t* weight, const uint16
 
 bool launch_matvec_gate_up_swiglu(GgufTensorType type, const uint8_t* w_gate, const uint8_t* w_up,
                                   const uint16_t* input, uint16_t* output, int in_features, int out_features) {
-    if (type != GgufTensorType::Q4_K && type != GgufTensorType::Q6_K) return false;
-    const int st = citlali_hip_matvec_gate_up_swiglu(static_cast<int>(type), w_gate, w_up, input, output,
-                                                     in_features, out_features);
-    if (st == CITLALI_ERR_UNSUPPORTED) return false;
-    CITLALI_HIP_CHECK(st);
-    return true;
+    if (!fusable(type)) return false;
+    return launched(citlali_hip_matvec_gate_up_swiglu(static_cast<int>(type), w_gate, w_up, input, output,
+                                                      in_features, out_features));
 }
 
 void launch_argmax(const float* logits, int n, int32_t* out_index) {

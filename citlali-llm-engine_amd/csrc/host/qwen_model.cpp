@@ -151,11 +151,36 @@ void QwenModel::allocate_runtime_buffers() {
     tokens_ = compute::make_device_buffer(static_cast<size_t>(max_context_) * sizeof(int32_t));
 }
 
+namespace {
+// A weight as an operand of the grouped / fused GEMV launches: a Q4_K / Q6_K
+// device tensor as its raw blocks, an fp16 device tensor as GGUF type F16
+// over its rows.  False for anything else or a buffer shorter than the
+// tensor (the separate launch then reports it).
+bool fused_operand(const WeightHandle& w, compute::GgufTensorType* type, const uint8_t** data) {
+    if (!w.buffer) return false;
+    const uint64_t n = w.cols() * w.rows();
+    if (w.storage_kind == compute::WeightStorageKind::QuantizedDevice) {
+        if (w.buffer->bytes() < compute::gguf_tensor_nbytes(w.gguf_type, n)) return false;
+        *type = w.gguf_type;
+        *data = w.device_quantized_data();
+        return true;
+    }
+    if (w.storage_kind == compute::WeightStorageKind::Fp16Device) {
+        if (w.buffer->bytes() < n * 2) return false;
+        *type = compute::GgufTensorType::F16;
+        *data = reinterpret_cast<const uint8_t*>(w.device_half_data());
+        return true;
+    }
+    return false;
+}
+}  // namespace
+
 // attn_q, attn_k and attn_v in one launch when all three are Q4_K/Q6_K
-// device tensors (the separate GEMVs' results bit for bit), reading `input`
-// or, with `norm`, the residual add + RMSNorm of it; false, nothing
-// launched, otherwise -- then LinearBackend::forward runs (and reports what
-// it rejects).  The bias adds that follow are independent of order.
+// device tensors or all three fp16 ones (the separate GEMVs' results bit for
+// bit), reading `input` or, with `norm`, the residual add + RMSNorm of it;
+// false, nothing launched, otherwise -- then LinearBackend::forward runs
+// (and reports what it rejects).  The bias adds that follow are independent
+// of order.
 bool QwenModel::launch_qkv_grouped(const QwenLayerWeights& layer, int hidden, const uint16_t* input,
                                    const compute::NormInput* norm) {
     const WeightHandle* w[3] = {&layer.attn_q, &layer.attn_k, &layer.attn_v};
@@ -165,12 +190,8 @@ bool QwenModel::launch_qkv_grouped(const QwenLayerWeights& layer, int hidden, co
     uint16_t* outputs[3];
     int rows[3];
     for (int i = 0; i < 3; ++i) {
-        if (w[i]->storage_kind != compute::WeightStorageKind::QuantizedDevice || !w[i]->buffer) return false;
-        // a short weight buffer: the separate launch reports it
-        if (w[i]->buffer->bytes() < compute::gguf_tensor_nbytes(w[i]->gguf_type, w[i]->cols() * w[i]->rows()))
-            return false;
-        types[i] = w[i]->gguf_type;
-        weights[i] = w[i]->device_quantized_data();
+        if (!fused_operand(*w[i], &types[i], &weights[i])) return false;
+        if ((types[i] == compute::GgufTensorType::F16) != (types[0] == compute::GgufTensorType::F16)) return false;
         outputs[i] = (*out[i])->half_data();
         rows[i] = as_int(w[i]->rows(), w[i]->name + " rows");
     }
@@ -284,23 +305,19 @@ void QwenModel::enqueue_token(int32_t token_id, int pos, int32_t* state, int pla
         linear_backend_->forward(layer.attn_o, attn_out_, attn_proj_);
         add_bias_if_present(layer.attn_o_bias, attn_proj_, hidden);
 
-        const bool fuse_ffn = layer.ffn_gate.storage_kind == compute::WeightStorageKind::QuantizedDevice &&
-                              layer.ffn_up.storage_kind == compute::WeightStorageKind::QuantizedDevice &&
-                              layer.ffn_gate.gguf_type == layer.ffn_up.gguf_type && !layer.ffn_gate_bias.buffer &&
-                              !layer.ffn_up_bias.buffer;
+        compute::GgufTensorType gate_type{}, up_type{};
+        const uint8_t *gate_w = nullptr, *up_w = nullptr;
+        const bool fuse_ffn = fused_operand(layer.ffn_gate, &gate_type, &gate_w) &&
+                              fused_operand(layer.ffn_up, &up_type, &up_w) && gate_type == up_type &&
+                              !layer.ffn_gate_bias.buffer && !layer.ffn_up_bias.buffer;
         const compute::NormInput ffn_in = prologue(layer.ffn_norm, attn_proj_->half_data());
-        if (fuse_ffn && compute::launch_matvec_gate_up_swiglu_norm(layer.ffn_gate.gguf_type,
-                                                                   layer.ffn_gate.device_quantized_data(),
-                                                                   layer.ffn_up.device_quantized_data(), xr[cur],
-                                                                   ffn_in, ff_act_->half_data(), hidden, ff)) {
+        if (fuse_ffn && compute::launch_matvec_gate_up_swiglu_norm(gate_type, gate_w, up_w, xr[cur], ffn_in,
+                                                                   ff_act_->half_data(), hidden, ff)) {
             cur ^= 1;
         } else {
             norm_into_buffer(layer.ffn_norm, attn_proj_->half_data());
-            if (!fuse_ffn || !compute::launch_matvec_gate_up_swiglu(layer.ffn_gate.gguf_type,
-                                                                    layer.ffn_gate.device_quantized_data(),
-                                                                    layer.ffn_up.device_quantized_data(),
-                                                                    norm_->half_data(), ff_act_->half_data(), hidden,
-                                                                    ff)) {
+            if (!fuse_ffn || !compute::launch_matvec_gate_up_swiglu(gate_type, gate_w, up_w, norm_->half_data(),
+                                                                    ff_act_->half_data(), hidden, ff)) {
                 linear_backend_->forward(layer.ffn_gate, norm_, gate_);
                 add_bias_if_present(layer.ffn_gate_bias, gate_, ff);
                 linear_backend_->forward(layer.ffn_up, norm_, up_);
@@ -327,9 +344,14 @@ void QwenModel::enqueue_token(int32_t token_id, int pos, int32_t* state, int pla
                                                 hidden, vocab);
         }
     } else {
-        norm_into_buffer(output_norm_, pending);
-        compute::launch_matvec_fp16_to_float(output_weight_.device_half_data(), norm_->half_data(), logits, hidden,
-                                             vocab);
+        compute::GgufTensorType type{};
+        const uint8_t* w = nullptr;
+        if (!fused_operand(output_weight_, &type, &w) ||
+            !compute::launch_matvec_norm(type, w, xr[cur], out_in, logits, true, hidden, vocab)) {
+            norm_into_buffer(output_norm_, pending);
+            compute::launch_matvec_fp16_to_float(output_weight_.device_half_data(), norm_->half_data(), logits,
+                                                 hidden, vocab);
+        }
     }
     if (state)
         compute::launch_argmax_advance(static_cast<const float*>(logits_->data()), vocab, state,

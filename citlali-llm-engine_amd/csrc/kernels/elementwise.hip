@@ -5,6 +5,7 @@
 // fp16 stores rounded nearest-even.
 #include "device_common.hpp"
 #include "launch.hpp"
+#include "citlali_hip.h"
 
 #include <math.h>
 
@@ -205,8 +206,9 @@ __global__ void swiglu_kernel(const uint16_t* __restrict__ g, const uint16_t* __
     }
 }
 
-// fp16 weights [N][K] (the DequantizeToFp16 path): one wave per row, 128-bit
-// loads when K is a multiple of 8, fp32 accumulation.
+// fp16 weights [N][K] (the DequantizeToFp16 path) for K not a multiple of
+// 256: one wave per row, 128-bit loads when K is a multiple of 8, fp32
+// accumulation.
 template <bool kF32>
 __global__ __launch_bounds__(kBlk) void matvec_f16_kernel(const uint16_t* __restrict__ w,
                                                           const uint16_t* __restrict__ x, void* __restrict__ y,
@@ -407,6 +409,9 @@ hipError_t launch_swiglu(const uint16_t* g, const uint16_t* u, uint16_t* out, in
 
 hipError_t launch_matvec_f16(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
                              hipStream_t s) {
+    // whole 256-value blocks: the streaming GEMV kernels (the fused fp16
+    // launches use the same ones, so their results are these bits)
+    if (K % 256 == 0 && K <= CITLALI_MAX_IN_FEATURES) return launch_matvec_f16_blocks(w, x, y, f32_out, K, N, s);
     const dim3 g((unsigned)((N + (kBlk / kWave) - 1) / (kBlk / kWave)));
     if (f32_out) launch_kernel(matvec_f16_kernel<true>, g, dim3(kBlk), 0, s, w, x, y, K, N);
     else launch_kernel(matvec_f16_kernel<false>, g, dim3(kBlk), 0, s, w, x, y, K, N);

@@ -42,7 +42,12 @@ inline void launch_kernel(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipS
 }
 
 // ---- fused dequant GEMV (matvec_kquant.hip) ----
+// kind: 4 = Q4_K, 6 = Q6_K, 1 = fp16 weights
 size_t matvec_lds_bytes(int kind, int K);
+// fp16 weights [N][K], K a multiple of 256 up to CITLALI_MAX_IN_FEATURES,
+// through the streaming kernels of the K-quant GEMVs
+hipError_t launch_matvec_f16_blocks(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                                    hipStream_t s);
 hipError_t launch_matvec_q4k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
                              hipStream_t s);
 hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
@@ -136,7 +141,7 @@ hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const
                                uint16_t* const* y, const int* n, int K, const NormIn* norm, hipStream_t s);
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
                                         uint16_t* act, int K, int N, const NormIn* norm, hipStream_t s);
-// kind 4 / 6 GEMV with the input prologue; K a multiple of 4096 up to 16384
+// kind 4 / 6 / 1 GEMV with the input prologue; K a multiple of 4096 up to 16384
 hipError_t launch_matvec_norm(int kind, const uint8_t* w, const uint16_t* x, const NormIn& norm, void* y,
                               bool f32_out, int K, int N, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);

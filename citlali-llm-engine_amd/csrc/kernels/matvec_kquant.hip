@@ -34,6 +34,7 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 // Layouts of the x-sum tables the traits read (see stage_x8).
 constexpr int kSum32 = 0;     // Q4K: sum over each 32-value group, [b][g]
 constexpr int kSumQ6 = 1;     // Q6K: 16-value slices, [b][h][ih][k]
+constexpr int kPlain = 2;     // F16: x in its own order, no sums
 constexpr int kBatch = 4;        // wave steps whose loads are issued together
 // The streaming kernels run two workgroups per CU (two waves per SIMD):
 // their register budget is capped to keep both resident.
@@ -47,6 +48,10 @@ constexpr int kWavesPerSimd = 2;
 // group sums in the layout kLayout.
 template <int kLayout>
 __device__ __forceinline__ void stage_x8(const u32x4 raw, int v8, uint32_t* xp, float* sx) {
+    if constexpr (kLayout == kPlain) {
+        *reinterpret_cast<u32x4*>(xp + (size_t)v8 * 4) = raw;
+        return;
+    }
     u32x4 perm;
     perm.x = __builtin_amdgcn_perm(raw.y, raw.x, 0x05040100u);
     perm.y = __builtin_amdgcn_perm(raw.y, raw.x, 0x07060302u);
@@ -145,6 +150,7 @@ struct Q4K {
     static constexpr int kSumLayout = kSum32;
     static constexpr int kLanesPerSb = 4;
     static constexpr int kSbPerStep = kWave / kLanesPerSb;
+    static constexpr int kHoistSteps = 4;   // x held in registers for rows of up to this many steps
     struct Frag { u32x4 hdr, q0, q1; };
 
     __device__ static __forceinline__ Frag load(const uint8_t* sb, int j) {
@@ -231,6 +237,7 @@ struct Q6K {
     static constexpr int kSumLayout = kSumQ6;
     static constexpr int kLanesPerSb = 4;
     static constexpr int kSbPerStep = kWave / kLanesPerSb;
+    static constexpr int kHoistSteps = 4;
     struct Frag { uint32_t wa[4], wb[4], u[4]; uint32_t s0, s1, dbits; };
 
     // lane_in_sb = 2*h + ih.  A 210-byte block starts on a 2-byte boundary;
@@ -317,6 +324,60 @@ struct Q6K {
     }
 };
 
+// ---------------------------------------------------------------------------
+// F16: fp16 weights (the DequantizeToFp16 path, kernels.cu:27-35, 381-412),
+// seen as 512-byte blocks of 256 values so that the streaming kernels below
+// serve them too.  Lane j of a block reads bytes 16 j + 64 i, i = 0..7:
+// every load instruction of a wave covers 64 contiguous bytes of each of
+// its 16 blocks.  x is staged in its own order; a weight word (two fp16)
+// meets the matching x word in one v_dot2_f32_f16.
+// ---------------------------------------------------------------------------
+struct F16 {
+    static constexpr int kBytes = 2 * kQK;
+    static constexpr int kSxPerBlock = 0;
+    static constexpr int kSumLayout = kPlain;
+    static constexpr int kLanesPerSb = 4;
+    static constexpr int kSbPerStep = kWave / kLanesPerSb;
+    // a lane's x is 32 registers per step: rows of three or four steps
+    // read it from LDS instead
+    static constexpr int kHoistSteps = 2;
+    struct Frag { u32x4 v[8]; };
+
+    __device__ static __forceinline__ Frag load(const uint8_t* sb, int j) {
+        Frag f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) f.v[i] = *reinterpret_cast<const u32x4*>(sb + 16 * j + 64 * i);
+        return f;
+    }
+
+    struct XRegs { u32x4 v[8]; };
+    __device__ static __forceinline__ XRegs xload(const uint32_t* xp, const float*, int j, int b) {
+        const uint32_t* xb = xp + ((b * kQK + 8 * j) >> 1);
+        XRegs r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r.v[i] = *reinterpret_cast<const u32x4*>(xb + 16 * i);
+        return r;
+    }
+    __device__ static __forceinline__ float dot(const Frag& f, int j, const uint32_t* xp, const float* sx, int b) {
+        return dot(f, j, xload(xp, sx, j, b));
+    }
+
+    // Sum over lane j's 64 values of the block: four fp32 partial chains
+    // (one per word of a 16-byte load), added in a fixed order.
+    __device__ static __forceinline__ float dot(const Frag& f, int, const XRegs& x) {
+#pragma clang fp contract(off)
+        float p0 = 0.f, p1 = 0.f, p2 = 0.f, p3 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            p0 = dot2(f.v[i].x, x.v[i].x, p0);
+            p1 = dot2(f.v[i].y, x.v[i].y, p1);
+            p2 = dot2(f.v[i].z, x.v[i].z, p2);
+            p3 = dot2(f.v[i].w, x.v[i].w, p3);
+        }
+        return (p0 + p1) + (p2 + p3);
+    }
+};
+
 template <bool kF32>
 __device__ __forceinline__ void store_y(void* y, int row, float v) {
     if constexpr (kF32) {
@@ -380,9 +441,12 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
             __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
         }
     xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
-    typename QT::XRegs xr[S];   // this lane's x, the same for every row
+    constexpr bool kHoist = S <= QT::kHoistSteps;
+    typename QT::XRegs xr[kHoist ? S : 1];   // this lane's x, the same for every row
+    if constexpr (kHoist) {
 #pragma unroll
-    for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, t * QT::kSbPerStep + sub);
+        for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, t * QT::kSbPerStep + sub);
+    }
 
     for (int row = gw; row < N; row += M * W) {
 #pragma unroll
@@ -391,7 +455,8 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
             float acc = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
-                const float c = QT::dot(fr[m * S + t], l4, xr[t]);
+                const float c = kHoist ? QT::dot(fr[m * S + t], l4, xr[kHoist ? t : 0])
+                                       : QT::dot(fr[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
                 acc += c;
                 // Refill after the dot has read the slot (issue_after), in
                 // slot order (vmcnt retires loads in issue order: a reordered
@@ -478,6 +543,7 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
             __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
         }
     xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
+    static_assert(S <= QT::kHoistSteps, "gate/up holds x in registers");
     typename QT::XRegs xr[S];   // this lane's x, the same for every row
 #pragma unroll
     for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, t * QT::kSbPerStep + sub);
@@ -684,8 +750,9 @@ void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int
 }
 
 template <bool kNorm>
-bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], const uint16_t* x, int K, const NormIn& nrm,
-                  hipStream_t s) {
+bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], bool f16, const uint16_t* x, int K,
+                  const NormIn& nrm, hipStream_t s) {
+    if (f16) return launch_stream_for<F16, false, 3, kNorm>(nb, set[0], x, lds_bytes<F16>(K), nrm, s);
     if (cnt[1] == 0) return launch_stream_for<Q4K, false, 3, kNorm>(nb, set[0], x, lds_bytes<Q4K>(K), nrm, s);
     if (cnt[0] == 0) return launch_stream_for<Q6K, false, 3, kNorm>(nb, set[1], x, lds_bytes<Q6K>(K), nrm, s);
     switch (nb) {
@@ -698,7 +765,7 @@ bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], const uint16_t*
 }
 
 template <class QT, bool kNorm>
-hipError_t launch_gate_up(const uint8_t* wg, const uint8_t* wu, const uint16_t* x, uint16_t* act, int K, int N,
+hipError_t launch_gate_up_t(const uint8_t* wg, const uint8_t* wu, const uint16_t* x, uint16_t* act, int K, int N,
                           const NormIn& nrm, hipStream_t stream) {
     const size_t lds = lds_bytes<QT>(K);
     int grid = 2 * device_cus();
@@ -718,10 +785,26 @@ hipError_t launch_gate_up(const uint8_t* wg, const uint8_t* wu, const uint16_t* 
     return hipGetLastError();
 }
 
+template <bool kNorm>
+hipError_t launch_gate_up(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x, uint16_t* act, int K,
+                          int N, const NormIn& nrm, hipStream_t s) {
+    switch (kind) {
+        case 6: return launch_gate_up_t<Q6K, kNorm>(wg, wu, x, act, K, N, nrm, s);
+        case 1: return launch_gate_up_t<F16, kNorm>(wg, wu, x, act, K, N, nrm, s);
+        default: return launch_gate_up_t<Q4K, kNorm>(wg, wu, x, act, K, N, nrm, s);
+    }
+}
+
 }  // namespace
 
 size_t matvec_lds_bytes(int kind, int K) {
-    return kind == 6 ? lds_bytes<Q6K>(K) : lds_bytes<Q4K>(K);
+    return kind == 6 ? lds_bytes<Q6K>(K) : kind == 1 ? lds_bytes<F16>(K) : lds_bytes<Q4K>(K);
+}
+
+hipError_t launch_matvec_f16_blocks(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
+                                    hipStream_t s) {
+    const uint8_t* wb = reinterpret_cast<const uint8_t*>(w);
+    return f32_out ? launch_matvec<F16, true>(wb, x, y, K, N, s) : launch_matvec<F16, false>(wb, x, y, K, N, s);
 }
 
 hipError_t launch_matvec_q4k(const uint8_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,
@@ -736,6 +819,9 @@ hipError_t launch_matvec_q6k(const uint8_t* w, const uint16_t* x, void* y, bool 
 
 hipError_t launch_matvec_norm(int kind, const uint8_t* w, const uint16_t* x, const NormIn& norm, void* y,
                               bool f32_out, int K, int N, hipStream_t s) {
+    if (kind == 1)
+        return f32_out ? launch_matvec_prologue<F16, true>(w, x, norm, y, K, N, s)
+                       : launch_matvec_prologue<F16, false>(w, x, norm, y, K, N, s);
     if (kind == 6)
         return f32_out ? launch_matvec_prologue<Q6K, true>(w, x, norm, y, K, N, s)
                        : launch_matvec_prologue<Q6K, false>(w, x, norm, y, K, N, s);
@@ -743,13 +829,17 @@ hipError_t launch_matvec_norm(int kind, const uint8_t* w, const uint16_t* x, con
                    : launch_matvec_prologue<Q4K, false>(w, x, norm, y, K, N, s);
 }
 
-// count matrices (1..3) reading x: kinds[i] 4 = Q4_K, 6 = Q6_K, n[i] rows,
-// fp16 outputs y[i].  hipErrorInvalidValue, nothing launched, for a length
-// other than 4096, 8192, 12288 or 16384.
+// count matrices (1..3) reading x: kinds[i] 4 = Q4_K, 6 = Q6_K, 1 = fp16
+// (all or none), n[i] rows, fp16 outputs y[i].  hipErrorInvalidValue,
+// nothing launched, for a length other than 4096, 8192, 12288 or 16384 or
+// fp16 mixed with quantized matrices.
 hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const* w, const uint16_t* x,
                                uint16_t* const* y, const int* n, int K, const NormIn* norm, hipStream_t s) {
     RowSet set[2];
     int cnt[2] = {0, 0};
+    int f16 = 0;
+    for (int i = 0; i < count; ++i) f16 += kinds[i] == 1;
+    if (f16 != 0 && f16 != count) return hipErrorInvalidValue;
     for (int i = 0; i < count; ++i) {
         const int t = kinds[i] == 6;
         const int j = cnt[t]++;
@@ -764,19 +854,17 @@ hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const
             set[t].end[j] = set[t].end[j - 1];
         }
     const int nb = K / kQK;
-    const bool ok = norm ? launch_group<true>(nb, set, cnt, x, K, *norm, s)
-                         : launch_group<false>(nb, set, cnt, x, K, kNoNorm, s);
+    const bool ok = norm ? launch_group<true>(nb, set, cnt, f16 != 0, x, K, *norm, s)
+                         : launch_group<false>(nb, set, cnt, f16 != 0, x, K, kNoNorm, s);
     return ok ? hipGetLastError() : hipErrorInvalidValue;
 }
 
-// kind 4: Q4_K, 6: Q6_K; in_features 4096 or 8192 (16 or 32 super-blocks)
+// kind 4: Q4_K, 6: Q6_K, 1: fp16; in_features 4096 or 8192 (16 or 32
+// blocks of 256)
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
                                         uint16_t* act, int K, int N, const NormIn* norm, hipStream_t s) {
-    if (norm)
-        return kind == 6 ? launch_gate_up<Q6K, true>(wg, wu, x, act, K, N, *norm, s)
-                         : launch_gate_up<Q4K, true>(wg, wu, x, act, K, N, *norm, s);
-    return kind == 6 ? launch_gate_up<Q6K, false>(wg, wu, x, act, K, N, kNoNorm, s)
-                     : launch_gate_up<Q4K, false>(wg, wu, x, act, K, N, kNoNorm, s);
+    return norm ? launch_gate_up<true>(kind, wg, wu, x, act, K, N, *norm, s)
+                : launch_gate_up<false>(kind, wg, wu, x, act, K, N, kNoNorm, s);
 }
 
 }  // namespace citlali::hip

@@ -67,6 +67,9 @@ class DeviceArray:
             pass
 
 
+# GGUF type codes of the GEMV weight kinds
+_GGUF_TYPE = {"q4k": 12, "q6k": 14, "fp16": 1}
+
 def synchronize() -> None:
     _lib.call("citlali_hip_synchronize")
 
@@ -220,14 +223,14 @@ def qk_norm_rope_store(q, k, v, q_norm, k_norm, heads: int, kv_heads: int, head_
 
 
 def matvec_gate_up_swiglu(kind: str, w_gate, w_up, x, act, in_features: int, out_features: int) -> None:
-    _lib.call("citlali_hip_matvec_gate_up_swiglu", 12 if kind == "q4k" else 14, _vp(w_gate), _vp(w_up), _vp(x),
+    _lib.call("citlali_hip_matvec_gate_up_swiglu", _GGUF_TYPE[kind], _vp(w_gate), _vp(w_up), _vp(x),
               _vp(act), int(in_features), int(out_features))
 
 
 def matvec_group(kinds, weights, x, outputs, out_features, in_features: int) -> None:
     """One launch of up to three Q4_K/Q6_K GEMVs that read `x`."""
     n = len(kinds)
-    types = (ctypes.c_int * n)(*[12 if k == "q4k" else 14 for k in kinds])
+    types = (ctypes.c_int * n)(*[_GGUF_TYPE[k] for k in kinds])
     ws = (ctypes.c_void_p * n)(*[w.ptr for w in weights])
     ys = (ctypes.c_void_p * n)(*[y.ptr for y in outputs])
     rows = (ctypes.c_int * n)(*[int(r) for r in out_features])
@@ -334,7 +337,7 @@ def _norm(delta, weight, sum_out, eps):
 
 def matvec_group_norm(kinds, weights, x, delta, weight, sum_out, eps, outputs, out_features, in_features) -> None:
     n = len(kinds)
-    types = (ctypes.c_int * n)(*[12 if k == "q4k" else 14 for k in kinds])
+    types = (ctypes.c_int * n)(*[_GGUF_TYPE[k] for k in kinds])
     ws = (ctypes.c_void_p * n)(*[w.ptr for w in weights])
     ys = (ctypes.c_void_p * n)(*[y.ptr for y in outputs])
     rows = (ctypes.c_int * n)(*[int(r) for r in out_features])
@@ -345,13 +348,13 @@ def matvec_group_norm(kinds, weights, x, delta, weight, sum_out, eps, outputs, o
 def matvec_gate_up_swiglu_norm(kind, w_gate, w_up, x, delta, weight, sum_out, eps, act, in_features: int,
                                out_features: int) -> None:
     nrm = _norm(delta, weight, sum_out, eps)
-    _lib.call("citlali_hip_matvec_gate_up_swiglu_norm", 12 if kind == "q4k" else 14, _vp(w_gate), _vp(w_up), _vp(x),
+    _lib.call("citlali_hip_matvec_gate_up_swiglu_norm", _GGUF_TYPE[kind], _vp(w_gate), _vp(w_up), _vp(x),
               ctypes.byref(nrm), _vp(act), int(in_features), int(out_features))
 
 
 def matvec_norm(kind, w, x, delta, weight, sum_out, eps, y, in_features: int, out_features: int,
                 f32_out: bool = False) -> None:
     nrm = _norm(delta, weight, sum_out, eps)
-    _lib.call("citlali_hip_matvec_norm", 12 if kind == "q4k" else 14, _vp(w), _vp(x), ctypes.byref(nrm), _vp(y),
+    _lib.call("citlali_hip_matvec_norm", _GGUF_TYPE[kind], _vp(w), _vp(x), ctypes.byref(nrm), _vp(y),
               1 if f32_out else 0, int(in_features), int(out_features))
 

@@ -87,6 +87,9 @@ def q6k_blocks(rng: Rng, n_blocks: int, d_lo: float = 1e-3, d_hi: float = 1e-2) 
 
 
 def quant_matrix(kind: str, rng: Rng, rows: int, cols: int, **kw) -> np.ndarray:
-    """Row-major [rows][cols/256] super-blocks of the given kind ("q4k"/"q6k")."""
+    """Row-major [rows][cols/256] super-blocks of the given kind ("q4k"/"q6k"),
+    or for "fp16" a [rows*cols] matrix of N(0, 1) fp16 bits."""
+    if kind == "fp16":
+        return normal_f16(rng, rows * cols)
     nb = rows * (cols // QK)
     return q4k_blocks(rng, nb, **kw) if kind == "q4k" else q6k_blocks(rng, nb, **kw)

@@ -233,21 +233,27 @@ int citlali_hip_add_rms_norm(uint16_t* x, const uint16_t* delta, const uint16_t*
 int citlali_hip_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_t* v, const uint16_t* q_norm,
                                    const uint16_t* k_norm, int heads, int kv_heads, int head_dim, int position,
                                    float theta, float eps, uint16_t* k_cache, uint16_t* v_cache);
-/* LinearBackend::forward for ffn_gate and ffn_up (both of GGUF type
- * `gguf_type`, 12 = Q4_K or 14 = Q6_K) then launch_swiglu.  Returns
+/* GEMV weight types of the grouped / fused entry points below: GGUF type
+ * 12 = Q4_K or 14 = Q6_K (KeepQuantized blocks; Q4_K 16-byte, Q6_K 4-byte
+ * aligned), or 1 = F16 (DequantizeToFp16 rows, the weight pointer to the
+ * fp16 values, 16-byte aligned; the results equal citlali_hip_matvec_fp16 /
+ * _to_float bit for bit).
+ *
+ * LinearBackend::forward for ffn_gate and ffn_up (both of GGUF type
+ * `gguf_type`) then launch_swiglu.  Returns
  * CITLALI_ERR_UNSUPPORTED, launching nothing, for in_features other than
  * 4096 or 8192 -- then use the separate launches. */
 int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up, const uint16_t* x,
                                       uint16_t* act, int in_features, int out_features);
 /* LinearBackend::forward (linear_backend.cpp:17-61) for `count` (1..3)
- * KeepQuantized weights that read the same input -- attn_q, attn_k and
- * attn_v of one layer (qwen_model.cpp:315-321) -- in one launch.
- * gguf_types[i] is 12 = Q4_K or 14 = Q6_K, outputs[i] receives
+ * weights that read the same input -- attn_q, attn_k and attn_v of one
+ * layer (qwen_model.cpp:315-321) -- in one launch.  gguf_types[i] is 12 =
+ * Q4_K, 14 = Q6_K or 1 = F16 (all or none), outputs[i] receives
  * out_features[i] fp16 values: the results of the separate
- * citlali_hip_matvec_q4k / _q6k calls bit for bit.  Outputs must not overlap
- * each other or x.  Returns CITLALI_ERR_UNSUPPORTED, launching nothing, for
- * in_features other than 4096, 8192, 12288 or 16384 -- then use the
- * separate launches. */
+ * citlali_hip_matvec_q4k / _q6k / _fp16 calls bit for bit.  Outputs must
+ * not overlap each other or x.  Returns CITLALI_ERR_UNSUPPORTED, launching
+ * nothing, for in_features other than 4096, 8192, 12288 or 16384, or F16
+ * mixed with quantized types -- then use the separate launches. */
 int citlali_hip_matvec_group(int count, const int* gguf_types, const uint8_t* const* weights, const uint16_t* x,
                              uint16_t* const* outputs, const int* out_features, int in_features);
 
@@ -274,7 +280,7 @@ int citlali_hip_matvec_group_norm(int count, const int* gguf_types, const uint8_
 int citlali_hip_matvec_gate_up_swiglu_norm(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up,
                                            const uint16_t* x, const citlali_hip_norm* norm, uint16_t* act,
                                            int in_features, int out_features);
-/* gguf_type 12 / 14; y fp16 (f32_out 0) or fp32 (f32_out 1) */
+/* gguf_type 12 / 14 / 1; y fp16 (f32_out 0) or fp32 (f32_out 1) */
 int citlali_hip_matvec_norm(int gguf_type, const uint8_t* w, const uint16_t* x, const citlali_hip_norm* norm,
                             void* y, int f32_out, int in_features, int out_features);
 

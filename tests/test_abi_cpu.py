@@ -83,7 +83,7 @@ def test_matvec_group_validation():
     st, msg = g(4, ints(12, 12, 12, 12), ptrs(*[0x10000] * 4), ptrs(*[0x10000] * 4), ints(4, 4, 4, 4), 4096)
     assert st == 1 and "count" in msg
     st, msg = g(2, ints(12, 10), ptrs(0x10000, 0x10000), ptrs(0x10000, 0x10000), ints(4, 4), 4096)
-    assert st == 1 and "not Q4_K or Q6_K" in msg
+    assert st == 1 and "not Q4_K, Q6_K or F16" in msg
     st, msg = g(2, ints(12, 14), ptrs(0x10000, 0), ptrs(0x10000, 0x10000), ints(4, 4), 4096)
     assert st == 1 and "null buffer" in msg
     st, msg = g(1, ints(12), ptrs(0x10004), ptrs(0x10000), ints(4), 4096)
@@ -93,6 +93,11 @@ def test_matvec_group_validation():
     assert st == 1 and "INT_MAX" in msg
     st, msg = g(1, ints(14), ptrs(0x10000), ptrs(0x10000), ints(4), 2048)
     assert st == 2 and "no grouped kernel" in msg
+    # fp16 weights (GGUF type 1): 16-byte aligned, never mixed with quantized ones
+    st, msg = g(2, ints(1, 14), ptrs(0x10000, 0x10000), ptrs(0x10000, 0x10000), ints(4, 4), 4096)
+    assert st == 2 and "F16 and quantized" in msg
+    st, msg = g(1, ints(1), ptrs(0x10004), ptrs(0x10000), ints(4), 4096)
+    assert st == 1 and "16-byte aligned" in msg
     st, msg = _status("citlali_hip_matvec_group", 1, None, ptrs(0x10000), fake, ptrs(0x10000), ints(4), 4096)
     assert st == 1 and "null array" in msg
 
@@ -116,7 +121,7 @@ def test_norm_prologue_validation():
                       fake, 0, 4096, 8)
     assert st == 1 and "sum_out must not be the input" in msg
     st, msg = _status("citlali_hip_matvec_norm", 10, fake, fake, ctypes.byref(ok), fake, 0, 4096, 8)
-    assert st == 1 and "not Q4_K or Q6_K" in msg
+    assert st == 1 and "not Q4_K, Q6_K or F16" in msg
     st, msg = _status("citlali_hip_matvec_norm", 14, fake, fake, ctypes.byref(ok), fake, 1, 2048, 8)
     assert st == 2 and "no prologue kernel" in msg
     st, msg = _status("citlali_hip_matvec_group_norm", 1, ints(12), ptrs(0x10000), fake, ctypes.byref(ok),

@@ -146,7 +146,12 @@ def test_argmax_matches_host_rule(hip, orc):
 
 
 @pytest.mark.parametrize("f32", [False, True])
-@pytest.mark.parametrize("k,n", [(1024, 3072), (4096, 1024), (1000, 64)])
+@pytest.mark.parametrize("k,n", [
+    (1024, 3072), (2560, 100), (28672, 64),       # whole 256-value blocks, any count: the flat walk
+    (4096, 1024), (4096, 4096), (4096, 12288),    # Qwen3-8B shapes: one pass / streamed
+    (8192, 1000), (12288, 4096), (16384, 300),    # longer rows (x from LDS beyond two steps)
+    (1000, 64),                                   # K not a multiple of 256: one wave per row
+])
 def test_matvec_fp16(hip, orc, k, n, f32):
     rng = hip.synth.Rng(k + n)
     w = hip.synth.normal_f16(rng, n * k)
@@ -165,21 +170,27 @@ def test_matvec_fp16(hip, orc, k, n, f32):
 
 def test_kernel_timer_brackets_the_calls_kernels(hip):
     """KernelTimer spans the first kernel's start to the last kernel's end of
-    the calls made while armed, and disarms afterwards."""
+    the calls made while armed, and disarms afterwards.  Each span is the
+    least of five trials (a single kernel's time varies with the clocks)."""
     n, k = 12288, 4096
     w = hip.synth.quant_matrix("q4k", hip.synth.Rng(1), n, k)
     dw, dx, dy = up(hip, w), up(hip, hip.synth.normal_f16(hip.synth.Rng(2), k)), hip.DeviceArray(n * 2)
     hip.device.matvec("q4k", dw, dx, dy, k, n)
-    one, two = hip.device.KernelTimer(), hip.device.KernelTimer()
-    with one:
-        hip.device.matvec("q4k", dw, dx, dy, k, n)
-    with two:
-        hip.device.matvec("q4k", dw, dx, dy, k, n)
-        hip.device.matvec("q4k", dw, dx, dy, k, n)
-    hip.device.matvec("q4k", dw, dx, dy, k, n)   # not timed
-    hip.synchronize()
-    t1, t2 = one.ms(), two.ms()
-    assert 0 < t1 < 5 and t2 > 1.5 * t1, (t1, t2)
+
+    def span(calls):
+        best = float("inf")
+        for _ in range(5):
+            t = hip.device.KernelTimer()
+            with t:
+                for _ in range(calls):
+                    hip.device.matvec("q4k", dw, dx, dy, k, n)
+            hip.device.matvec("q4k", dw, dx, dy, k, n)   # not timed
+            hip.synchronize()
+            best = min(best, t.ms())
+        return best
+
+    t1, t3 = span(1), span(3)
+    assert 0 < t1 < 5 and t3 > 2.0 * t1, (t1, t3)
 
 
 def test_argmax_signed_zero_and_block_edges(hip, orc):
@@ -239,7 +250,8 @@ def test_qk_norm_rope_store_equals_separate_launches(hip, heads, kv, hd, pos, wi
     assert np.array_equal(vc1.download(np.uint16), vc2.download(np.uint16))
 
 
-@pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q4k", 3000, 8192), ("q6k", 2048, 4096)])
+@pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q4k", 3000, 8192), ("q6k", 2048, 4096),
+                                      ("fp16", 12288, 4096), ("fp16", 3000, 8192)])
 def test_gate_up_swiglu_equals_two_gemvs_and_swiglu(hip, kind, n, k):
     rng = hip.synth.Rng(n + k)
     wg, wu = hip.synth.quant_matrix(kind, rng, n, k), hip.synth.quant_matrix(kind, rng, n, k)

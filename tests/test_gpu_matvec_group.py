@@ -51,6 +51,12 @@ CASES = [
     (("q4k",), (4096,), 4096),
     (("q6k", "q4k"), (1024, 4096), 4096),
     (("q4k", "q6k"), (1, 1), 4096),
+    # fp16 weights (DequantizeToFp16): the plain launch is matvec_fp16
+    (("fp16", "fp16", "fp16"), (4096, 1024, 1024), 4096),
+    (("fp16", "fp16", "fp16"), (8192, 1024, 1024), 4096),
+    (("fp16", "fp16"), (513, 7), 8192),
+    (("fp16", "fp16", "fp16"), (300, 100, 3), 12288),
+    (("fp16",), (200,), 16384),
 ]
 
 
@@ -79,6 +85,18 @@ def test_group_declines_other_lengths_without_writing(hip, k):
     with pytest.raises(hip.CitlaliError, match="no grouped kernel"):
         hip.device.matvec_group(["q4k"], [w], x, [y], [n], k)
     assert (y.download(np.uint16, n) == 0x3c00).all()
+
+
+def test_group_declines_fp16_mixed_with_quantized(hip):
+    n, k = 64, 4096
+    rng = hip.synth.Rng(6)
+    wq = up(hip, hip.synth.quant_matrix("q4k", rng, n, k))
+    wf = up(hip, hip.synth.quant_matrix("fp16", rng, n, k))
+    x = up(hip, hip.synth.normal_f16(rng, k))
+    y = [up(hip, np.full(n, 0x3c00, np.uint16)) for _ in range(2)]
+    with pytest.raises(hip.CitlaliError, match="F16 and quantized"):
+        hip.device.matvec_group(["q4k", "fp16"], [wq, wf], x, y, [n, n], k)
+    assert all((t.download(np.uint16, n) == 0x3c00).all() for t in y)
 
 
 def test_group_rejects_bad_arguments(hip):

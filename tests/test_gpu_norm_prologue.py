@@ -36,6 +36,8 @@ def reference_norm(hip, x, d, w, k, eps=1e-6):
     (("q6k", "q4k"), (700, 9), 8192),
     (("q4k", "q4k", "q4k"), (300, 300, 300), 12288),
     (("q6k",), (64,), 16384),
+    (("fp16", "fp16", "fp16"), (4096, 1024, 1024), 4096),
+    (("fp16", "fp16"), (500, 20), 12288),
 ])
 def test_group_norm_equals_add_rms_norm_then_group(hip, kinds, rows, k, with_delta):
     rng, x, d, w = inputs(hip, k, sum(rows) + k)
@@ -56,7 +58,8 @@ def test_group_norm_equals_add_rms_norm_then_group(hip, kinds, rows, k, with_del
         assert (sum_out.download(np.uint16, k) == 0x7bff).all()   # untouched
 
 
-@pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q6k", 1000, 8192)])
+@pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q6k", 1000, 8192), ("fp16", 12288, 4096),
+                                      ("fp16", 900, 8192)])
 def test_gate_up_norm_equals_add_rms_norm_then_gate_up(hip, kind, n, k):
     rng, x, d, w = inputs(hip, k, n + k)
     wg, wu = (up(hip, hip.synth.quant_matrix(kind, rng, n, k)) for _ in range(2))
@@ -71,7 +74,7 @@ def test_gate_up_norm_equals_add_rms_norm_then_gate_up(hip, kind, n, k):
 
 @pytest.mark.parametrize("f32_out", [True, False])
 @pytest.mark.parametrize("kind,n,k", [("q6k", 30000, 4096), ("q4k", 5000, 4096), ("q6k", 777, 12288),
-                                      ("q4k", 100, 16384)])
+                                      ("q4k", 100, 16384), ("fp16", 30000, 4096), ("fp16", 333, 12288)])
 def test_matvec_norm_equals_add_rms_norm_then_matvec(hip, kind, n, k, f32_out):
     rng, x, d, w = inputs(hip, k, 3 * n + k)
     dw = up(hip, hip.synth.quant_matrix(kind, rng, n, k))
