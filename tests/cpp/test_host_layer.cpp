@@ -449,14 +449,46 @@ struct OracleModel {
     int32_t step(int32_t tok, int pos, float* logits) { return orc_forward_token(&m, cache_ptrs.data(), tok, pos, logits); }
 };
 
-model::WeightHandle handle_of(const HostMatrix& m, const std::string& name) {
+// The host loader's fp16 values of a quantised matrix (DequantizeToFp16).
+std::vector<uint16_t> dequant_f16(const HostMatrix& m) {
+    std::vector<uint16_t> out((size_t)m.rows * m.cols);
+    if (m.type == GgufTensorType::Q4_K) {
+        orc_dequant_q4k_f16(m.bytes.data(), out.size(), out.data());
+    } else {
+        orc_dequant_q6k_f16(m.bytes.data(), out.size(), out.data());
+    }
+    return out;
+}
+
+// The oracle's matrices replaced by their fp16 dequantisation (`keep` owns
+// the values), as QwenModel sees them under DequantizeToFp16.
+void oracle_over_f16(OracleModel& o, const SynthModel& s, std::vector<std::vector<uint16_t>>& keep) {
+    auto f16 = [&](const HostMatrix& m) {
+        keep.push_back(dequant_f16(m));
+        return OrcMatrix{ORC_F16, keep.back().data()};
+    };
+    keep.reserve(keep.size() + 2 + 7 * o.layers.size());
+    o.m.token_embd = f16(s.embd);
+    o.m.output = f16(s.output);
+    for (size_t l = 0; l < o.layers.size(); ++l) {
+        const auto& L = s.layers[l];
+        OrcLayer& d = o.layers[l];
+        d.q = f16(L.q); d.k = f16(L.k); d.v = f16(L.v); d.o = f16(L.o);
+        d.gate = f16(L.gate); d.up = f16(L.up); d.down = f16(L.down);
+    }
+    o.m.layers = o.layers.data();
+}
+
+// A matrix as QwenModel holds it: raw blocks (KeepQuantized) or, with fp16,
+// the host loader's fp16 values (DequantizeToFp16).
+model::WeightHandle handle_of(const HostMatrix& m, const std::string& name, bool fp16 = false) {
     model::WeightHandle w;
     w.name = name;
     w.gguf_type = m.type;
-    w.storage_kind = WeightStorageKind::QuantizedDevice;
+    w.storage_kind = fp16 ? WeightStorageKind::Fp16Device : WeightStorageKind::QuantizedDevice;
     w.dims = {(uint64_t)m.cols, (uint64_t)m.rows};
     w.element_count = (uint64_t)m.rows * m.cols;
-    w.buffer = upload(m.bytes);
+    w.buffer = fp16 ? upload(dequant_f16(m)) : upload(m.bytes);
     return w;
 }
 
@@ -471,20 +503,20 @@ model::WeightHandle handle_of_norm(const std::vector<uint16_t>& v, const std::st
     return w;
 }
 
-model::QwenWeights device_weights(const SynthModel& s) {
+model::QwenWeights device_weights(const SynthModel& s, bool fp16 = false) {
     model::QwenWeights w;
-    w.token_embedding = handle_of(s.embd, "token_embd.weight");
+    w.token_embedding = handle_of(s.embd, "token_embd.weight", fp16);
     w.output_norm = handle_of_norm(s.output_norm, "output_norm.weight");
-    w.output_weight = handle_of(s.output, "output.weight");
+    w.output_weight = handle_of(s.output, "output.weight", fp16);
     for (size_t l = 0; l < s.layers.size(); ++l) {
         const auto& L = s.layers[l];
         const std::string b = "blk." + std::to_string(l) + ".";
         model::QwenLayerWeights d;
         d.attn_norm = handle_of_norm(L.attn_norm, b + "attn_norm.weight");
-        d.attn_q = handle_of(L.q, b + "attn_q.weight");
-        d.attn_k = handle_of(L.k, b + "attn_k.weight");
-        d.attn_v = handle_of(L.v, b + "attn_v.weight");
-        d.attn_o = handle_of(L.o, b + "attn_output.weight");
+        d.attn_q = handle_of(L.q, b + "attn_q.weight", fp16);
+        d.attn_k = handle_of(L.k, b + "attn_k.weight", fp16);
+        d.attn_v = handle_of(L.v, b + "attn_v.weight", fp16);
+        d.attn_o = handle_of(L.o, b + "attn_output.weight", fp16);
         const auto vec = [&](const std::vector<uint16_t>& v, const std::string& name) {
             return v.empty() ? model::WeightHandle{} : handle_of_norm(v, b + name);
         };
@@ -498,9 +530,9 @@ model::QwenWeights device_weights(const SynthModel& s) {
         d.ffn_up_bias = vec(L.up_bias, "ffn_up.bias");
         d.ffn_down_bias = vec(L.down_bias, "ffn_down.bias");
         d.ffn_norm = handle_of_norm(L.ffn_norm, b + "ffn_norm.weight");
-        d.ffn_gate = handle_of(L.gate, b + "ffn_gate.weight");
-        d.ffn_up = handle_of(L.up, b + "ffn_up.weight");
-        d.ffn_down = handle_of(L.down, b + "ffn_down.weight");
+        d.ffn_gate = handle_of(L.gate, b + "ffn_gate.weight", fp16);
+        d.ffn_up = handle_of(L.up, b + "ffn_up.weight", fp16);
+        d.ffn_down = handle_of(L.down, b + "ffn_down.weight", fp16);
         w.layers.push_back(std::move(d));
     }
     return w;
@@ -583,15 +615,22 @@ void test_model_load_errors() {
 // lockstep, and the GPU must stay within the spread that this 1-ulp input
 // noise produces in the oracle.
 void greedy_run(uint64_t seed, int prompt, int steps, int* identical, int* ties, int hidden = 2048,
-                int heads = 16, bool biased = false) {
+                int heads = 16, bool biased = false, bool fp16 = false) {
     SynthModel s = biased ? make_model_biased(seed, hidden, heads, 8, 4096, 2, 8192)
                           : make_model(seed, hidden, heads, 8, 4096, 2, 8192);
     const int ctx = 128;
     model::QwenModel gpu;
-    gpu.load(s.cfg, device_weights(s), ctx);
+    gpu.load(s.cfg, device_weights(s, fp16), ctx);
     OracleModel orc(s, ctx, 2), ctl(s, ctx, 2);
+    std::vector<std::vector<uint16_t>> keep;
     std::vector<uint16_t> e16((size_t)8192 * hidden);
-    for (int t = 0; t < 8192; ++t) orc_embed_q6k(s.embd.bytes.data(), t, e16.data() + (size_t)t * hidden, hidden);
+    if (fp16) {   // DequantizeToFp16: the oracle over the same fp16 values
+        oracle_over_f16(orc, s, keep);
+        oracle_over_f16(ctl, s, keep);
+        e16 = keep.front();   // the embedding table
+    } else {
+        for (int t = 0; t < 8192; ++t) orc_embed_q6k(s.embd.bytes.data(), t, e16.data() + (size_t)t * hidden, hidden);
+    }
     Rng flip{seed + 100};
     for (auto& h : e16)
         if ((h & 0x7fff) && (flip.next() & 1)) h ^= 1;
@@ -648,10 +687,11 @@ void greedy_run(uint64_t seed, int prompt, int steps, int* identical, int* ties,
                                              " exceeds twice the logit error " + std::to_string(step_err));
         }
     }
-    std::printf("greedy decode seed %llu (hidden %d%s): %d prompt tokens, %d greedy steps: %d identical, %d numerical ties; "
+    std::printf("greedy decode seed %llu (hidden %d%s%s): %d prompt tokens, %d greedy steps: %d identical, %d numerical ties; "
                 "max |logit diff| / rms(logits) = %.2e (rms %.2f; by position%s); oracle under 1-ulp embedding "
                 "noise: %.2e; min oracle top-2 margin %.2e\n",
-                (unsigned long long)seed, hidden, biased ? ", Qwen2-style biases, no q/k norm" : "", prompt, steps, *identical, *ties, worst, rms_sum / (prompt + steps),
+                (unsigned long long)seed, hidden, biased ? ", Qwen2-style biases, no q/k norm" : "",
+                fp16 ? ", fp16 weights" : "", prompt, steps, *identical, *ties, worst, rms_sum / (prompt + steps),
                 profile.c_str(), ctl_worst, min_margin);
     check(worst <= ctl_worst, "GPU logits within the oracle's own 1-ulp sensitivity");
 }
@@ -670,18 +710,22 @@ void test_forward_greedy() {
     // the attention prologue without norm weights)
     greedy_run(12, 8, 64, &identical, &ties, 2048, 16, /*biased=*/true);
     all_ties += ties;
-    check(all_ties <= 5, "at most one numerical tie per 64-step run on average");
+    // DequantizeToFp16 weights at hidden 4096: the fp16 GEMVs in the grouped,
+    // gate/up and norm-prologue launches
+    greedy_run(13, 8, 64, &identical, &ties, 4096, 32, /*biased=*/false, /*fp16=*/true);
+    all_ties += ties;
+    check(all_ties <= 6, "at most one numerical tie per 64-step run on average");
 }
 
 // QwenModel::decode_greedy (captured steps replayed per token) against the
 // forward_token loop: the same tokens exactly, across attention plan lengths
 // 256, 512 and the max_context cap (600), replayed several times with eager
 // work and synchronisations in between, and split over two calls.
-void test_decode_greedy_graph(int hidden, int heads) {
+void test_decode_greedy_graph(int hidden, int heads, bool fp16 = false) {
     SynthModel s = make_model(11, hidden, heads, 8, 4096, 2, 8192);
     const int ctx = 600, first = 240, steps = ctx - first;
     model::QwenModel gpu;
-    gpu.load(s.cfg, device_weights(s), ctx);
+    gpu.load(s.cfg, device_weights(s, fp16), ctx);
     Rng r{77};
     for (int p = 0; p < first; ++p) gpu.forward_token((int32_t)(r.next() % 8192), (uint32_t)p, false);
     const int32_t start = (int32_t)(r.next() % 8192);
@@ -779,16 +823,6 @@ std::string temp_path(const std::string& name) {
     return std::string(d && *d ? d : "/tmp") + "/citlali_" + std::to_string((long long)getpid()) + "_" + name;
 }
 
-std::vector<uint16_t> dequant_f16(const HostMatrix& m) {
-    std::vector<uint16_t> out((size_t)m.rows * m.cols);
-    if (m.type == GgufTensorType::Q4_K) {
-        orc_dequant_q4k_f16(m.bytes.data(), out.size(), out.data());
-    } else {
-        orc_dequant_q6k_f16(m.bytes.data(), out.size(), out.data());
-    }
-    return out;
-}
-
 // QwenModel::load from a GGUF file of the synthetic model.  KeepQuantized:
 // the same device bytes as the model built from WeightHandles, so the same
 // logits bit for bit and the same tokens.  DequantizeToFp16: fp16 weights and
@@ -818,22 +852,9 @@ void test_load_from_gguf(bool biased) {
 
     // the oracle over fp16 weights, and a twin with 1-ulp embedding noise
     std::vector<std::vector<uint16_t>> keep;
-    auto f16 = [&](const HostMatrix& m) {
-        keep.push_back(dequant_f16(m));
-        return OrcMatrix{ORC_F16, keep.back().data()};
-    };
-    keep.reserve(2 * (2 + 7 * s.layers.size()));
     OracleModel orc(s, ctx, 2), ctl(s, ctx, 2);
-    for (OracleModel* o : {&orc, &ctl}) {
-        o->m.token_embd = f16(s.embd);
-        o->m.output = f16(s.output);
-        for (size_t l = 0; l < s.layers.size(); ++l) {
-            const auto& L = s.layers[l];
-            OrcLayer& d = o->layers[l];
-            d.q = f16(L.q); d.k = f16(L.k); d.v = f16(L.v); d.o = f16(L.o);
-            d.gate = f16(L.gate); d.up = f16(L.up); d.down = f16(L.down);
-        }
-    }
+    oracle_over_f16(orc, s, keep);
+    oracle_over_f16(ctl, s, keep);
     std::vector<uint16_t> noisy(static_cast<const uint16_t*>(ctl.m.token_embd.data),
                                 static_cast<const uint16_t*>(ctl.m.token_embd.data) + (size_t)vocab * 1024);
     Rng flip{5};
@@ -907,6 +928,7 @@ int main(int argc, char** argv) {
             test_forward_greedy();
             test_decode_greedy_graph(2048, 16);
             test_decode_greedy_graph(4096, 32);
+            test_decode_greedy_graph(4096, 32, /*fp16=*/true);
             test_load_from_gguf(false);
             test_load_from_gguf(true);
             compute::synchronize();
