@@ -664,9 +664,11 @@ void launch_rows_once(const RowSet& rs, const uint16_t* x, size_t lds, const Nor
 }
 
 // K = 4096 S.  Shapes measured on MI355X: at K = 4096 a launch of up to 4096
-// rows is fastest as one pass of one or two rows per wave (the refill loop's
-// loads past the last row cost more than they hide); longer matrices stream
-// with one row in flight, two once each wave walks at least four rows.
+// rows is fastest as one pass of one, two or four rows per wave (the refill
+// loop's loads past the last row cost more than they hide; attn_o, 4096 rows:
+// 4.02 us with four rows per wave, 4.31 with two, 4.43 with one); longer
+// matrices stream with one row in flight, two once each wave walks at least
+// four rows.
 template <class QT, bool kF32, int kSegs, bool kNorm = false>
 bool launch_stream_for(int nb, const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm,
                        hipStream_t stream) {
@@ -675,8 +677,10 @@ bool launch_stream_for(int nb, const RowSet& rs, const uint16_t* x, size_t lds, 
         case 16:
             if (rows <= 1024)
                 launch_rows_once<QT, kF32, 1, kSegs, kNorm>(rs, x, lds, nrm, stream);
-            else if (rows <= 4096)
+            else if (rows <= 3072)
                 launch_rows_once<QT, kF32, 2, kSegs, kNorm>(rs, x, lds, nrm, stream);
+            else if (rows <= 4096)
+                launch_rows_once<QT, kF32, 4, kSegs, kNorm>(rs, x, lds, nrm, stream);
             else if (rows >= 4 * kWavesPerBlock * stream_grid(rows))
                 launch_stream<QT, kF32, 1, 2, kSegs, kNorm>(rs, x, lds, nrm, stream);
             else
