@@ -12,7 +12,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <algorithm>
 #include <mutex>
+#include <thread>
+#include <vector>
 
 #define CITLALI_EXPORT extern "C" __attribute__((visibility("default")))
 
@@ -144,9 +147,79 @@ CITLALI_EXPORT int citlali_hip_free(void* ptr) {
     return CITLALI_OK;
 }
 
+namespace {
+// Large host -> device copies (weight uploads, WeightLoader) go through two
+// pinned staging buffers: host threads copy the next piece of the (pageable)
+// source into one buffer while the DMA engine moves the other, on the
+// library stream so the copy stays ordered with the launches.  Each device's
+// buffers (2 x kStageBytes of pinned host memory) are allocated on first use
+// and kept until the process ends; copies through them are serialised.
+constexpr size_t kStageBytes = (size_t)8 << 20;
+constexpr size_t kStageMin = (size_t)8 << 20;   // smaller copies: one pageable hipMemcpyAsync
+struct Staging {
+    void* buf[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    bool failed = false;   // pinned allocation refused: stay on the pageable path
+};
+Staging g_stage[kMaxDevices];
+std::mutex g_stage_mu;
+
+// memcpy split over up to 8 host threads (page-aligned pieces of >= 1 MB)
+void parallel_copy(void* dst, const void* src, size_t n) {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const size_t threads = std::min<size_t>(std::min<size_t>(8, hw ? hw : 1), n >> 20);
+    if (threads <= 1) {
+        std::memcpy(dst, src, n);
+        return;
+    }
+    const size_t per = (n / threads + 4095) & ~(size_t)4095;
+    std::vector<std::thread> pool;
+    for (size_t off = per; off < n; off += per) {
+        const size_t len = std::min(per, n - off);
+        pool.emplace_back([=] { std::memcpy(static_cast<char*>(dst) + off, static_cast<const char*>(src) + off, len); });
+    }
+    std::memcpy(dst, src, std::min(per, n));
+    for (auto& t : pool) t.join();
+}
+
+bool staging_ready(Staging& s) {
+    if (s.buf[0]) return true;
+    if (s.failed) return false;
+    for (int i = 0; i < 2; ++i) {
+        if (hipHostMalloc(&s.buf[i], kStageBytes, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&s.done[i], hipEventDisableTiming) != hipSuccess) {
+            s.failed = true;
+            (void)hipGetLastError();
+            return false;
+        }
+    }
+    return true;
+}
+}  // namespace
+
 CITLALI_EXPORT int citlali_hip_memcpy_h2d(void* dst, const void* src, size_t bytes) {
     if (bytes == 0) return CITLALI_OK;
     REQUIRE(dst && src, "copy_from_host received a null pointer");
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    if (bytes >= kStageMin && dev >= 0 && dev < kMaxDevices) {
+        std::lock_guard<std::mutex> lock(g_stage_mu);
+        Staging& s = g_stage[dev];
+        if (staging_ready(s)) {
+            bool used[2] = {false, false};
+            for (size_t off = 0, i = 0; off < bytes; off += kStageBytes, ++i) {
+                const int b = (int)(i & 1);
+                const size_t n = std::min(kStageBytes, bytes - off);
+                if (used[b]) HIP_TRY(hipEventSynchronize(s.done[b]));   // its previous DMA is done
+                parallel_copy(s.buf[b], static_cast<const char*>(src) + off, n);
+                HIP_TRY(hipMemcpyAsync(static_cast<char*>(dst) + off, s.buf[b], n, hipMemcpyHostToDevice, g_stream));
+                HIP_TRY(hipEventRecord(s.done[b], g_stream));
+                used[b] = true;
+            }
+            HIP_TRY(hipStreamSynchronize(g_stream));
+            return CITLALI_OK;
+        }
+    }
     HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_stream));
     HIP_TRY(hipStreamSynchronize(g_stream));
     return CITLALI_OK;

@@ -270,3 +270,17 @@ def test_gate_up_swiglu_declines_other_lengths(hip):
     d = hip.DeviceArray(1 << 20)
     with pytest.raises(hip.CitlaliError, match="no fused kernel"):
         hip.device.matvec_gate_up_swiglu("q4k", d, d, d, d, 2048, 64)
+
+
+@pytest.mark.parametrize("nbytes,offset", [(16 << 20, 0), ((100 << 20) + 12345, 4096), ((64 << 20) - 2, 6)])
+def test_large_host_to_device_copies_are_exact(hip, nbytes, offset):
+    """citlali_hip_memcpy_h2d from 16 MB up (the pinned double-buffered
+    staging path): every byte arrives, across piece boundaries, at an offset
+    into the destination, with the bytes around it untouched."""
+    rng = np.random.default_rng(nbytes)
+    src = rng.integers(0, 256, nbytes, dtype=np.uint8)
+    dev = up(hip, np.full(offset + nbytes + 4096, 0xA5, np.uint8))
+    dev.upload(src, offset)
+    got = dev.download(np.uint8, offset + nbytes + 4096)
+    assert np.array_equal(got[offset:offset + nbytes], src)
+    assert (got[:offset] == 0xA5).all() and (got[offset + nbytes:] == 0xA5).all()
