@@ -63,7 +63,11 @@ int citlali_hip_synchronize(void);
 
 int citlali_hip_malloc(void** ptr, size_t bytes);              /* tensor.cu:49-59 (bytes == 0 -> *ptr = NULL) */
 int citlali_hip_free(void* ptr);                               /* tensor.cu:67-73 */
-int citlali_hip_memcpy_h2d(void* dst, const void* host_src, size_t bytes); /* tensor.cu:76-78 */
+/* tensor.cu:76-78; returns once the bytes are on the device.  Copies of 8 MB
+ * and more go through two pinned 8 MB staging buffers per device (allocated
+ * on first use, kept until the process ends), host threads filling one while
+ * the DMA engine drains the other. */
+int citlali_hip_memcpy_h2d(void* dst, const void* host_src, size_t bytes);
 int citlali_hip_memcpy_d2h(void* host_dst, const void* src, size_t bytes); /* tensor.cu:88-90, waits */
 int citlali_hip_memcpy_d2d(void* dst, const void* src, size_t bytes);
 /* cuda_zero (kernels.h:8, kernels.cu:655-657); a fill kernel, so it is safe
