@@ -668,6 +668,15 @@ CITLALI_EXPORT int citlali_hip_graph_destroy(void* graph) {
 }
 
 namespace {
+// Row lengths the grouped / prologue GEMV kernels cover: one wave step or
+// less (1024, 2048, 3072: Qwen3-0.6B) and 1..4 whole steps of 4096; gate/up
+// with SwiGLU up to 8192.
+bool norm_length_ok(int in_f) {
+    return in_f == 1024 || in_f == 2048 || in_f == 3072 || (in_f % 4096 == 0 && in_f <= 16384);
+}
+bool gate_up_length_ok(int in_f) {
+    return in_f == 1024 || in_f == 2048 || in_f == 3072 || in_f == 4096 || in_f == 8192;
+}
 // GEMV weight types of the grouped / fused entry points: GGUF Q4_K (12),
 // Q6_K (14) and F16 (1, fp16 rows), as the kernels' kinds 4, 6, 1
 bool fused_type_ok(int t) { return t == 12 || t == 14 || t == 1; }
@@ -682,7 +691,7 @@ CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_
     int st = check_matvec("matvec_gate_up_swiglu", w_gate, x, act, in_f, out_f, walign, 2);
     if (st) return st;
     REQUIRE(w_up && aligned(w_up, walign), "matvec_gate_up_swiglu: bad up weight");
-    if (in_f != 4096 && in_f != 8192)
+    if (!gate_up_length_ok(in_f))
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_gate_up_swiglu: in_features %d has no fused kernel", in_f);
     HIP_TRY(launch_matvec_gate_up_swiglu(fused_kind(gguf_type), w_gate, w_up, x, act, in_f, out_f, nullptr,
                                          g_stream));
@@ -709,7 +718,7 @@ CITLALI_EXPORT int citlali_hip_matvec_group(int count, const int* gguf_types, co
     REQUIRE(rows <= INT_MAX, "matvec_group: %lld rows in total exceed INT_MAX", rows);
     if (f16 != 0 && f16 != count)
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: F16 and quantized weights have no grouped kernel");
-    if (in_f % 4096 != 0 || in_f > 16384)
+    if (!norm_length_ok(in_f))
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: in_features %d has no grouped kernel", in_f);
     HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, nullptr, g_stream));
     return CITLALI_OK;
@@ -728,7 +737,6 @@ int check_norm(const char* who, const uint16_t* x, const citlali_hip_norm* n, in
     (void)in_f;
     return CITLALI_OK;
 }
-bool norm_length_ok(int in_f) { return in_f % 4096 == 0 && in_f <= 16384; }
 }  // namespace
 
 CITLALI_EXPORT int citlali_hip_matvec_group_norm(int count, const int* gguf_types, const uint8_t* const* weights,
@@ -773,7 +781,7 @@ CITLALI_EXPORT int citlali_hip_matvec_gate_up_swiglu_norm(int gguf_type, const u
     st = check_matvec("matvec_gate_up_swiglu_norm", w_gate, x, act, in_f, out_f, walign, 2);
     if (st) return st;
     REQUIRE(w_up && aligned(w_up, walign), "matvec_gate_up_swiglu_norm: bad up weight");
-    if (in_f != 4096 && in_f != 8192)
+    if (!gate_up_length_ok(in_f))
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_gate_up_swiglu_norm: in_features %d has no fused kernel", in_f);
     HIP_TRY(launch_matvec_gate_up_swiglu(fused_kind(gguf_type), w_gate, w_up, x, act, in_f, out_f, &nrm,
                                          g_stream));

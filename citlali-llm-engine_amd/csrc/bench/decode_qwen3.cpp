@@ -21,10 +21,12 @@
 // (with --gguf) loads it with DequantizeToFp16 instead, the reference's
 // default policy: every matrix becomes fp16 in device memory and the fp16
 // GEMVs run.
+// `--model 0.6b` builds Qwen3-0.6B shapes instead (28 layers, hidden 1024,
+// FFN 3072, 16/8 heads, head_dim 128, the same vocab and quant types).
 // Prints one JSON line.
 //
-// usage: decode_qwen3 [--layers 36] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1] [--no-graph]
-//                     [--gguf PATH [--fp16]]
+// usage: decode_qwen3 [--model 8b|0.6b] [--layers N] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1]
+//                     [--no-graph] [--gguf PATH [--fp16]]
 #include "citlali/common.h"
 #include "citlali/compute/hip/kernels.h"
 #include "citlali/io/gguf_reader.h"
@@ -121,7 +123,13 @@ int arg(int argc, char** argv, const char* key, int def) {
 }  // namespace
 
 int main(int argc, char** argv) {
-    const int layers = arg(argc, argv, "--layers", 36);
+    const char* model_arg = str_arg(argc, argv, "--model");
+    const bool small = model_arg != nullptr && std::strcmp(model_arg, "0.6b") == 0;
+    if (model_arg != nullptr && !small && std::strcmp(model_arg, "8b") != 0) {
+        std::fprintf(stderr, "decode_qwen3: --model is 8b or 0.6b\n");
+        return 2;
+    }
+    const int layers = arg(argc, argv, "--layers", small ? 28 : 36);
     const int prompt = arg(argc, argv, "--prompt", 512);
     const int steps = arg(argc, argv, "--steps", 256);
     const int distinct = arg(argc, argv, "--distinct", 4);
@@ -138,15 +146,16 @@ int main(int argc, char** argv) {
         cfg.architecture = "qwen3";
         cfg.vocab_size = 151936;
         cfg.context_length = 40960;
-        cfg.embedding_length = 4096;
+        const int H = small ? 1024 : 4096, F = small ? 3072 : 12288, HEADS = small ? 16 : 32, KVH = 8;
+        const int NQ = HEADS * 128, NKV = KVH * 128, V = 151936;
+        cfg.embedding_length = (uint32_t)H;
         cfg.block_count = layers;
-        cfg.feed_forward_length = 12288;
-        cfg.head_count = 32;
-        cfg.head_count_kv = 8;
+        cfg.feed_forward_length = (uint32_t)F;
+        cfg.head_count = (uint32_t)HEADS;
+        cfg.head_count_kv = (uint32_t)KVH;
         cfg.head_dim = 128;
         cfg.rms_norm_eps = 1e-6f;
         cfg.rope_theta = 1e6f;
-        const int H = 4096, F = 12288, NQ = 32 * 128, NKV = 8 * 128, V = 151936;
 
         const auto t0 = std::chrono::steady_clock::now();
         struct LayerBytes {
@@ -163,7 +172,7 @@ int main(int argc, char** argv) {
             sets[i].up = quant_bytes(s + 6, GgufTensorType::Q4_K, F, H, 1.0);
             sets[i].down = quant_bytes(s + 7, GgufTensorType::Q6_K, H, F, 0.5);
         }
-        const std::vector<uint8_t> embd = quant_bytes(seed * 7 + 11, GgufTensorType::Q6_K, V, H, std::sqrt(4096.0));
+        const std::vector<uint8_t> embd = quant_bytes(seed * 7 + 11, GgufTensorType::Q6_K, V, H, std::sqrt((double)H));
         const std::vector<uint8_t> outw = quant_bytes(seed * 7 + 13, GgufTensorType::Q6_K, V, H, 3.0);
         const int ctx = prompt + steps;
         model::QwenModel m;
@@ -178,8 +187,8 @@ int main(int argc, char** argv) {
             o.u32("qwen3.embedding_length", H);
             o.u32("qwen3.block_count", (uint32_t)layers);
             o.u32("qwen3.feed_forward_length", F);
-            o.u32("qwen3.attention.head_count", 32);
-            o.u32("qwen3.attention.head_count_kv", 8);
+            o.u32("qwen3.attention.head_count", (uint32_t)HEADS);
+            o.u32("qwen3.attention.head_count_kv", (uint32_t)KVH);
             o.u32("qwen3.attention.key_length", 128);
             o.u32("qwen3.attention.value_length", 128);
             o.f32("qwen3.attention.layer_norm_rms_epsilon", cfg.rms_norm_eps);
@@ -307,13 +316,16 @@ int main(int argc, char** argv) {
         // bytes one decode step must read: every weight once, the KV cache
         // up to the position, the embedding row and the logits
         // (fp16 weights: every matrix as 2-byte values)
+        // (K-quants: 144 / 210 bytes per 256 values; fp16 weights 2 bytes each)
+        const auto q4 = [](double rows, double cols) { return rows * cols / 256 * 144; };
+        const auto q6 = [](double rows, double cols) { return rows * cols / 256 * 210; };
         const double layer_bytes = fp16_weights ? 2.0 * ((double)NQ * H * 2 + (double)NKV * H * 2 + 3.0 * F * H)
-                                                : 9437184.0 * 2 + 2359296 + 3440640 + 28311552.0 * 2 + 41287680;
+                                                : q4(NQ, H) * 2 + q4(NKV, H) + q6(NKV, H) + q4(F, H) * 2 + q6(H, F);
         const double mean_len = prompt + (steps + 1) / 2.0;
-        const double out_bytes = fp16_weights ? 2.0 * V * H : 510504960.0;
-        const double step_bytes = layer_bytes * layers + out_bytes + 3360 + V * 4.0 +
+        const double out_bytes = fp16_weights ? 2.0 * V * H : q6(V, H);
+        const double step_bytes = layer_bytes * layers + out_bytes + q6(1, H) + V * 4.0 +
                                   (double)layers * 2 * 2 * NKV * mean_len;
-        std::printf("{\"workload\": \"BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode\", \"layers\": %d, "
+        std::printf("{\"workload\": \"%s\", \"layers\": %d, "
                     "\"distinct_layer_weight_sets\": %d, \"prompt\": %d, \"steps\": %d, \"decode_tok_per_s\": %.2f, "
                     "\"decode_ms_per_token\": %.4f, \"decode_mode\": \"%s\", "
                     "\"decode_GBps\": %.1f, \"decode_tok_per_s_forward_token\": %.2f, "
@@ -322,6 +334,8 @@ int main(int argc, char** argv) {
                     "\"prompt_ms_per_token_wall\": %.4f, \"setup_s\": %.1f, \"token_checksum\": %llu, "
                     "\"weights_from\": \"%s\", \"gguf_file_bytes\": %.0f, \"gguf_write_s\": %.2f, "
                     "\"gguf_load_s\": %.3f, \"gguf_load_GBps\": %.2f}\n",
+                    small ? "Qwen3-0.6B shapes, synthetic Q4_K_M greedy decode"
+                          : "BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode",
                     layers, distinct, prompt, steps, steps / (decode_ms * 1e-3), decode_ms / steps,
                     graph_pass ? "QwenModel::decode_greedy (graph replay), wall clock"
                                : "forward_token loop, wall clock (--no-graph)",

@@ -141,7 +141,8 @@ hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const
                                uint16_t* const* y, const int* n, int K, const NormIn* norm, hipStream_t s);
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
                                         uint16_t* act, int K, int N, const NormIn* norm, hipStream_t s);
-// kind 4 / 6 / 1 GEMV with the input prologue; K a multiple of 4096 up to 16384
+// kind 4 / 6 / 1 GEMV with the input prologue; K 1024, 2048, 3072 or a
+// multiple of 4096 up to 16384
 hipError_t launch_matvec_norm(int kind, const uint8_t* w, const uint16_t* x, const NormIn& norm, void* y,
                               bool f32_out, int K, int N, hipStream_t s);
 hipError_t launch_fill_zero(void* p, size_t bytes, hipStream_t s);

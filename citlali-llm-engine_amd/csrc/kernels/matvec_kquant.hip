@@ -82,25 +82,39 @@ __device__ __forceinline__ void stage_x8(const u32x4 raw, int v8, uint32_t* xp, 
 
 // x staging split in two so its global loads can be issued before the weight
 // loads: vmcnt retires loads in order, so x issued last would wait for every
-// weight load.  kIter = K / (8 * kBlock) runs of eight values per thread.
+// weight load.  kRuns = K / 8 runs of eight values; thread t stages runs
+// t, t + kBlock, ... (kIter per thread; when kRuns is not a multiple of
+// kBlock the last pass has whole waves without a run, which hold zeros).
 // kNorm: the staged input is the residual add + RMSNorm of x (NormIn, in the
 // run order of device_common.hpp; d, w and xs_out 16-byte aligned), its
 // loads issued with x's; `red` is 4 floats of LDS.
-template <int kLayout, int kIter, bool kNorm = false>
+template <int kLayout, int kRuns, bool kNorm = false>
 struct XStage {
+    static constexpr int kIter = (kRuns + kBlock - 1) / kBlock;
+    static_assert(kRuns % kWave == 0, "whole waves of runs");
     u32x4 raw[kIter];
     u32x4 dr[kNorm ? kIter : 1], wr[kNorm ? kIter : 1];
+    __device__ static __forceinline__ bool has_run(int i) {
+        return kRuns % kBlock == 0 || i * kBlock + (int)threadIdx.x < kRuns;
+    }
+    // run index of pass i (a thread without a run re-reads its first one)
+    __device__ static __forceinline__ size_t run_of(int i) {
+        return has_run(i) ? (size_t)i * kBlock + threadIdx.x : (size_t)threadIdx.x;
+    }
+    __device__ static __forceinline__ u32x4 keep(u32x4 v, int i) {
+        if (has_run(i)) return v;
+        return u32x4{0u, 0u, 0u, 0u};   // zeros: add nothing to the sum of squares
+    }
     __device__ __forceinline__ void load(const uint16_t* __restrict__ x, const NormIn& n) {
 #pragma unroll
-        for (int i = 0; i < kIter; ++i)
-            raw[i] = *reinterpret_cast<const u32x4*>(x + ((size_t)i * kBlock + threadIdx.x) * 8);
+        for (int i = 0; i < kIter; ++i) raw[i] = *reinterpret_cast<const u32x4*>(x + run_of(i) * 8);
         if constexpr (kNorm) {
             // branch-free: without d the loads re-read x (unused)
             const uint16_t* dp = n.d ? n.d : x;
 #pragma unroll
             for (int i = 0; i < kIter; ++i) {
-                dr[i] = *reinterpret_cast<const u32x4*>(dp + ((size_t)i * kBlock + threadIdx.x) * 8);
-                wr[i] = *reinterpret_cast<const u32x4*>(n.w + ((size_t)i * kBlock + threadIdx.x) * 8);
+                dr[i] = *reinterpret_cast<const u32x4*>(dp + run_of(i) * 8);
+                wr[i] = *reinterpret_cast<const u32x4*>(n.w + run_of(i) * 8);
             }
         }
     }
@@ -111,21 +125,23 @@ struct XStage {
             float s = 0.f;
 #pragma unroll
             for (int i = 0; i < kIter; ++i) {
-                raw[i] = add_run(raw[i], dr[i], has_d);
+                raw[i] = keep(add_run(raw[i], dr[i], has_d), i);
                 s = sq_run(raw[i], s);
             }
             if (n.xs_out && blockIdx.x == 0) {
 #pragma unroll
                 for (int i = 0; i < kIter; ++i)
-                    *reinterpret_cast<u32x4*>(n.xs_out + ((size_t)i * kBlock + threadIdx.x) * 8) = raw[i];
+                    if (has_run(i))
+                        *reinterpret_cast<u32x4*>(n.xs_out + ((size_t)i * kBlock + threadIdx.x) * 8) = raw[i];
             }
             s = norm_block_sum(s, red);
-            const float inv = rsqrtf(s / (float)(kIter * kBlock * 8) + n.eps);
+            const float inv = rsqrtf(s / (float)(kRuns * 8) + n.eps);
 #pragma unroll
             for (int i = 0; i < kIter; ++i) raw[i] = norm_run(raw[i], wr[i], inv);
         }
 #pragma unroll
-        for (int i = 0; i < kIter; ++i) stage_x8<kLayout>(raw[i], i * kBlock + threadIdx.x, xp, sx);
+        for (int i = 0; i < kIter; ++i)
+            if (has_run(i)) stage_x8<kLayout>(raw[i], i * kBlock + threadIdx.x, xp, sx);   // wave-uniform
         lds_barrier();
     }
 };
@@ -404,18 +420,22 @@ struct RowSet {
 // in LDS behind them.  Loads are branch-free (rows past the end re-read the
 // last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave
 // computes its M rows (all loaded up front) and stops; the grid then has
-// M * W >= rows.
-template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false>
+// M * W >= rows.  NB (4, 8 or 12; S = 1): rows shorter than one wave step,
+// nb = NB super-blocks; the lanes of blocks NB.. load block NB - 1 (in
+// bounds) and add nothing.
+template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false, int NB = 0>
 __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __restrict__ x, int K, uint8_t* smem,
                                             int gw, int W, const NormIn& nrm) {
-    constexpr int nb = S * QT::kSbPerStep;   // K = 256 nb
+    static_assert(NB == 0 || (S == 1 && NB < QT::kSbPerStep && NB % 4 == 0), "short rows: one partial step");
+    constexpr int nb = NB ? NB : S * QT::kSbPerStep;   // K = 256 nb
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
     const int N = rs.end[kSegs - 1];
 
     const int lane = threadIdx.x & (kWave - 1);
     const int l4 = lane % QT::kLanesPerSb;
-    const int sub = lane / QT::kLanesPerSb;
+    const int sub = NB ? min(lane / QT::kLanesPerSb, nb - 1) : lane / QT::kLanesPerSb;
+    const bool live = NB == 0 || lane / QT::kLanesPerSb < nb;   // a lane of a real block
     constexpr int D = S * M;
 
     // matrix of row r and r's first row index in it
@@ -429,7 +449,7 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
         return QT::load(w + f * QT::kBytes, l4);
     };
 
-    XStage<QT::kSumLayout, nb / 8, kNorm> xs;   // nb / 8 runs of eight values per thread
+    XStage<QT::kSumLayout, nb * 32, kNorm> xs;   // K / 8 = 32 nb runs of eight values
     xs.load(x, nrm);
     __builtin_amdgcn_sched_barrier(0);   // issue order: x, first fragments, staging
     typename QT::Frag fr[D];
@@ -455,8 +475,9 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
             float acc = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
-                const float c = kHoist ? QT::dot(fr[m * S + t], l4, xr[kHoist ? t : 0])
-                                       : QT::dot(fr[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
+                float c = kHoist ? QT::dot(fr[m * S + t], l4, xr[kHoist ? t : 0])
+                                 : QT::dot(fr[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
+                if constexpr (NB != 0) c = live ? c : 0.f;
                 acc += c;
                 // Refill after the dot has read the slot (issue_after), in
                 // slot order (vmcnt retires loads in issue order: a reordered
@@ -476,30 +497,31 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
     }
 }
 
-template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false>
+template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false, int NB = 0>
 __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_stream_kernel(RowSet rs, const uint16_t* __restrict__ x,
                                                                              int K, NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
-    stream_rows<QT, kF32, S, M, kSegs, kRefill, kNorm>(rs, x, K, smem,
-                                                       blockIdx.x * kWavesPerBlock + threadIdx.x / kWave,
-                                                       gridDim.x * kWavesPerBlock, nrm);
+    stream_rows<QT, kF32, S, M, kSegs, kRefill, kNorm, NB>(rs, x, K, smem,
+                                                           blockIdx.x * kWavesPerBlock + threadIdx.x / kWave,
+                                                           gridDim.x * kWavesPerBlock, nrm);
 }
 
 // Two row sets of different types in one launch: blocks [0, blocks_a) walk
 // set `a` (type QA), the rest walk set `b` (type QB).  Each row is computed
 // exactly as the single-matrix launch computes it.
-template <class QA, class QB, int S, int M, bool kRefill = true, bool kNorm = false>
+template <class QA, class QB, int S, int M, bool kRefill = true, bool kNorm = false, int NB = 0>
 __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_group_kernel(RowSet a, RowSet b, int blocks_a,
                                                                             const uint16_t* __restrict__ x, int K,
                                                                             NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int wave = threadIdx.x / kWave;
     if ((int)blockIdx.x < blocks_a)
-        stream_rows<QA, false, S, M, 3, kRefill, kNorm>(a, x, K, smem, blockIdx.x * kWavesPerBlock + wave,
-                                                        blocks_a * kWavesPerBlock, nrm);
+        stream_rows<QA, false, S, M, 3, kRefill, kNorm, NB>(a, x, K, smem, blockIdx.x * kWavesPerBlock + wave,
+                                                            blocks_a * kWavesPerBlock, nrm);
     else
-        stream_rows<QB, false, S, M, 3, kRefill, kNorm>(b, x, K, smem, (blockIdx.x - blocks_a) * kWavesPerBlock + wave,
-                                                        (gridDim.x - blocks_a) * kWavesPerBlock, nrm);
+        stream_rows<QB, false, S, M, 3, kRefill, kNorm, NB>(b, x, K, smem,
+                                                            (blockIdx.x - blocks_a) * kWavesPerBlock + wave,
+                                                            (gridDim.x - blocks_a) * kWavesPerBlock, nrm);
 }
 
 // ffn_gate and ffn_up GEMVs plus SwiGLU in one launch (the reference's two
@@ -508,7 +530,7 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_group_kernel(Row
 // does (same lane mapping and summation order), rounds both to fp16 where
 // the separate GEMVs store, and writes act[r] = fp16(silu(g) * u) with the
 // swiglu_kernel expression -- the separate launches' results bit for bit.
-template <class QT, int S, int M, bool kNorm = false>
+template <class QT, int S, int M, bool kNorm = false, int NB = 0>
 __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(const uint8_t* __restrict__ wg,
                                                                 const uint8_t* __restrict__ wu,
                                                                 const uint16_t* __restrict__ x,
@@ -517,10 +539,12 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
 
+    static_assert(NB == 0 || (S == 1 && NB < QT::kSbPerStep && NB % 4 == 0), "short rows: one partial step");
     const int lane = threadIdx.x & (kWave - 1);
     const int l4 = lane % QT::kLanesPerSb;
-    const int sub = lane / QT::kLanesPerSb;
-    constexpr int nb = S * QT::kSbPerStep;
+    constexpr int nb = NB ? NB : S * QT::kSbPerStep;
+    const int sub = NB ? min(lane / QT::kLanesPerSb, nb - 1) : lane / QT::kLanesPerSb;
+    const bool live = NB == 0 || lane / QT::kLanesPerSb < nb;   // a lane of a real block
     constexpr int D = S * M;
     const int W = gridDim.x * kWavesPerBlock;
     const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
@@ -530,7 +554,7 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
         return QT::load(w + f * QT::kBytes, l4);
     };
 
-    XStage<QT::kSumLayout, nb / 8, kNorm> xs;   // K = 256 nb
+    XStage<QT::kSumLayout, nb * 32, kNorm> xs;   // K = 256 nb
     xs.load(x, nrm);
     __builtin_amdgcn_sched_barrier(0);
     typename QT::Frag fg[D], fu[D];
@@ -555,8 +579,12 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
             float ag = 0.f, au = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
-                const float cg = QT::dot(fg[m * S + t], l4, xr[t]);
-                const float cu = QT::dot(fu[m * S + t], l4, xr[t]);
+                float cg = QT::dot(fg[m * S + t], l4, xr[t]);
+                float cu = QT::dot(fu[m * S + t], l4, xr[t]);
+                if constexpr (NB != 0) {
+                    cg = live ? cg : 0.f;
+                    cu = live ? cu : 0.f;
+                }
                 ag += cg;
                 au += cu;
                 const int nr = issue_after(r + M * W, cg, cu);   // refill after the dots, in slot order
@@ -647,20 +675,37 @@ int stream_grid(int rows) {
     return grid > need ? need : grid;
 }
 
-template <class QT, bool kF32, int S, int M, int kSegs, bool kNorm>
+// K = 256 nb, nb = NB (short rows) or 16 S
+template <class QT, bool kF32, int S, int M, int kSegs, bool kNorm, int NB = 0>
 void launch_stream(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
-    launch_kernel((matvec_stream_kernel<QT, kF32, S, M, kSegs, true, kNorm>), dim3(stream_grid(rs.end[kSegs - 1])),
-                  dim3(kBlock), lds, stream, rs, x, S * 4096, nrm);
+    constexpr int K = (NB ? NB : S * QT::kSbPerStep) * kQK;
+    launch_kernel((matvec_stream_kernel<QT, kF32, S, M, kSegs, true, kNorm, NB>),
+                  dim3(stream_grid(rs.end[kSegs - 1])), dim3(kBlock), lds, stream, rs, x, K, nrm);
 }
 
-// K = 4096, few rows: every wave loads its M rows up front and computes
-// them, no refills (M * waves >= rows).
-template <class QT, bool kF32, int M, int kSegs, bool kNorm>
+// Rows of one wave step (K <= 4096), few rows: every wave loads its M rows
+// up front and computes them, no refills (M * waves >= rows).
+template <class QT, bool kF32, int M, int kSegs, bool kNorm, int NB = 0>
 void launch_rows_once(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
+    constexpr int K = (NB ? NB : QT::kSbPerStep) * kQK;
     const int rows = rs.end[kSegs - 1];
     const int grid = (rows + M * kWavesPerBlock - 1) / (M * kWavesPerBlock);
-    launch_kernel((matvec_stream_kernel<QT, kF32, 1, M, kSegs, false, kNorm>), dim3(grid), dim3(kBlock), lds, stream,
-                  rs, x, 4096, nrm);
+    launch_kernel((matvec_stream_kernel<QT, kF32, 1, M, kSegs, false, kNorm, NB>), dim3(grid), dim3(kBlock), lds,
+                  stream, rs, x, K, nrm);
+}
+
+// Rows shorter than one wave step (K = 1024, 2048, 3072: Qwen3-0.6B): one
+// pass of one row per wave up to 1024 rows, of two up to 4096, streamed
+// with one row in flight beyond.
+template <class QT, bool kF32, int kSegs, bool kNorm, int NB>
+void launch_short(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
+    const int rows = rs.end[kSegs - 1];
+    if (rows <= 1024)
+        launch_rows_once<QT, kF32, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
+    else if (rows <= 4096)
+        launch_rows_once<QT, kF32, 2, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
+    else
+        launch_stream<QT, kF32, 1, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
 }
 
 // K = 4096 S.  Shapes measured on MI355X: at K = 4096 a launch of up to 4096
@@ -689,6 +734,9 @@ bool launch_stream_for(int nb, const RowSet& rs, const uint16_t* x, size_t lds, 
         case 32: launch_stream<QT, kF32, 2, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
         case 48: launch_stream<QT, kF32, 3, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
         case 64: launch_stream<QT, kF32, 4, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
+        case 4: launch_short<QT, kF32, kSegs, kNorm, 4>(rs, x, lds, nrm, stream); return true;
+        case 8: launch_short<QT, kF32, kSegs, kNorm, 8>(rs, x, lds, nrm, stream); return true;
+        case 12: launch_short<QT, kF32, kSegs, kNorm, 12>(rs, x, lds, nrm, stream); return true;
         default: return false;
     }
 }
@@ -728,7 +776,7 @@ hipError_t launch_matvec_prologue(const uint8_t* w, const uint16_t* x, const Nor
     return hipGetLastError();
 }
 
-template <int S, int M, bool kNorm>
+template <int S, int M, bool kNorm, int NB = 0>
 void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int K, const NormIn& nrm,
                         hipStream_t stream) {
     const int na = a.end[2], nbr = b.end[2];
@@ -739,8 +787,8 @@ void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int
         constexpr int kM = 2;
         const int ga = (na + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
         const int gb = (nbr + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
-        launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false, kNorm>), dim3(ga + gb), dim3(kBlock), lds, stream,
-                      a, b, ga, x, K, nrm);
+        launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false, kNorm, NB>), dim3(ga + gb), dim3(kBlock), lds,
+                      stream, a, b, ga, x, K, nrm);
         return;
     }
     // blocks split in proportion to the bytes each set streams
@@ -749,8 +797,8 @@ void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int
     int ga = (int)(grid * ba / (ba + bb) + 0.5);
     ga = std::max(1, std::min(ga, std::min(grid - 1, stream_grid(na))));
     const int gb = std::max(1, std::min(grid - ga, stream_grid(nbr)));
-    launch_kernel((matvec_group_kernel<Q4K, Q6K, S, M, true, kNorm>), dim3(ga + gb), dim3(kBlock), lds, stream, a, b,
-                  ga, x, K, nrm);
+    launch_kernel((matvec_group_kernel<Q4K, Q6K, S, M, true, kNorm, NB>), dim3(ga + gb), dim3(kBlock), lds, stream,
+                  a, b, ga, x, K, nrm);
 }
 
 template <bool kNorm>
@@ -764,6 +812,9 @@ bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], bool f16, const
         case 32: launch_group_mixed<2, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
         case 48: launch_group_mixed<3, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
         case 64: launch_group_mixed<4, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
+        case 4: launch_group_mixed<1, 1, kNorm, 4>(set[0], set[1], x, K, nrm, s); return true;
+        case 8: launch_group_mixed<1, 1, kNorm, 8>(set[0], set[1], x, K, nrm, s); return true;
+        case 12: launch_group_mixed<1, 1, kNorm, 12>(set[0], set[1], x, K, nrm, s); return true;
         default: return false;
     }
 }
@@ -783,6 +834,18 @@ hipError_t launch_gate_up_t(const uint8_t* wg, const uint8_t* wu, const uint16_t
         case 32:
             launch_kernel((matvec_gate_up_kernel<QT, 2, 1, kNorm>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x,
                           act, K, N, nrm);
+            break;
+        case 4:   // rows shorter than one wave step (Qwen3-0.6B: hidden 1024)
+            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 4>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
+                          x, act, K, N, nrm);
+            break;
+        case 8:
+            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 8>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
+                          x, act, K, N, nrm);
+            break;
+        case 12:
+            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 12>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
+                          x, act, K, N, nrm);
             break;
         default: return hipErrorInvalidValue;
     }
@@ -835,8 +898,8 @@ hipError_t launch_matvec_norm(int kind, const uint8_t* w, const uint16_t* x, con
 
 // count matrices (1..3) reading x: kinds[i] 4 = Q4_K, 6 = Q6_K, 1 = fp16
 // (all or none), n[i] rows, fp16 outputs y[i].  hipErrorInvalidValue,
-// nothing launched, for a length other than 4096, 8192, 12288 or 16384 or
-// fp16 mixed with quantized matrices.
+// nothing launched, for a length other than 1024, 2048, 3072, 4096, 8192,
+// 12288 or 16384 or fp16 mixed with quantized matrices.
 hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const* w, const uint16_t* x,
                                uint16_t* const* y, const int* n, int K, const NormIn* norm, hipStream_t s) {
     RowSet set[2];
@@ -863,8 +926,8 @@ hipError_t launch_matvec_group(int count, const int* kinds, const uint8_t* const
     return ok ? hipGetLastError() : hipErrorInvalidValue;
 }
 
-// kind 4: Q4_K, 6: Q6_K, 1: fp16; in_features 4096 or 8192 (16 or 32
-// blocks of 256)
+// kind 4: Q4_K, 6: Q6_K, 1: fp16; in_features 1024, 2048, 3072, 4096 or
+// 8192 (4, 8, 12, 16 or 32 blocks of 256)
 hipError_t launch_matvec_gate_up_swiglu(int kind, const uint8_t* wg, const uint8_t* wu, const uint16_t* x,
                                         uint16_t* act, int K, int N, const NormIn* norm, hipStream_t s) {
     return norm ? launch_gate_up<true>(kind, wg, wu, x, act, K, N, *norm, s)

@@ -91,7 +91,7 @@ def test_matvec_group_validation():
     st, msg = g(3, ints(14, 14, 14), ptrs(*[0x10000] * 3), ptrs(*[0x10000] * 3), ints(2 ** 30, 2 ** 30, 2 ** 30),
                 4096)
     assert st == 1 and "INT_MAX" in msg
-    st, msg = g(1, ints(14), ptrs(0x10000), ptrs(0x10000), ints(4), 2048)
+    st, msg = g(1, ints(14), ptrs(0x10000), ptrs(0x10000), ints(4), 1536)
     assert st == 2 and "no grouped kernel" in msg
     # fp16 weights (GGUF type 1): 16-byte aligned, never mixed with quantized ones
     st, msg = g(2, ints(1, 14), ptrs(0x10000, 0x10000), ptrs(0x10000, 0x10000), ints(4, 4), 4096)
@@ -122,7 +122,7 @@ def test_norm_prologue_validation():
     assert st == 1 and "sum_out must not be the input" in msg
     st, msg = _status("citlali_hip_matvec_norm", 10, fake, fake, ctypes.byref(ok), fake, 0, 4096, 8)
     assert st == 1 and "not Q4_K, Q6_K or F16" in msg
-    st, msg = _status("citlali_hip_matvec_norm", 14, fake, fake, ctypes.byref(ok), fake, 1, 2048, 8)
+    st, msg = _status("citlali_hip_matvec_norm", 14, fake, fake, ctypes.byref(ok), fake, 1, 1536, 8)
     assert st == 2 and "no prologue kernel" in msg
     st, msg = _status("citlali_hip_matvec_group_norm", 1, ints(12), ptrs(0x10000), fake, ctypes.byref(ok),
                       ptrs(0x50000), ints(8), 20480)

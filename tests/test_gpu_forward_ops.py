@@ -251,7 +251,8 @@ def test_qk_norm_rope_store_equals_separate_launches(hip, heads, kv, hd, pos, wi
 
 
 @pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q4k", 3000, 8192), ("q6k", 2048, 4096),
-                                      ("fp16", 12288, 4096), ("fp16", 3000, 8192)])
+                                      ("fp16", 12288, 4096), ("fp16", 3000, 8192), ("q4k", 3072, 1024),
+                                      ("q6k", 700, 3072), ("fp16", 5000, 2048)])
 def test_gate_up_swiglu_equals_two_gemvs_and_swiglu(hip, kind, n, k):
     rng = hip.synth.Rng(n + k)
     wg, wu = hip.synth.quant_matrix(kind, rng, n, k), hip.synth.quant_matrix(kind, rng, n, k)
@@ -269,7 +270,7 @@ def test_gate_up_swiglu_equals_two_gemvs_and_swiglu(hip, kind, n, k):
 def test_gate_up_swiglu_declines_other_lengths(hip):
     d = hip.DeviceArray(1 << 20)
     with pytest.raises(hip.CitlaliError, match="no fused kernel"):
-        hip.device.matvec_gate_up_swiglu("q4k", d, d, d, d, 2048, 64)
+        hip.device.matvec_gate_up_swiglu("q4k", d, d, d, d, 1536, 64)
 
 
 @pytest.mark.parametrize("nbytes,offset", [(16 << 20, 0), ((100 << 20) + 12345, 4096), ((64 << 20) - 2, 6)])

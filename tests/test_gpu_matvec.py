@@ -37,6 +37,10 @@ SHAPES = [
     ("q6k", 5000, 4096),
     ("q4k", 8192, 4096),
     ("q4k", 1030, 8192),     # nb = 32
+    # rows shorter than one wave step (Qwen3-0.6B attn_o; more rows than one
+    # pass covers: streamed)
+    ("q4k", 1024, 2048),
+    ("q6k", 6000, 1024),
     ("q6k", 3, 28672),       # the largest in_features the ABI takes
     ("q4k", 5, 28672),
 ]

@@ -57,6 +57,14 @@ CASES = [
     (("fp16", "fp16"), (513, 7), 8192),
     (("fp16", "fp16", "fp16"), (300, 100, 3), 12288),
     (("fp16",), (200,), 16384),
+    # rows shorter than one wave step (Qwen3-0.6B: hidden 1024, attn_o 2048,
+    # ffn_down 3072): one pass of one / two rows per wave, streamed beyond
+    (("q4k", "q4k", "q6k"), (2048, 1024, 1024), 1024),
+    (("q6k", "q4k"), (700, 300), 2048),
+    (("q4k", "q6k", "q4k"), (5000, 33, 1), 3072),
+    (("q6k", "q6k", "q6k"), (1024, 1024, 3000), 1024),
+    (("fp16", "fp16", "fp16"), (2048, 1024, 1024), 1024),
+    (("fp16",), (6000,), 3072),
 ]
 
 
@@ -75,7 +83,7 @@ def test_group_qwen3_8b_against_oracle(hip, orc):
         assert tol_ok(g.view(H).astype(np.float64), ref).all()
 
 
-@pytest.mark.parametrize("k", [2048, 20480])
+@pytest.mark.parametrize("k", [1536, 20480])
 def test_group_declines_other_lengths_without_writing(hip, k):
     n = 64
     rng = hip.synth.Rng(5)
