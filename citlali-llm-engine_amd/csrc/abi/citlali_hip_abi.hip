@@ -668,15 +668,10 @@ CITLALI_EXPORT int citlali_hip_graph_destroy(void* graph) {
 }
 
 namespace {
-// Row lengths the grouped / prologue GEMV kernels cover: one wave step or
-// less (1024, 2048, 3072: Qwen3-0.6B) and 1..4 whole steps of 4096; gate/up
-// with SwiGLU up to 8192.
-bool norm_length_ok(int in_f) {
-    return in_f == 1024 || in_f == 2048 || in_f == 3072 || (in_f % 4096 == 0 && in_f <= 16384);
-}
-bool gate_up_length_ok(int in_f) {
-    return in_f == 1024 || in_f == 2048 || in_f == 3072 || in_f == 4096 || in_f == 8192;
-}
+// Row lengths the grouped / prologue / gate-up GEMV kernels cover
+bool norm_length_ok(int in_f) { return matvec_fused_length(in_f, true); }
+bool group_length_ok(int in_f) { return matvec_fused_length(in_f, true); }   // hidden-sized inputs
+bool gate_up_length_ok(int in_f) { return matvec_gate_up_length(in_f); }
 // GEMV weight types of the grouped / fused entry points: GGUF Q4_K (12),
 // Q6_K (14) and F16 (1, fp16 rows), as the kernels' kinds 4, 6, 1
 bool fused_type_ok(int t) { return t == 12 || t == 14 || t == 1; }
@@ -718,7 +713,7 @@ CITLALI_EXPORT int citlali_hip_matvec_group(int count, const int* gguf_types, co
     REQUIRE(rows <= INT_MAX, "matvec_group: %lld rows in total exceed INT_MAX", rows);
     if (f16 != 0 && f16 != count)
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: F16 and quantized weights have no grouped kernel");
-    if (!norm_length_ok(in_f))
+    if (!group_length_ok(in_f))
         return fail(CITLALI_ERR_UNSUPPORTED, "matvec_group: in_features %d has no grouped kernel", in_f);
     HIP_TRY(launch_matvec_group(count, kinds, weights, x, outputs, out_features, in_f, nullptr, g_stream));
     return CITLALI_OK;

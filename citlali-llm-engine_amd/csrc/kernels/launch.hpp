@@ -44,6 +44,14 @@ inline void launch_kernel(Kernel kernel, dim3 grid, dim3 block, size_t lds, hipS
 // ---- fused dequant GEMV (matvec_kquant.hip) ----
 // kind: 4 = Q4_K, 6 = Q6_K, 1 = fp16 weights
 size_t matvec_lds_bytes(int kind, int K);
+// in_features the streaming kernels cover: 1024, 2048, 2560, 3072, 4096,
+// 5120, 6144, 8192, 9728, 12288, 16384 (the grouped GEMV and the input
+// prologue take these), and with norm = false also 17408 and 25600 (plain
+// K-quant GEMVs)
+bool matvec_fused_length(int K, bool norm);
+// in_features of the gate/up + SwiGLU launch: 1024, 2048, 2560, 3072, 4096,
+// 5120, 8192
+bool matvec_gate_up_length(int K);
 // fp16 weights [N][K], K a multiple of 256 up to CITLALI_MAX_IN_FEATURES,
 // through the streaming kernels of the K-quant GEMVs
 hipError_t launch_matvec_f16_blocks(const uint16_t* w, const uint16_t* x, void* y, bool f32_out, int K, int N,

@@ -167,6 +167,7 @@ struct Q4K {
     static constexpr int kLanesPerSb = 4;
     static constexpr int kSbPerStep = kWave / kLanesPerSb;
     static constexpr int kHoistSteps = 4;   // x held in registers for rows of up to this many steps
+    static constexpr int kMaxSteps = 7;     // longest row a wave streams (K = 25600)
     struct Frag { u32x4 hdr, q0, q1; };
 
     __device__ static __forceinline__ Frag load(const uint8_t* sb, int j) {
@@ -254,6 +255,7 @@ struct Q6K {
     static constexpr int kLanesPerSb = 4;
     static constexpr int kSbPerStep = kWave / kLanesPerSb;
     static constexpr int kHoistSteps = 4;
+    static constexpr int kMaxSteps = 7;
     struct Frag { uint32_t wa[4], wb[4], u[4]; uint32_t s0, s1, dbits; };
 
     // lane_in_sb = 2*h + ih.  A 210-byte block starts on a 2-byte boundary;
@@ -357,6 +359,9 @@ struct F16 {
     // a lane's x is 32 registers per step: rows of three or four steps
     // read it from LDS instead
     static constexpr int kHoistSteps = 2;
+    // 32 registers of weights per step in flight: longer rows take the flat
+    // kernel
+    static constexpr int kMaxSteps = 4;
     struct Frag { u32x4 v[8]; };
 
     __device__ static __forceinline__ Frag load(const uint8_t* sb, int j) {
@@ -420,13 +425,13 @@ struct RowSet {
 // in LDS behind them.  Loads are branch-free (rows past the end re-read the
 // last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave
 // computes its M rows (all loaded up front) and stops; the grid then has
-// M * W >= rows.  NB (4, 8 or 12; S = 1): rows shorter than one wave step,
-// nb = NB super-blocks; the lanes of blocks NB.. load block NB - 1 (in
-// bounds) and add nothing.
+// M * W >= rows.  NB (an even block count that is not a multiple of 16,
+// S = ceil(NB / 16)): rows ending in a partial wave step; in that step the
+// lanes of blocks NB.. load block NB - 1 (in bounds) and add nothing.
 template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false, int NB = 0>
 __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __restrict__ x, int K, uint8_t* smem,
                                             int gw, int W, const NormIn& nrm) {
-    static_assert(NB == 0 || (S == 1 && NB < QT::kSbPerStep && NB % 4 == 0), "short rows: one partial step");
+    static_assert(NB == 0 || (NB % 2 == 0 && (NB + QT::kSbPerStep - 1) / QT::kSbPerStep == S), "partial last step");
     constexpr int nb = NB ? NB : S * QT::kSbPerStep;   // K = 256 nb
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
@@ -434,8 +439,10 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
 
     const int lane = threadIdx.x & (kWave - 1);
     const int l4 = lane % QT::kLanesPerSb;
-    const int sub = NB ? min(lane / QT::kLanesPerSb, nb - 1) : lane / QT::kLanesPerSb;
-    const bool live = NB == 0 || lane / QT::kLanesPerSb < nb;   // a lane of a real block
+    const int sub = lane / QT::kLanesPerSb;
+    // block of step t this lane reads; false: past the row end (adds nothing)
+    auto blk = [&](int t) { return NB ? min(t * QT::kSbPerStep + sub, nb - 1) : t * QT::kSbPerStep + sub; };
+    auto live = [&](int t) { return NB == 0 || t * QT::kSbPerStep + sub < nb; };
     constexpr int D = S * M;
 
     // matrix of row r and r's first row index in it
@@ -445,7 +452,7 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
         const int r = min(row, N - 1);
         const int sg = seg_of(r);
         const uint8_t* w = sg == 0 ? rs.w[0] : sg == 1 ? rs.w[1] : rs.w[2];
-        const size_t f = (size_t)(r - seg_base(sg)) * nb + t * QT::kSbPerStep + sub;
+        const size_t f = (size_t)(r - seg_base(sg)) * nb + blk(t);
         return QT::load(w + f * QT::kBytes, l4);
     };
 
@@ -465,7 +472,7 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
     typename QT::XRegs xr[kHoist ? S : 1];   // this lane's x, the same for every row
     if constexpr (kHoist) {
 #pragma unroll
-        for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, t * QT::kSbPerStep + sub);
+        for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, blk(t));
     }
 
     for (int row = gw; row < N; row += M * W) {
@@ -476,8 +483,8 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
 #pragma unroll
             for (int t = 0; t < S; ++t) {
                 float c = kHoist ? QT::dot(fr[m * S + t], l4, xr[kHoist ? t : 0])
-                                 : QT::dot(fr[m * S + t], l4, xp, sx, t * QT::kSbPerStep + sub);
-                if constexpr (NB != 0) c = live ? c : 0.f;
+                                 : QT::dot(fr[m * S + t], l4, xp, sx, blk(t));
+                if (NB != 0 && t == S - 1) c = live(t) ? c : 0.f;
                 acc += c;
                 // Refill after the dot has read the slot (issue_after), in
                 // slot order (vmcnt retires loads in issue order: a reordered
@@ -539,18 +546,19 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
 
-    static_assert(NB == 0 || (S == 1 && NB < QT::kSbPerStep && NB % 4 == 0), "short rows: one partial step");
+    static_assert(NB == 0 || (NB % 2 == 0 && (NB + QT::kSbPerStep - 1) / QT::kSbPerStep == S), "partial last step");
     const int lane = threadIdx.x & (kWave - 1);
     const int l4 = lane % QT::kLanesPerSb;
     constexpr int nb = NB ? NB : S * QT::kSbPerStep;
-    const int sub = NB ? min(lane / QT::kLanesPerSb, nb - 1) : lane / QT::kLanesPerSb;
-    const bool live = NB == 0 || lane / QT::kLanesPerSb < nb;   // a lane of a real block
+    const int sub = lane / QT::kLanesPerSb;
+    auto blk = [&](int t) { return NB ? min(t * QT::kSbPerStep + sub, nb - 1) : t * QT::kSbPerStep + sub; };
+    auto live = [&](int t) { return NB == 0 || t * QT::kSbPerStep + sub < nb; };
     constexpr int D = S * M;
     const int W = gridDim.x * kWavesPerBlock;
     const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
 
     auto frag_at = [&](const uint8_t* w, int row, int t) {
-        const size_t f = (size_t)min(row, N - 1) * nb + t * QT::kSbPerStep + sub;
+        const size_t f = (size_t)min(row, N - 1) * nb + blk(t);
         return QT::load(w + f * QT::kBytes, l4);
     };
 
@@ -570,7 +578,7 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
     static_assert(S <= QT::kHoistSteps, "gate/up holds x in registers");
     typename QT::XRegs xr[S];   // this lane's x, the same for every row
 #pragma unroll
-    for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, t * QT::kSbPerStep + sub);
+    for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, blk(t));
 
     for (int row = gw; row < N; row += M * W) {
 #pragma unroll
@@ -581,9 +589,9 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(c
             for (int t = 0; t < S; ++t) {
                 float cg = QT::dot(fg[m * S + t], l4, xr[t]);
                 float cu = QT::dot(fu[m * S + t], l4, xr[t]);
-                if constexpr (NB != 0) {
-                    cg = live ? cg : 0.f;
-                    cu = live ? cu : 0.f;
+                if (NB != 0 && t == S - 1) {
+                    cg = live(t) ? cg : 0.f;
+                    cu = live(t) ? cu : 0.f;
                 }
                 ag += cg;
                 au += cu;
@@ -694,18 +702,24 @@ void launch_rows_once(const RowSet& rs, const uint16_t* x, size_t lds, const Nor
                   stream, rs, x, K, nrm);
 }
 
-// Rows shorter than one wave step (K = 1024, 2048, 3072: Qwen3-0.6B): one
+// Rows ending in a partial wave step (NB blocks, not a multiple of 16).
+// Shorter than one step (K = 1024, 2048, 2560, 3072: Qwen3-0.6B / 4B): one
 // pass of one row per wave up to 1024 rows, of two up to 4096, streamed
-// with one row in flight beyond.
+// with one row in flight beyond; longer rows stream with one row in flight.
 template <class QT, bool kF32, int kSegs, bool kNorm, int NB>
-void launch_short(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
+void launch_partial(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
+    constexpr int S = (NB + QT::kSbPerStep - 1) / QT::kSbPerStep;
     const int rows = rs.end[kSegs - 1];
-    if (rows <= 1024)
-        launch_rows_once<QT, kF32, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
-    else if (rows <= 4096)
-        launch_rows_once<QT, kF32, 2, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
-    else
-        launch_stream<QT, kF32, 1, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
+    if constexpr (S == 1) {
+        if (rows <= 1024)
+            launch_rows_once<QT, kF32, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
+        else if (rows <= 4096)
+            launch_rows_once<QT, kF32, 2, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
+        else
+            launch_stream<QT, kF32, 1, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
+    } else {
+        launch_stream<QT, kF32, S, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
+    }
 }
 
 // K = 4096 S.  Shapes measured on MI355X: at K = 4096 a launch of up to 4096
@@ -734,9 +748,24 @@ bool launch_stream_for(int nb, const RowSet& rs, const uint16_t* x, size_t lds, 
         case 32: launch_stream<QT, kF32, 2, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
         case 48: launch_stream<QT, kF32, 3, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
         case 64: launch_stream<QT, kF32, 4, 1, kSegs, kNorm>(rs, x, lds, nrm, stream); return true;
-        case 4: launch_short<QT, kF32, kSegs, kNorm, 4>(rs, x, lds, nrm, stream); return true;
-        case 8: launch_short<QT, kF32, kSegs, kNorm, 8>(rs, x, lds, nrm, stream); return true;
-        case 12: launch_short<QT, kF32, kSegs, kNorm, 12>(rs, x, lds, nrm, stream); return true;
+        // the other Qwen3 row lengths: hidden 1024 / 2048 / 2560 / 5120, FFN
+        // 3072 / 6144 / 9728 / 17408 / 25600 (the last two without the norm
+        // prologue, which only hidden-sized inputs take)
+        case 4: launch_partial<QT, kF32, kSegs, kNorm, 4>(rs, x, lds, nrm, stream); return true;
+        case 8: launch_partial<QT, kF32, kSegs, kNorm, 8>(rs, x, lds, nrm, stream); return true;
+        case 10: launch_partial<QT, kF32, kSegs, kNorm, 10>(rs, x, lds, nrm, stream); return true;
+        case 12: launch_partial<QT, kF32, kSegs, kNorm, 12>(rs, x, lds, nrm, stream); return true;
+        case 20: launch_partial<QT, kF32, kSegs, kNorm, 20>(rs, x, lds, nrm, stream); return true;
+        case 24: launch_partial<QT, kF32, kSegs, kNorm, 24>(rs, x, lds, nrm, stream); return true;
+        case 38: launch_partial<QT, kF32, kSegs, kNorm, 38>(rs, x, lds, nrm, stream); return true;
+        case 68:
+            if constexpr (kNorm || 5 > QT::kMaxSteps) return false;
+            else launch_partial<QT, kF32, kSegs, kNorm, 68>(rs, x, lds, nrm, stream);
+            return true;
+        case 100:
+            if constexpr (kNorm || 7 > QT::kMaxSteps) return false;
+            else launch_partial<QT, kF32, kSegs, kNorm, 100>(rs, x, lds, nrm, stream);
+            return true;
         default: return false;
     }
 }
@@ -781,15 +810,17 @@ void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int
                         hipStream_t stream) {
     const int na = a.end[2], nbr = b.end[2];
     const size_t lds = std::max(lds_bytes<Q4K>(K), lds_bytes<Q6K>(K));
-    if (S == 1 && na + nbr <= 8192) {
-        // one pass, two rows per wave (attn_q/k/v at hidden 4096: measured
-        // faster than streaming)
-        constexpr int kM = 2;
-        const int ga = (na + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
-        const int gb = (nbr + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
-        launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false, kNorm, NB>), dim3(ga + gb), dim3(kBlock), lds,
-                      stream, a, b, ga, x, K, nrm);
-        return;
+    if constexpr (S == 1) {
+        if (na + nbr <= 8192) {
+            // one pass, two rows per wave (attn_q/k/v at hidden 4096: measured
+            // faster than streaming)
+            constexpr int kM = 2;
+            const int ga = (na + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
+            const int gb = (nbr + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
+            launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false, kNorm, NB>), dim3(ga + gb), dim3(kBlock), lds,
+                          stream, a, b, ga, x, K, nrm);
+            return;
+        }
     }
     // blocks split in proportion to the bytes each set streams
     const double ba = (double)na * Q4K::kBytes, bb = (double)nbr * Q6K::kBytes;
@@ -814,7 +845,11 @@ bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], bool f16, const
         case 64: launch_group_mixed<4, 1, kNorm>(set[0], set[1], x, K, nrm, s); return true;
         case 4: launch_group_mixed<1, 1, kNorm, 4>(set[0], set[1], x, K, nrm, s); return true;
         case 8: launch_group_mixed<1, 1, kNorm, 8>(set[0], set[1], x, K, nrm, s); return true;
+        case 10: launch_group_mixed<1, 1, kNorm, 10>(set[0], set[1], x, K, nrm, s); return true;
         case 12: launch_group_mixed<1, 1, kNorm, 12>(set[0], set[1], x, K, nrm, s); return true;
+        case 20: launch_group_mixed<2, 1, kNorm, 20>(set[0], set[1], x, K, nrm, s); return true;
+        case 24: launch_group_mixed<2, 1, kNorm, 24>(set[0], set[1], x, K, nrm, s); return true;
+        case 38: launch_group_mixed<3, 1, kNorm, 38>(set[0], set[1], x, K, nrm, s); return true;
         default: return false;
     }
 }
@@ -847,6 +882,14 @@ hipError_t launch_gate_up_t(const uint8_t* wg, const uint8_t* wu, const uint16_t
             launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 12>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
                           x, act, K, N, nrm);
             break;
+        case 10:   // hidden 2560 (Qwen3-4B)
+            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 10>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
+                          x, act, K, N, nrm);
+            break;
+        case 20:   // hidden 5120 (Qwen3-14B / 32B)
+            launch_kernel((matvec_gate_up_kernel<QT, 2, 1, kNorm, 20>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
+                          x, act, K, N, nrm);
+            break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -863,6 +906,19 @@ hipError_t launch_gate_up(int kind, const uint8_t* wg, const uint8_t* wu, const 
 }
 
 }  // namespace
+
+bool matvec_fused_length(int K, bool norm) {
+    if (K <= 0 || K % kQK != 0) return false;
+    switch (K / kQK) {
+        case 4: case 8: case 10: case 12: case 16: case 20: case 24: case 32: case 38: case 48: case 64: return true;
+        case 68: case 100: return !norm;
+        default: return false;
+    }
+}
+
+bool matvec_gate_up_length(int K) {
+    return K == 1024 || K == 2048 || K == 2560 || K == 3072 || K == 4096 || K == 5120 || K == 8192;
+}
 
 size_t matvec_lds_bytes(int kind, int K) {
     return kind == 6 ? lds_bytes<Q6K>(K) : kind == 1 ? lds_bytes<F16>(K) : lds_bytes<Q4K>(K);

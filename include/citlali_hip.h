@@ -246,7 +246,8 @@ int citlali_hip_qk_norm_rope_store(uint16_t* q, const uint16_t* k, const uint16_
  * LinearBackend::forward for ffn_gate and ffn_up (both of GGUF type
  * `gguf_type`) then launch_swiglu.  Returns
  * CITLALI_ERR_UNSUPPORTED, launching nothing, for in_features other than
- * 1024, 2048, 3072, 4096 or 8192 -- then use the separate launches. */
+ * 1024, 2048, 2560, 3072, 4096, 5120 or 8192 -- then use the separate
+ * launches. */
 int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, const uint8_t* w_up, const uint16_t* x,
                                       uint16_t* act, int in_features, int out_features);
 /* LinearBackend::forward (linear_backend.cpp:17-61) for `count` (1..3)
@@ -256,9 +257,9 @@ int citlali_hip_matvec_gate_up_swiglu(int gguf_type, const uint8_t* w_gate, cons
  * out_features[i] fp16 values: the results of the separate
  * citlali_hip_matvec_q4k / _q6k / _fp16 calls bit for bit.  Outputs must
  * not overlap each other or x.  Returns CITLALI_ERR_UNSUPPORTED, launching
- * nothing, for in_features other than 1024, 2048, 3072, 4096, 8192, 12288
- * or 16384, or F16 mixed with quantized types -- then use the separate
- * launches. */
+ * nothing, for in_features other than 1024, 2048, 2560, 3072, 4096, 5120,
+ * 6144, 8192, 9728, 12288 or 16384, or F16 mixed with quantized types --
+ * then use the separate launches. */
 int citlali_hip_matvec_group(int count, const int* gguf_types, const uint8_t* const* weights, const uint16_t* x,
                              uint16_t* const* outputs, const int* out_features, int in_features);
 
@@ -271,8 +272,9 @@ int citlali_hip_matvec_group(int count, const int* gguf_types, const uint8_t* co
  * add_inplace + rms_norm before attn_q/k/v, ffn_gate/up and the output
  * (qwen_model.cpp:306, 340-341, 372, 385).  weight, delta and sum_out
  * 16-byte aligned; sum_out must not be x or delta.  in_features 1024,
- * 2048, 3072, 4096, 8192, 12288 or 16384 (gate_up: up to 8192), else
- * CITLALI_ERR_UNSUPPORTED with nothing launched. */
+ * 2048, 2560, 3072, 4096, 5120, 6144, 8192, 9728, 12288 or 16384 (gate_up:
+ * 1024, 2048, 2560, 3072, 4096, 5120 or 8192), else CITLALI_ERR_UNSUPPORTED
+ * with nothing launched. */
 typedef struct citlali_hip_norm {
     const uint16_t* delta;
     const uint16_t* weight;

@@ -150,6 +150,8 @@ def test_argmax_matches_host_rule(hip, orc):
     (1024, 3072), (2560, 100), (28672, 64),       # whole 256-value blocks, any count: the flat walk
     (4096, 1024), (4096, 4096), (4096, 12288),    # Qwen3-8B shapes: one pass / streamed
     (8192, 1000), (12288, 4096), (16384, 300),    # longer rows (x from LDS beyond two steps)
+    (2560, 300), (5120, 257),                     # rows ending in a partial wave step
+    (17408, 30), (25600, 20),                     # beyond four steps: the flat walk
     (1000, 64),                                   # K not a multiple of 256: one wave per row
 ])
 def test_matvec_fp16(hip, orc, k, n, f32):
@@ -252,7 +254,8 @@ def test_qk_norm_rope_store_equals_separate_launches(hip, heads, kv, hd, pos, wi
 
 @pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q4k", 3000, 8192), ("q6k", 2048, 4096),
                                       ("fp16", 12288, 4096), ("fp16", 3000, 8192), ("q4k", 3072, 1024),
-                                      ("q6k", 700, 3072), ("fp16", 5000, 2048)])
+                                      ("q6k", 700, 3072), ("fp16", 5000, 2048), ("q4k", 1000, 2560),
+                                      ("q6k", 500, 5120), ("fp16", 700, 5120)])
 def test_gate_up_swiglu_equals_two_gemvs_and_swiglu(hip, kind, n, k):
     rng = hip.synth.Rng(n + k)
     wg, wu = hip.synth.quant_matrix(kind, rng, n, k), hip.synth.quant_matrix(kind, rng, n, k)

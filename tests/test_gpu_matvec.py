@@ -41,6 +41,14 @@ SHAPES = [
     # pass covers: streamed)
     ("q4k", 1024, 2048),
     ("q6k", 6000, 1024),
+    # the other Qwen3 sizes: rows ending in a partial wave step
+    ("q4k", 300, 2560),      # 4B hidden (nb = 10)
+    ("q4k", 257, 5120),      # 14B / 32B hidden (nb = 20)
+    ("q6k", 300, 6144),      # 1.7B FFN (nb = 24)
+    ("q6k", 500, 9728),      # 4B FFN (nb = 38)
+    ("q6k", 64, 17408),      # 14B FFN (nb = 68)
+    ("q4k", 40, 25600),      # 32B FFN (nb = 100)
+    ("q6k", 40, 25600),
     ("q6k", 3, 28672),       # the largest in_features the ABI takes
     ("q4k", 5, 28672),
 ]

@@ -65,6 +65,13 @@ CASES = [
     (("q6k", "q6k", "q6k"), (1024, 1024, 3000), 1024),
     (("fp16", "fp16", "fp16"), (2048, 1024, 1024), 1024),
     (("fp16",), (6000,), 3072),
+    # the other Qwen3 sizes (4B hidden 2560, 14B / 32B hidden 5120, 1.7B /
+    # 4B FFN 6144 / 9728): partial last wave step
+    (("q4k", "q4k", "q6k"), (4096, 1024, 1024), 2560),
+    (("q4k", "q4k", "q6k"), (5120, 1024, 1024), 5120),
+    (("q6k", "q4k"), (100, 200), 6144),
+    (("q4k",), (300,), 9728),
+    (("fp16", "fp16", "fp16"), (512, 128, 128), 5120),
 ]
 
 

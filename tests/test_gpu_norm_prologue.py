@@ -41,6 +41,8 @@ def reference_norm(hip, x, d, w, k, eps=1e-6):
     (("q4k", "q4k", "q6k"), (2048, 1024, 1024), 1024),   # Qwen3-0.6B attn_q/k/v
     (("q6k",), (300,), 3072),
     (("fp16", "fp16", "fp16"), (2048, 1024, 1024), 1024),
+    (("q4k", "q4k", "q6k"), (4096, 1024, 1024), 2560),   # Qwen3-4B
+    (("q4k", "q6k"), (5120, 1024), 5120),                # Qwen3-14B
 ])
 def test_group_norm_equals_add_rms_norm_then_group(hip, kinds, rows, k, with_delta):
     rng, x, d, w = inputs(hip, k, sum(rows) + k)
@@ -63,7 +65,8 @@ def test_group_norm_equals_add_rms_norm_then_group(hip, kinds, rows, k, with_del
 
 @pytest.mark.parametrize("kind,n,k", [("q4k", 12288, 4096), ("q6k", 1000, 8192), ("fp16", 12288, 4096),
                                       ("fp16", 900, 8192), ("q4k", 3072, 1024), ("q6k", 500, 2048),
-                                      ("fp16", 3072, 1024)])
+                                      ("fp16", 3072, 1024), ("q4k", 9728, 2560), ("q4k", 2000, 5120),
+                                      ("fp16", 1000, 5120)])
 def test_gate_up_norm_equals_add_rms_norm_then_gate_up(hip, kind, n, k):
     rng, x, d, w = inputs(hip, k, n + k)
     wg, wu = (up(hip, hip.synth.quant_matrix(kind, rng, n, k)) for _ in range(2))
@@ -79,7 +82,8 @@ def test_gate_up_norm_equals_add_rms_norm_then_gate_up(hip, kind, n, k):
 @pytest.mark.parametrize("f32_out", [True, False])
 @pytest.mark.parametrize("kind,n,k", [("q6k", 30000, 4096), ("q4k", 5000, 4096), ("q6k", 777, 12288),
                                       ("q4k", 100, 16384), ("fp16", 30000, 4096), ("fp16", 333, 12288),
-                                      ("q6k", 30000, 1024), ("q4k", 1000, 3072), ("fp16", 5000, 2048)])
+                                      ("q6k", 30000, 1024), ("q4k", 1000, 3072), ("fp16", 5000, 2048),
+                                      ("q6k", 20000, 2560), ("q4k", 300, 5120)])
 def test_matvec_norm_equals_add_rms_norm_then_matvec(hip, kind, n, k, f32_out):
     rng, x, d, w = inputs(hip, k, 3 * n + k)
     dw = up(hip, hip.synth.quant_matrix(kind, rng, n, k))
