@@ -21,12 +21,14 @@
 // (with --gguf) loads it with DequantizeToFp16 instead, the reference's
 // default policy: every matrix becomes fp16 in device memory and the fp16
 // GEMVs run.
-// `--model 0.6b` builds Qwen3-0.6B shapes instead (28 layers, hidden 1024,
-// FFN 3072, 16/8 heads, head_dim 128, the same vocab and quant types).
+// `--model` picks another Qwen3 size's shapes (layers, hidden, FFN, query /
+// kv heads; head_dim 128, the same vocab and quant types): 0.6b (28, 1024,
+// 3072, 16/8), 1.7b (28, 2048, 6144, 16/8), 4b (36, 2560, 9728, 32/8), 8b
+// (the default), 14b (40, 5120, 17408, 40/8), 32b (64, 5120, 25600, 64/8).
 // Prints one JSON line.
 //
-// usage: decode_qwen3 [--model 8b|0.6b] [--layers N] [--prompt 512] [--steps 256] [--distinct 4] [--seed 1]
-//                     [--no-graph] [--gguf PATH [--fp16]]
+// usage: decode_qwen3 [--model 0.6b|1.7b|4b|8b|14b|32b] [--layers N] [--prompt 512] [--steps 256]
+//                     [--distinct 4] [--seed 1] [--no-graph] [--gguf PATH [--fp16]]
 #include "citlali/common.h"
 #include "citlali/compute/hip/kernels.h"
 #include "citlali/io/gguf_reader.h"
@@ -122,14 +124,33 @@ int arg(int argc, char** argv, const char* key, int def) {
 
 }  // namespace
 
+struct ModelShape {
+    const char* name;
+    int layers, hidden, ffn, heads;
+    const char* workload;
+};
+constexpr ModelShape kShapes[] = {
+    {"0.6b", 28, 1024, 3072, 16, "Qwen3-0.6B shapes, synthetic Q4_K_M greedy decode"},
+    {"1.7b", 28, 2048, 6144, 16, "Qwen3-1.7B shapes, synthetic Q4_K_M greedy decode"},
+    {"4b", 36, 2560, 9728, 32, "Qwen3-4B shapes, synthetic Q4_K_M greedy decode"},
+    {"8b", 36, 4096, 12288, 32, "BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode"},
+    {"14b", 40, 5120, 17408, 40, "Qwen3-14B shapes, synthetic Q4_K_M greedy decode"},
+    {"32b", 64, 5120, 25600, 64, "Qwen3-32B shapes, synthetic Q4_K_M greedy decode"},
+};
+
 int main(int argc, char** argv) {
     const char* model_arg = str_arg(argc, argv, "--model");
-    const bool small = model_arg != nullptr && std::strcmp(model_arg, "0.6b") == 0;
-    if (model_arg != nullptr && !small && std::strcmp(model_arg, "8b") != 0) {
-        std::fprintf(stderr, "decode_qwen3: --model is 8b or 0.6b\n");
-        return 2;
+    const ModelShape* shape = &kShapes[3];
+    if (model_arg != nullptr) {
+        shape = nullptr;
+        for (const ModelShape& m : kShapes)
+            if (std::strcmp(model_arg, m.name) == 0) shape = &m;
+        if (shape == nullptr) {
+            std::fprintf(stderr, "decode_qwen3: --model is one of 0.6b 1.7b 4b 8b 14b 32b\n");
+            return 2;
+        }
     }
-    const int layers = arg(argc, argv, "--layers", small ? 28 : 36);
+    const int layers = arg(argc, argv, "--layers", shape->layers);
     const int prompt = arg(argc, argv, "--prompt", 512);
     const int steps = arg(argc, argv, "--steps", 256);
     const int distinct = arg(argc, argv, "--distinct", 4);
@@ -146,7 +167,7 @@ int main(int argc, char** argv) {
         cfg.architecture = "qwen3";
         cfg.vocab_size = 151936;
         cfg.context_length = 40960;
-        const int H = small ? 1024 : 4096, F = small ? 3072 : 12288, HEADS = small ? 16 : 32, KVH = 8;
+        const int H = shape->hidden, F = shape->ffn, HEADS = shape->heads, KVH = 8;
         const int NQ = HEADS * 128, NKV = KVH * 128, V = 151936;
         cfg.embedding_length = (uint32_t)H;
         cfg.block_count = layers;
@@ -334,8 +355,7 @@ int main(int argc, char** argv) {
                     "\"prompt_ms_per_token_wall\": %.4f, \"setup_s\": %.1f, \"token_checksum\": %llu, "
                     "\"weights_from\": \"%s\", \"gguf_file_bytes\": %.0f, \"gguf_write_s\": %.2f, "
                     "\"gguf_load_s\": %.3f, \"gguf_load_GBps\": %.2f}\n",
-                    small ? "Qwen3-0.6B shapes, synthetic Q4_K_M greedy decode"
-                          : "BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode",
+                    shape->workload,
                     layers, distinct, prompt, steps, steps / (decode_ms * 1e-3), decode_ms / steps,
                     graph_pass ? "QwenModel::decode_greedy (graph replay), wall clock"
                                : "forward_token loop, wall clock (--no-graph)",
