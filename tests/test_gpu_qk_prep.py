@@ -63,7 +63,7 @@ def run_pair(hip, heads, kv_heads, ctx, pos, seed, device_position, norms=True):
 
 
 @pytest.mark.parametrize("device_position", [False, True])
-@pytest.mark.parametrize("heads,kv_heads", [(32, 8), (16, 8), (64, 8), (24, 8)])
+@pytest.mark.parametrize("heads,kv_heads", [(32, 8), (16, 8), (64, 8), (24, 8), (40, 8)])
 def test_fused_equals_separate_launches(hip, heads, kv_heads, device_position):
     ctx = 1200
     for pos in (0, 1, 15, 16, 63, 64, 200, 255, 256, 300, 511, 512, 700, 1023, ctx - 1):
