@@ -29,3 +29,12 @@ def test_host_layer_gpu():
     """LinearBackend::forward for Q4_K, Q6_K and fp16 weights, launch_attention
     and launch_embed_q6k through the C++ API, against the oracle."""
     _run("gpu", 300)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("mode", ["greedy", "greedy2", "graph", "gguf"])
+def test_host_layer_model(mode):
+    """QwenModel: greedy decode against the oracle's forward (greedy,
+    greedy2: the model forms in two halves), decode_greedy's graph replay
+    against the forward_token loop (graph), loading from a GGUF file (gguf)."""
+    _run(mode, 300)
