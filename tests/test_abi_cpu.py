@@ -1,7 +1,7 @@
 """The C ABI without a GPU: the libraries load, export every symbol the
 headers declare, and reject bad arguments before touching the device (the
-failure cases of SURVEY-listed reference checks: null buffers, in_features
-not a multiple of 256, head_count % head_count_kv, position >= max_context)."""
+failure cases of the reference's own checks: null buffers, in_features not
+a multiple of 256, head_count % head_count_kv, position >= max_context)."""
 from __future__ import annotations
 
 import ctypes
