@@ -356,9 +356,9 @@ struct F16 {
     static constexpr int kSumLayout = kPlain;
     static constexpr int kLanesPerSb = 4;
     static constexpr int kSbPerStep = kWave / kLanesPerSb;
-    // a lane's x is 32 registers per step: rows of three or four steps
-    // read it from LDS instead
-    static constexpr int kHoistSteps = 2;
+    // a lane's x is 32 registers per step: rows of four steps read it from
+    // LDS instead
+    static constexpr int kHoistSteps = 3;
     // 32 registers of weights per step in flight: longer rows take the flat
     // kernel
     static constexpr int kMaxSteps = 4;
