@@ -198,6 +198,96 @@ def run_gpu(args):
     return total_ms, dominant, dom_ms, per, (stream_gbps, copy_gbps), host
 
 
+ROTATE_BYTES = 512 << 20   # configs 1 and 2 cycle through this much of independent copies
+
+
+def _rotated_copies(hip, host_bytes, unit_bytes):
+    """ceil(ROTATE_BYTES / unit_bytes) device copies of `host_bytes` (uint8)
+    in one allocation, each slot 256-byte aligned; returns (buffer, slot, n)."""
+    slot = -(-unit_bytes // 256) * 256
+    n = -(-ROTATE_BYTES // unit_bytes)
+    buf = hip.DeviceArray(slot * n)
+    buf.upload(host_bytes, 0)
+    for i in range(1, n):
+        hip.check(hip.load().citlali_hip_memcpy_d2d(buf.at(i * slot), buf.vp, host_bytes.nbytes))
+    return buf, slot, n
+
+
+def _time_rotated(hip, launch, n, reps):
+    """Mean launch time (us) over reps passes of n back-to-back launches
+    (launch(i) uses copy i): HIP events around all of them, and the kernels'
+    own dispatch-stamped time of one more pass."""
+    for i in range(n):
+        launch(i)
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record()
+    for _ in range(reps):
+        for i in range(n):
+            launch(i)
+    e1.record()
+    e1.synchronize()
+    wall_us = e0.elapsed_ms(e1) / (reps * n) * 1e3
+    timers = [hip.device.KernelTimer() for _ in range(n)]
+    for i in range(n):
+        with timers[i]:
+            launch(i)
+    hip.synchronize()
+    kern_us = sum(t.ms() for t in timers) / n * 1e3
+    return wall_us, kern_us
+
+
+def matvec_cfg1():
+    """Q4_K GEMV of a 3072 x 1024 matrix (4 super-blocks
+    per row, seed 0), x N(0,1) fp16, y fp32 (citlali_hip_matvec_q4k_to_float);
+    also the same bytes read as 1024 rows of 12 super-blocks (K = 3072).
+    Rotated over >= 512 MB of copies so the weights come from HBM."""
+    import pycitlali as hip
+    rng = hip.synth.Rng(0)
+    w = hip.synth.quant_matrix("q4k", rng, 3072, 1024)
+    x = hip.synth.normal_f16(rng, 3072)
+    buf, slot, n = _rotated_copies(hip, w, w.nbytes)
+    dx = hip.DeviceArray.from_numpy(x)
+    dy = hip.DeviceArray(3072 * 4)
+    out = {}
+    for name, rows, cols in (("3072x1024", 3072, 1024), ("1024x3072", 1024, 3072)):
+        wall, kern = _time_rotated(hip, lambda i: hip.device.matvec("q4k", buf.at(i * slot), dx, dy, cols, rows,
+                                                                   f32_out=True), n, 10)
+        alg = w.nbytes + cols * 2 + rows * 4
+        out[name] = {"bytes_per_launch": alg, "copies_rotated": n, "us_per_launch": round(wall, 3),
+                     "GBps": round(alg / (wall * 1e-6) / 1e9, 1), "frac_of_8TBps": round(alg / (wall * 1e-6) / 8e12, 4),
+                     "kernel_us": round(kern, 3), "kernel_GBps": round(alg / (kern * 1e-6) / 1e9, 1)}
+    for a in (buf, dx, dy):
+        a.close()
+    return {"workload": "BASELINE config 1: Q4_K GEMV 3072 rows x 1024 cols (4 super-blocks/row), fp32 y; "
+                        "also read as 1024 x 3072 (12 super-blocks/row)", **out}
+
+
+def attention_cfg2():
+    """Qwen3-0.6B decode attention, 16 query / 8 kv heads,
+    head_dim 128, 1024 cached positions (position 1023), q/K/V N(0,1) fp16
+    (seed 0), fp16 output; rotated over >= 512 MB of K/V copies."""
+    import pycitlali as hip
+    heads, kv, hd, L = 16, 8, 128, 1024
+    rng = hip.synth.Rng(0)
+    q = hip.synth.normal_f16(rng, heads * hd)
+    k = hip.synth.normal_f16(rng, L * kv * hd)
+    v = hip.synth.normal_f16(rng, L * kv * hd)
+    kv_bytes = k.nbytes
+    kb, slot, n = _rotated_copies(hip, np.concatenate([k, v]).view(np.uint8), 2 * kv_bytes)   # slot: K then V
+    dq = hip.DeviceArray.from_numpy(q)
+    scores = hip.DeviceArray(heads * L * 4)
+    do = hip.DeviceArray(heads * hd * 2)
+    wall, kern = _time_rotated(hip, lambda i: hip.device.attention(dq, kb.at(i * slot), kb.at(i * slot + kv_bytes),
+                                                                  scores, do, L - 1, L, heads, kv, hd), n, 10)
+    alg = 2 * kv_bytes + 2 * heads * hd * 2
+    for a in (kb, dq, scores, do):
+        a.close()
+    return {"workload": "BASELINE config 2: Qwen3-0.6B decode attention, 16/8 heads, head_dim 128, L=1024",
+            "bytes_per_launch": alg, "copies_rotated": n, "us_per_launch": round(wall, 3),
+            "GBps": round(alg / (wall * 1e-6) / 1e9, 1), "frac_of_8TBps": round(alg / (wall * 1e-6) / 8e12, 4),
+            "kernel_us": round(kern, 3), "kernel_GBps": round(alg / (kern * 1e-6) / 1e9, 1)}
+
+
 def attention_cfg4():
     """BASELINE config 4 beside the headline: 16 independent sequences at the
     Qwen3-8B head shape (32 / 8 heads, head_dim 128) in one batched attention
@@ -245,30 +335,147 @@ def attention_cfg4():
 
 
 def cpu_baseline(host, budget_s):
-    """The oracle (restated reference arithmetic) on the host cores: one
-    layer step -- every GEMV as repo dequant to fp16 + fp32 dot, attention in
-    fp32 -- repeated until ~budget_s seconds have passed."""
+    """BASELINE's CPU path on this machine's host cores, in the same run: the
+    reference's own host dequant (weight_loader.cpp:147-323, compiled from
+    its sources into oracle/_ref by oracle/Makefile; the oracle's pinned
+    restatement of it where that build is absent) of each weight row to fp16,
+    then an fp32 dot -- variant (i), per call, the CPU analogue of the fused
+    GPU kernel -- or the fp32 dot over rows dequantised beforehand (variant
+    (ii)); attention in fp32 (the oracle's, kernels.cu:545-649's arithmetic:
+    the reference has no CPU attention).  Every config at 1 thread and at
+    all cores, on bounded samples (each said in `sample`), ~budget_s per
+    measurement.  Returns (headline, entries): the headline is config 3,
+    variant (i), all cores."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    from oracle_binding import Oracle
+    from oracle_binding import Oracle, RefLib
+    import pycitlali as hip
     orc = Oracle()
-    threads = int(orc.lib.orc_num_threads())
+    ref = RefLib.try_load()
+    cores = int(orc.lib.orc_num_threads())
+    kind = "reference" if ref else "port"
+    code = ("reference dequant (oracle/_ref) + fp32 dot" if ref else
+            "oracle restatement of the reference dequant + fp32 dot")
+
+    def mv_i(k, w, x, cin, rows, th):
+        if ref:
+            return ref.matvec_dequant_dot(k, w, x, cin, rows, th)
+        return orc.matvec_f16dot(k, w, x, cin, rows, th)
+
+    def mv_ii(wf16, x, cin, rows, th):
+        if ref:
+            return ref.matvec_f16_dot(wf16, x, cin, rows, th)
+        y = np.empty(rows, np.float32)
+        orc.lib.orc_matvec_f16(wf16.ctypes.data, x.ctypes.data, y.ctypes.data, cin, rows, th)
+        return y
+
+    def dequant(k, w, count):
+        if ref:
+            return ref.dequant(k, w, count)
+        out = np.empty(count, np.uint16)
+        getattr(orc.lib, f"orc_dequant_{k}_f16")(w.ctypes.data, count, out.ctypes.data)
+        return out
+
+    def rate(fn, budget):
+        """calls per second: at least one call, then until `budget` seconds"""
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return n / el, n, el
+
+    entries = []
+
+    def add(config, variant, th, value, unit, sample):
+        entries.append({"config": config, "variant": variant, "threads": th, "value": round(value, 4),
+                        "unit": unit, "kind": kind, "sample": sample})
+
+    spec = {n: (k, r, c, i) for n, k, r, c, i, _ in GEMVS}
     x = host["x"]
-    q = np.ascontiguousarray(host["x"][: HEADS * HEAD_DIM])
-    up = np.ascontiguousarray(np.resize(host["x"], FFN))
-    ins = {"x": x, "att": q, "up": up}
-    runs, t_start = 0, time.perf_counter()
-    while True:
-        for n, k, r, c, i, _ in GEMVS:
-            orc.matvec_f16dot(k, host[n], ins[i], c, r, threads)
-        orc.attention_f32(q, host["k_cache"], host["v_cache"], CTX - 1, HEADS, KV_HEADS, HEAD_DIM, threads)
-        runs += 1
-        el = time.perf_counter() - t_start
-        if el >= budget_s:
-            break
-    step_bytes = sum(kernel_bytes().values())
-    return {"value": round(step_bytes * runs / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{runs} full Qwen3-8B layer step(s) (7 GEMVs dequant->fp16->fp32 dot + fp32 attention "
-                      f"at L={CTX}) in {el:.1f} s"}
+    ins = {"x": x, "att": np.ascontiguousarray(x[: HEADS * HEAD_DIM]), "up": np.ascontiguousarray(np.resize(x, FFN))}
+    f16 = {n: dequant(k, host[n], r * c) for n, (k, r, c, _) in spec.items()}
+    kb = kernel_bytes()
+    layer_bytes = sum(kb.values())
+
+    # config 1: Q4_K 3072 x 1024, fp32 y
+    rng = hip.synth.Rng(0)
+    w1 = hip.synth.quant_matrix("q4k", rng, 3072, 1024)
+    x1 = hip.synth.normal_f16(rng, 1024)
+    w1f = dequant("q4k", w1, 3072 * 1024)
+    b1 = w1.nbytes + 1024 * 2 + 3072 * 4
+    for th in (1, cores):
+        r, n, el = rate(lambda: mv_i("q4k", w1, x1, 1024, 3072, th), budget_s)
+        add(1, "i", th, b1 * r / 1e9, "GB/s", f"{n} calls in {el:.1f} s ({code}; {1e6 / r:.0f} us/call)")
+        r, n, el = rate(lambda: mv_ii(w1f, x1, 1024, 3072, th), budget_s)
+        add(1, "ii", th, b1 * r / 1e9, "GB/s", f"{n} calls in {el:.1f} s (fp32 dot over pre-dequantised fp16; "
+                                                f"{1e6 / r:.0f} us/call)")
+
+    # config 2: attention 16/8/128 at L = 1024
+    rng = hip.synth.Rng(0)
+    q2 = hip.synth.normal_f16(rng, 16 * 128)
+    k2 = hip.synth.normal_f16(rng, 1024 * 8 * 128)
+    v2 = hip.synth.normal_f16(rng, 1024 * 8 * 128)
+    b2 = 2 * k2.nbytes + 2 * 16 * 128 * 2
+    for th in (1, cores):
+        r, n, el = rate(lambda: orc.attention_f32(q2, k2, v2, 1023, 16, 8, 128, th), budget_s)
+        add(2, "fp32", th, b2 * r / 1e9, "GB/s", f"{n} calls in {el:.1f} s ({1e6 / r:.0f} us/call)")
+
+    # config 3: one Qwen3-8B layer step (7 GEMVs + attention at L = 8192)
+    q = ins["att"]
+
+    def layer_step(th, variant, L=CTX):
+        for n, (k, r, c, i) in spec.items():
+            if variant == "i":
+                mv_i(k, host[n], ins[i], c, r, th)
+            else:
+                mv_ii(f16[n], ins[i], c, r, th)
+        orc.attention_f32(q, host["k_cache"], host["v_cache"], L - 1, HEADS, KV_HEADS, HEAD_DIM, th)
+
+    headline = None
+    for th in (1, cores):
+        for variant in ("i", "ii"):
+            r, n, el = rate(lambda: layer_step(th, variant), budget_s)
+            add(3, variant, th, layer_bytes * r / 1e9, "GB/s",
+                f"{n} full Qwen3-8B layer step(s) (7 GEMVs, "
+                f"{code if variant == 'i' else 'fp32 dot over pre-dequantised fp16'}; fp32 attention at "
+                f"L={CTX}) in {el:.1f} s")
+            if th == cores and variant == "i":
+                headline = dict(entries[-1])
+
+    # config 4: 16 sequences, lengths from default_rng(4) in [4096, 32768]:
+    # timed on the first sequences of the set, scaled per K/V byte
+    lens = np.random.default_rng(4).integers(4096, 32768 + 1, 16)
+    gen = np.random.default_rng(44)
+    kv_s = [gen.standard_normal(int(L) * KV_HEADS * HEAD_DIM, dtype=np.float32).astype(np.float16).view(np.uint16)
+            for L in lens[:2]]
+    vv_s = [gen.standard_normal(int(L) * KV_HEADS * HEAD_DIM, dtype=np.float32).astype(np.float16).view(np.uint16)
+            for L in lens[:2]]
+    q4 = gen.standard_normal(HEADS * HEAD_DIM, dtype=np.float32).astype(np.float16).view(np.uint16)
+    for th, nseq in ((1, 1), (cores, 2)):
+        def seqs():
+            for j in range(nseq):
+                orc.attention_f32(q4, kv_s[j], vv_s[j], int(lens[j]) - 1, HEADS, KV_HEADS, HEAD_DIM, th)
+        r, n, el = rate(seqs, budget_s)
+        bytes_ = int(sum(lens[:nseq])) * KV_HEADS * HEAD_DIM * 4
+        add(4, "fp32", th, bytes_ * r / 1e9, "GB/s",
+            f"sequence(s) 0..{nseq - 1} of the 16 (L={','.join(str(int(v)) for v in lens[:nseq])}), "
+            f"{n} pass(es) in {el:.1f} s; the full set is {int(lens.sum())} positions")
+
+    # config 5: tok/s of the whole decode = 36 layer steps (attention at the
+    # mean decode length 640) + the Q6_K output GEMV (151936 x 4096), from one
+    # layer step and 1/16 of the output rows
+    rows_part = 151936 // 16
+    wo = hip.synth.quant_matrix("q6k", hip.synth.Rng(5), rows_part, HIDDEN)
+    for th in (1, cores):
+        t_layer = 1.0 / rate(lambda: layer_step(th, "i", L=640), budget_s / 2)[0]
+        t_out = 1.0 / rate(lambda: mv_i("q6k", wo, x, HIDDEN, rows_part, th), budget_s / 2)[0]
+        tok_s = 1.0 / (36 * t_layer + 16 * t_out)
+        add(5, "i", th, tok_s, "tok/s", f"1 layer step at L=640 ({t_layer * 1e3:.0f} ms) x 36 + 1/16 of the output "
+                                        f"GEMV rows ({t_out * 1e3:.0f} ms) x 16 ({code})")
+    cpu = {"value": headline["value"], "unit": headline["unit"], "cores": cores, "kind": kind,
+           "sample": headline["sample"]}
+    return cpu, entries
 
 
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "cfg3_layer_hbm_traffic_pmc.md")
@@ -279,15 +486,22 @@ DECODE_BIN = os.path.join(ROOT, "citlali-llm-engine_amd", "bin", "decode_qwen3")
 
 def decode_cfg5(fp16=False):
     """BASELINE config 5 beside the headline: the synthetic Qwen3-8B greedy
-    decode through QwenModel (bin/decode_qwen3, a child process), loaded from
-    a GGUF file of its weights (written to the temp directory, removed after
+    decode through QwenModel (bin/decode_qwen3, a child process; every one of
+    the 36 layers has its own weights), loaded from a GGUF file of its
+    weights (written to /dev/shm or the temp directory, removed after
     loading), 512-token prompt then 256 greedy steps; decode tok/s.  fp16:
     loaded with DequantizeToFp16, 64-token prompt then 128 steps."""
     import subprocess
     import tempfile
     if not os.path.exists(DECODE_BIN):
         return {"error": "citlali-llm-engine_amd/bin/decode_qwen3 is not built"}
-    path = os.path.join(tempfile.gettempdir(), f"citlali_cfg5_{os.getpid()}.gguf")
+    import shutil
+    # ~5.4 GB with every layer's own weights: a RAM-backed directory when it
+    # has room (the load then reads page-cache pages), else the temp directory
+    base = tempfile.gettempdir()
+    if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > (12 << 30):
+        base = "/dev/shm"
+    path = os.path.join(base, f"citlali_cfg5_{os.getpid()}.gguf")
     cmd = [DECODE_BIN, "--gguf", path] + (["--fp16", "--prompt", "64", "--steps", "128"] if fp16 else [])
     try:
         p = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
@@ -317,7 +531,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=2.0, help="per CPU-baseline measurement")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 whole-model decode run")
     args = ap.parse_args()
@@ -360,9 +574,11 @@ def main():
         "copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": None,
     }
+    line["matvec_cfg1"] = matvec_cfg1()
+    line["attention_cfg2"] = attention_cfg2()
     line["attention_cfg4"] = attention_cfg4()
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(host, args.cpu_seconds)
+        line["cpu_baseline"], line["cpu_baseline_configs"] = cpu_baseline(host, args.cpu_seconds)
     line["decode_cfg5"] = None if args.no_decode else decode_cfg5()
     line["decode_cfg5_fp16"] = None if args.no_decode else decode_cfg5(fp16=True)
     print(json.dumps(line), flush=True)

@@ -80,7 +80,9 @@ int workspace_for(size_t bytes, float** out) {
     Workspace& w = g_ws[dev];
     if (w.bytes < bytes) {
         if (w.ptr) {
-            HIP_TRY(hipStreamSynchronize(g_stream));   // a queued launch may still use it
+            // a launch queued on any stream (the library stream may have
+            // changed since) may still use it
+            HIP_TRY(hipDeviceSynchronize());
             HIP_TRY(hipFree(w.ptr));
         }
         w.ptr = nullptr;
@@ -345,8 +347,19 @@ CITLALI_EXPORT int citlali_hip_attention_plan_length(int length, int max_context
 CITLALI_EXPORT size_t citlali_hip_attention_workspace_bytes(int max_positions_bound, int nseq, int heads,
                                                             int kv_heads, int head_dim) {
     if (max_positions_bound <= 0 || nseq <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return 0;
+    return attention_workspace_bound(max_positions_bound, nseq, kv_heads, heads, head_dim, kAttnTargetBlocks);
+}
+
+CITLALI_EXPORT int citlali_hip_attention_plan_info(int max_positions_bound, int nseq, int heads, int kv_heads,
+                                                   int head_dim, int* chunk, int* n_splits) {
+    REQUIRE(chunk && n_splits, "attention_plan_info: null output pointer");
+    REQUIRE(max_positions_bound > 0 && nseq > 0, "attention_plan_info: bound and nseq must be positive");
+    const int st = check_attn_shape(heads, kv_heads, head_dim);
+    if (st) return st;
     const AttnPlan p = plan_attention(max_positions_bound, nseq, kv_heads, heads, head_dim, kAttnTargetBlocks);
-    return attention_workspace_bytes(p, nseq, heads, head_dim);
+    *chunk = p.chunk;
+    *n_splits = p.n_splits;
+    return CITLALI_OK;
 }
 
 CITLALI_EXPORT int citlali_hip_attention_batched(const uint16_t* q, const uint16_t* k_cache,

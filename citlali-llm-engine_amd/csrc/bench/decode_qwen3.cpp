@@ -6,11 +6,13 @@
 // output and the token embedding; a prompt of 512 random token ids fed as
 // the reference's session does (session.cpp:71-74: one forward_token per
 // prompt token, logits only for the last), then 256 greedy steps
-// (session.cpp:92).  Weights are random quant blocks whose d keeps every
-// matrix at rms ~ gain/sqrt(in) (random Q4_K codes give rms ~ 300 d, Q6_K
-// ~ 1366 d); `--distinct N` fills N distinct layer byte sets and gives every
-// one of the 36 layers its own device copy, so each layer reads its own
-// weights from HBM.  The greedy steps run twice: as the reference's loop of
+// (session.cpp:92).  Weights are the random quant blocks of
+// synth_qwen3.hpp (d keeps every matrix at rms ~ gain/sqrt(in)); every layer
+// has its own weights (36 distinct sets for Qwen3-8B, ~4.4 GB of layer
+// weights read from HBM per token); `--distinct N` reuses N byte sets
+// cyclically instead (each layer still gets its own device copy when loaded
+// from handles; a GGUF file then stores each set once).  The greedy steps
+// run twice: as the reference's loop of
 // forward_token calls, then through QwenModel::decode_greedy (each step
 // replayed from a captured HIP graph); both must give the same tokens.
 // With `--gguf PATH` the same weights are first written to a GGUF file at
@@ -28,14 +30,16 @@
 // Prints one JSON line.
 //
 // usage: decode_qwen3 [--model 0.6b|1.7b|4b|8b|14b|32b] [--layers N] [--prompt 512] [--steps 256]
-//                     [--distinct 4] [--seed 1] [--no-graph] [--gguf PATH [--fp16]]
+//                     [--distinct N] [--seed 1] [--no-graph] [--gguf PATH [--fp16]]
 #include "citlali/common.h"
 #include "citlali/compute/hip/kernels.h"
 #include "citlali/io/gguf_reader.h"
 #include "citlali/model/qwen_model.h"
 #include "citlali_hip.h"
 #include "gguf_out.hpp"
+#include "synth_qwen3.hpp"
 
+#include <algorithm>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
@@ -48,41 +52,6 @@ using namespace citlali;
 using compute::GgufTensorType;
 
 namespace {
-
-struct SplitMix {
-    uint64_t s;
-    uint64_t next() {
-        uint64_t z = (s += 0x9e3779b97f4a7c15ull);
-        z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-        z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-        return z ^ (z >> 31);
-    }
-};
-
-uint16_t half_bits(float v) { return compute::float_to_half_bits(v); }
-
-std::vector<uint8_t> quant_bytes(uint64_t seed, GgufTensorType t, int rows, int cols, double gain) {
-    const size_t bb = compute::gguf_type_block_bytes(t);
-    const size_t blocks = (size_t)rows * cols / 256;
-    std::vector<uint8_t> b(blocks * bb);
-    SplitMix r{seed};
-    for (size_t i = 0; i + 8 <= b.size(); i += 8) {
-        const uint64_t v = r.next();
-        std::memcpy(b.data() + i, &v, 8);
-    }
-    const double d = gain / std::sqrt((double)cols) / (t == GgufTensorType::Q4_K ? 300.0 : 1366.0);
-    const uint16_t dh = half_bits((float)d);
-    for (size_t i = 0; i < blocks; ++i) {
-        uint8_t* p = b.data() + i * bb;
-        if (t == GgufTensorType::Q4_K) {
-            std::memcpy(p, &dh, 2);
-            std::memcpy(p + 2, &dh, 2);
-        } else {
-            std::memcpy(p + 208, &dh, 2);
-        }
-    }
-    return b;
-}
 
 model::WeightHandle quant_handle(const std::vector<uint8_t>& bytes, GgufTensorType t, int rows, int cols,
                                  const std::string& name) {
@@ -98,7 +67,7 @@ model::WeightHandle quant_handle(const std::vector<uint8_t>& bytes, GgufTensorTy
 }
 
 model::WeightHandle norm_handle(int n, const std::string& name) {
-    std::vector<uint16_t> v(n, half_bits(1.0f));
+    std::vector<uint16_t> v(n, compute::float_to_half_bits(1.0f));
     model::WeightHandle w;
     w.name = name;
     w.gguf_type = GgufTensorType::F16;
@@ -124,26 +93,12 @@ int arg(int argc, char** argv, const char* key, int def) {
 
 }  // namespace
 
-struct ModelShape {
-    const char* name;
-    int layers, hidden, ffn, heads;
-    const char* workload;
-};
-constexpr ModelShape kShapes[] = {
-    {"0.6b", 28, 1024, 3072, 16, "Qwen3-0.6B shapes, synthetic Q4_K_M greedy decode"},
-    {"1.7b", 28, 2048, 6144, 16, "Qwen3-1.7B shapes, synthetic Q4_K_M greedy decode"},
-    {"4b", 36, 2560, 9728, 32, "Qwen3-4B shapes, synthetic Q4_K_M greedy decode"},
-    {"8b", 36, 4096, 12288, 32, "BASELINE config 5: Qwen3-8B synthetic Q4_K_M greedy decode"},
-    {"14b", 40, 5120, 17408, 40, "Qwen3-14B shapes, synthetic Q4_K_M greedy decode"},
-    {"32b", 64, 5120, 25600, 64, "Qwen3-32B shapes, synthetic Q4_K_M greedy decode"},
-};
-
 int main(int argc, char** argv) {
     const char* model_arg = str_arg(argc, argv, "--model");
-    const ModelShape* shape = &kShapes[3];
+    const bench::Qwen3Shape* shape = &bench::kConfig5;
     if (model_arg != nullptr) {
         shape = nullptr;
-        for (const ModelShape& m : kShapes)
+        for (const bench::Qwen3Shape& m : bench::kQwen3Shapes)
             if (std::strcmp(model_arg, m.name) == 0) shape = &m;
         if (shape == nullptr) {
             std::fprintf(stderr, "decode_qwen3: --model is one of 0.6b 1.7b 4b 8b 14b 32b\n");
@@ -153,7 +108,7 @@ int main(int argc, char** argv) {
     const int layers = arg(argc, argv, "--layers", shape->layers);
     const int prompt = arg(argc, argv, "--prompt", 512);
     const int steps = arg(argc, argv, "--steps", 256);
-    const int distinct = arg(argc, argv, "--distinct", 4);
+    const int distinct = std::max(1, std::min(layers, arg(argc, argv, "--distinct", layers)));
     const uint64_t seed = (uint64_t)arg(argc, argv, "--seed", 1);
     bool graph_pass = true;   // --no-graph: forward_token loop only (for tracing tools)
     bool fp16_weights = false;
@@ -179,22 +134,11 @@ int main(int argc, char** argv) {
         cfg.rope_theta = 1e6f;
 
         const auto t0 = std::chrono::steady_clock::now();
-        struct LayerBytes {
-            std::vector<uint8_t> q, k, v, o, gate, up, down;
-        };
-        std::vector<LayerBytes> sets(distinct);
-        for (int i = 0; i < distinct; ++i) {
-            const uint64_t s = seed * 1000 + (uint64_t)i * 10;
-            sets[i].q = quant_bytes(s + 1, GgufTensorType::Q4_K, NQ, H, 1.0);
-            sets[i].k = quant_bytes(s + 2, GgufTensorType::Q4_K, NKV, H, 1.0);
-            sets[i].v = quant_bytes(s + 3, GgufTensorType::Q6_K, NKV, H, 1.0);
-            sets[i].o = quant_bytes(s + 4, GgufTensorType::Q4_K, H, NQ, 0.5);
-            sets[i].gate = quant_bytes(s + 5, GgufTensorType::Q4_K, F, H, 1.0);
-            sets[i].up = quant_bytes(s + 6, GgufTensorType::Q4_K, F, H, 1.0);
-            sets[i].down = quant_bytes(s + 7, GgufTensorType::Q6_K, H, F, 0.5);
-        }
-        const std::vector<uint8_t> embd = quant_bytes(seed * 7 + 11, GgufTensorType::Q6_K, V, H, std::sqrt((double)H));
-        const std::vector<uint8_t> outw = quant_bytes(seed * 7 + 13, GgufTensorType::Q6_K, V, H, 3.0);
+        using bench::LayerBytes;
+        std::vector<LayerBytes> sets;
+        for (int i = 0; i < distinct; ++i) sets.push_back(bench::layer_bytes(seed, i, *shape));
+        const std::vector<uint8_t> embd = bench::embedding_bytes(seed, *shape);
+        const std::vector<uint8_t> outw = bench::output_bytes(seed, *shape);
         const int ctx = prompt + steps;
         model::QwenModel m;
         const char* gguf_path = str_arg(argc, argv, "--gguf");
@@ -287,9 +231,7 @@ int main(int argc, char** argv) {
         const double setup_s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
 
         // prompt, one token at a time (logits only for the last one)
-        SplitMix r{seed * 31 + 7};
-        std::vector<int32_t> ids(prompt);
-        for (auto& t : ids) t = (int32_t)(r.next() % (uint64_t)V);
+        const std::vector<int32_t> ids = bench::prompt_ids(seed, prompt, V);
         void *e0 = nullptr, *e1 = nullptr, *e2 = nullptr;
         citlali_hip_event_create(&e0);
         citlali_hip_event_create(&e1);

@@ -3,8 +3,8 @@
 // Same signatures and meaning as the reference's compute layer
 // (include/citlali/compute/cuda/kernels.h:8-61), implemented over the C ABI
 // of libcitlali_hip.so (gfx950 kernels).  Launches are asynchronous on the
-// library stream; failures throw citlali::Error.  `cuda_zero` is named
-// `device_zero` here.
+// library stream; failures throw citlali::Error.  `cuda_zero` keeps its
+// reference name (kernels.h:8); `device_zero` is the same call.
 #pragma once
 
 #include "citlali/compute/common/dtype.h"
@@ -14,6 +14,7 @@
 
 namespace citlali::compute {
 
+void cuda_zero(void* data, std::size_t bytes);   // kernels.h:8, kernels.cu:655-657
 void device_zero(void* data, std::size_t bytes);
 void launch_embed(const uint16_t* embedding, int32_t token_id, uint16_t* out, int hidden);
 void launch_copy(const uint16_t* input, uint16_t* output, int n);

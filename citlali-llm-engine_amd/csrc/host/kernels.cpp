@@ -7,7 +7,8 @@
 
 namespace citlali::compute {
 
-void device_zero(void* data, std::size_t bytes) { CITLALI_HIP_CHECK(citlali_hip_zero(data, bytes)); }
+void cuda_zero(void* data, std::size_t bytes) { CITLALI_HIP_CHECK(citlali_hip_zero(data, bytes)); }
+void device_zero(void* data, std::size_t bytes) { cuda_zero(data, bytes); }
 
 void launch_embed(const uint16_t* embedding, int32_t token_id, uint16_t* out, int hidden) {
     CITLALI_HIP_CHECK(citlali_hip_embed(embedding, token_id, out, hidden));

@@ -137,8 +137,8 @@ void QwenModel::allocate_runtime_buffers() {
     ff_out_ = compute::make_device_half_buffer(hidden);
     logits_ = compute::make_device_buffer(static_cast<size_t>(config_.vocab_size) * sizeof(float));
     // the reference's heads x max_context floats, or more: the attention
-    // split partials of the longest plan (the split count never falls as the
-    // plan length grows), so no step -- a captured one included -- needs the
+    // split partials of every plan up to max_context (each bucket's plan and
+    // max_context's own), so no step -- a captured one included -- needs the
     // library's own workspace
     const size_t reference_scores = static_cast<size_t>(config_.head_count) * max_context_ * sizeof(float);
     scores_ = compute::make_device_buffer(std::max(

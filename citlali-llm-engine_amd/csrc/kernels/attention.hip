@@ -814,6 +814,33 @@ size_t attention_workspace_bytes(const AttnPlan& p, int nseq, int heads, int hea
     return (size_t)nseq * heads * p.n_splits * (head_dim + 4) * sizeof(float);
 }
 
+// The split count is not monotone in the planned length: the chunk is
+// rounded up to whole tiles, so a longer plan can need fewer chunks (32/8
+// heads: 2048 positions plan 32 chunks of 64, 3000 plan 24 of 128).  Every
+// term of the chunk formula is non-decreasing in the length, so within a
+// run of lengths sharing one chunk the count peaks at the run's last length;
+// the walk visits those lengths only, from max_len down (a binary search
+// finds where the next shorter chunk ends), a few dozen plans in all.
+size_t attention_workspace_bound(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks) {
+    int most = 0;
+    for (int len = max_len; len >= 1;) {
+        const AttnPlan p = plan_attention(len, nseq, kv_heads, heads, head_dim, target_blocks);
+        if (p.n_splits > most) most = p.n_splits;
+        int lo = 0, hi = len - 1;   // the longest length with a shorter chunk, 0 if none
+        while (lo < hi) {
+            const int mid = lo + (hi - lo + 1) / 2;
+            if (plan_attention(mid, nseq, kv_heads, heads, head_dim, target_blocks).chunk < p.chunk)
+                lo = mid;
+            else
+                hi = mid - 1;
+        }
+        len = lo;
+    }
+    AttnPlan worst{};
+    worst.n_splits = most;
+    return attention_workspace_bytes(worst, nseq, heads, head_dim);
+}
+
 hipError_t launch_attention(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
     if (a.head_dim == 128) return launch_hd<128>(a, p, s);
     if (a.head_dim == 64) return launch_hd<64>(a, p, s);

@@ -100,6 +100,8 @@ bool attention_supported(int head_dim, int group);
 int attention_plan_length(int length, int max_context);
 AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks);
 size_t attention_workspace_bytes(const AttnPlan& p, int nseq, int heads, int head_dim);
+// Bytes that hold the partials of the plan for every length in [1, max_len].
+size_t attention_workspace_bound(int max_len, int nseq, int kv_heads, int heads, int head_dim, int target_blocks);
 hipError_t launch_attention(const AttnArgs& a, const AttnPlan& p, hipStream_t s);
 
 // ---- embedding / dequant (dequant.hip) ----

@@ -242,6 +242,16 @@ def attention_plan_length(length: int, max_context: int) -> int:
     return int(_lib.load().citlali_hip_attention_plan_length(int(length), int(max_context)))
 
 
+def attention_plan_info(max_positions_bound: int, nseq: int, heads: int, kv_heads: int,
+                        head_dim: int) -> tuple[int, int]:
+    """(chunk, n_splits) of the batched attention plan for this bound."""
+    chunk, n = ctypes.c_int(0), ctypes.c_int(0)
+    _lib.check(_lib.load().citlali_hip_attention_plan_info(int(max_positions_bound), int(nseq), int(heads),
+                                                           int(kv_heads), int(head_dim), ctypes.byref(chunk),
+                                                           ctypes.byref(n)))
+    return chunk.value, n.value
+
+
 def argmax_advance(logits, n: int, state, tokens, capacity: int) -> None:
     """argmax, then tokens[step] = pick, token = pick, position += 1, step += 1
     in the device int32 state {token, position, step, 0}."""

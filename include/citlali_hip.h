@@ -130,8 +130,20 @@ int citlali_hip_attention_batched(const uint16_t* q, const uint16_t* k_cache, co
  * with nseq 1 and this max_positions_bound) equals citlali_hip_attention at
  * every position of the bucket, bit for bit. */
 int citlali_hip_attention_plan_length(int length, int max_context);
+/* Workspace bytes that hold the split-KV partials of the plan for every
+ * bound in [1, max_positions_bound] (no reference counterpart; the
+ * reference's scores buffer is heads*max_context floats): the planned chunk
+ * count is not monotone in the length, so a buffer sized for the longest
+ * length alone can be too small for a shorter bucket.  0 when no length up
+ * to the bound splits. */
 size_t citlali_hip_attention_workspace_bytes(int max_positions_bound, int nseq, int heads, int kv_heads,
                                              int head_dim);
+/* The plan citlali_hip_attention_batched makes for this bound (and
+ * citlali_hip_attention for bound = its plan length): positions per
+ * workgroup and chunks of the longest sequence (no reference counterpart;
+ * for tests and sizing). */
+int citlali_hip_attention_plan_info(int max_positions_bound, int nseq, int heads, int kv_heads, int head_dim,
+                                    int* chunk, int* n_splits);
 int citlali_hip_release_workspace(void);
 
 /* citlali_hip_qk_norm_rope_store (or its _at form) followed by

@@ -363,9 +363,12 @@ void orc_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                    int position, int heads, int kv_heads, int hd, double* out) {
     const int group = heads / kv_heads;
     const int L = position + 1;
-    double* s = (double*)malloc((size_t)L * sizeof(double));
     const double scale = 1.0 / sqrt((double)hd);
+    /* heads are independent and each is summed serially, so the result does
+     * not depend on the thread count */
+    #pragma omp parallel for schedule(dynamic, 1) if ((long long)L * heads >= 65536)
     for (int h = 0; h < heads; ++h) {
+        double* s = (double*)malloc((size_t)L * sizeof(double));
         const int kvh = h / group;
         double mx = -INFINITY;
         for (int t = 0; t < L; ++t) {
@@ -377,14 +380,16 @@ void orc_attention(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
         }
         double den = 0.0;
         for (int t = 0; t < L; ++t) { s[t] = exp(s[t] - mx); den += s[t]; }
-        for (int d = 0; d < hd; ++d) {
-            double acc = 0.0;
-            for (int t = 0; t < L; ++t)
-                acc += s[t] * (double)orc_h2f(vc[((size_t)t * kv_heads + kvh) * hd + d]);
-            out[h * hd + d] = acc / den;
+        /* positions outer, dims inner: each dim's sum runs over t in order */
+        double* acc = (double*)calloc((size_t)hd, sizeof(double));
+        for (int t = 0; t < L; ++t) {
+            const uint16_t* v = vc + ((size_t)t * kv_heads + kvh) * hd;
+            for (int d = 0; d < hd; ++d) acc[d] += s[t] * (double)orc_h2f(v[d]);
         }
+        for (int d = 0; d < hd; ++d) out[h * hd + d] = acc[d] / den;
+        free(acc);
+        free(s);
     }
-    free(s);
 }
 
 /* Float version for the CPU baseline: same algorithm, fp32 scores and

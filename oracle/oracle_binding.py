@@ -173,6 +173,10 @@ class RefLib:
         self.lib.ref_dequant_q6k.argtypes = [_P, c_uint64, c_uint64, _P]
         self.lib.ref_tensor_nbytes.argtypes = [ctypes.c_uint32, c_uint64]
         self.lib.ref_tensor_nbytes.restype = c_uint64
+        self.lib.ref_matvec_dequant_dot.argtypes = [c_int, _P, _P, _P, c_int, c_int, c_int]
+        self.lib.ref_matvec_dequant_dot.restype = None
+        self.lib.ref_matvec_f16_dot.argtypes = [_P, _P, _P, c_int, c_int, c_int]
+        self.lib.ref_matvec_f16_dot.restype = None
 
     @classmethod
     def try_load(cls):
@@ -195,3 +199,15 @@ class RefLib:
         out = np.empty(count, np.uint16)
         getattr(self.lib, f"ref_dequant_{kind}")(_p(blocks), blocks.size, count, _p(out))
         return out
+
+    def matvec_dequant_dot(self, kind: str, w, x, in_f: int, out_f: int, nthreads: int) -> np.ndarray:
+        """CPU baseline (i): the reference's dequant of each row, then an fp32 dot."""
+        y = np.empty(out_f, np.float32)
+        self.lib.ref_matvec_dequant_dot(12 if kind == "q4k" else 14, _p(w), _p(x), _p(y), in_f, out_f, nthreads)
+        return y
+
+    def matvec_f16_dot(self, wf16, x, in_f: int, out_f: int, nthreads: int) -> np.ndarray:
+        """CPU baseline (ii): the fp32 dot over rows dequantised beforehand."""
+        y = np.empty(out_f, np.float32)
+        self.lib.ref_matvec_f16_dot(_p(wf16), _p(x), _p(y), in_f, out_f, nthreads)
+        return y

@@ -168,6 +168,43 @@ def test_workspace_query_is_host_only():
     assert lib.citlali_hip_attention_workspace_bytes(100, 1, 12, 8, 128) == 0
 
 
+def _plan_need(dev, bound, nseq, heads, kv, hd):
+    _, n = dev.attention_plan_info(bound, nseq, heads, kv, hd)
+    return 0 if n <= 1 else nseq * heads * n * (hd + 4) * 4
+
+
+def test_workspace_covers_every_bucket_and_length():
+    """The workspace query bounds the partials of the plan at every length up
+    to its bound -- every power-of-two bucket a decode step plans for, and
+    any max_positions_bound of the batched entry -- although the chunk count
+    is not monotone in the length."""
+    from pycitlali import device as dev
+    # the counterexample of a bound sized by the plan at max_context alone:
+    # 32/8/128 at max_context 3000 plans 24 chunks of 128, its 2048 bucket 32
+    # chunks of 64
+    assert dev.attention_plan_info(3000, 1, 32, 8, 128) == (128, 24)
+    assert dev.attention_plan_info(2048, 1, 32, 8, 128) == (64, 32)
+    assert dev.attention_workspace_bytes(3000, 1, 32, 8, 128) >= 32 * 32 * 132 * 4
+    shapes = [(32, 8, 128), (16, 8, 128), (32, 4, 128), (40, 8, 128), (8, 8, 64), (16, 2, 64), (12, 12, 128)]
+    for heads, kv, hd in shapes:
+        for nseq in (1, 3, 16):
+            prev = 0
+            for m in list(range(1, 5000, 7)) + [8192, 8193, 12000, 32768, 40960, 131072]:
+                ws = dev.attention_workspace_bytes(m, nseq, heads, kv, hd)
+                assert ws >= prev, (heads, kv, hd, nseq, m)   # monotone in the bound
+                prev = ws
+                buckets = {dev.attention_plan_length(L, m) for L in (1, m)}
+                b = 256
+                while b < m:
+                    buckets.add(b)
+                    b *= 2
+                for b in buckets:
+                    assert _plan_need(dev, b, nseq, heads, kv, hd) <= ws, (heads, kv, hd, nseq, m, b)
+                if m <= 4096 and m % 97 == 1:
+                    for L in range(1, m + 1):
+                        assert _plan_need(dev, L, nseq, heads, kv, hd) <= ws, (heads, kv, hd, nseq, m, L)
+
+
 def test_device_array_fails_loudly_without_library(tmp_path, monkeypatch):
     import pycitlali._lib as L
     monkeypatch.setattr(L, "_lib", None)

@@ -64,6 +64,66 @@ def test_attention_matches_oracle(hip, orc, heads, kv_heads, hd, L, max_ctx):
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2 ** -10 + 1e-4)
 
 
+# Plans with more chunks than the merge kernel folds in one pass (32 for
+# head_dim 128, 64 for head_dim 64): its loop over chunk batches runs 2 to 10
+# passes.  (heads, kv_heads, head_dim, L, chunks the plan must make)
+MANY_SPLITS = [
+    (32, 4, 128, 16384, 64),
+    (16, 2, 128, 32768, 128),
+    (8, 1, 128, 300000, 293),
+    (16, 2, 64, 40000, 125),
+]
+
+
+@pytest.mark.parametrize("heads,kv_heads,hd,L,splits", MANY_SPLITS)
+def test_attention_many_splits(hip, orc, heads, kv_heads, hd, L, splits):
+    print(f"[attention many splits] heads={heads} kv={kv_heads} hd={hd} L={L}", flush=True)
+    bound = hip.device.attention_plan_length(L, L)
+    assert hip.device.attention_plan_info(bound, 1, heads, kv_heads, hd)[1] == splits
+    k, v = _cache(hip, 300 + heads, L, kv_heads, hd)
+    q = hip.synth.normal_f16(hip.synth.Rng(L + hd), heads * hd)
+    got = _run(hip, q, k, v, L - 1, L, heads, kv_heads, hd)
+    ref = orc.attention(q, k, v, L - 1, heads, kv_heads, hd)
+    assert np.all(tol_ok(got, ref)), f"max err {np.abs(got - ref).max()}"
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2 ** -10 + 1e-4)
+
+
+def test_config4_batched_at_its_lengths(hip, orc):
+    """BASELINE config 4 at its workload: 16 sequences at 32/8/128 with KV
+    lengths uniform in [4096, 32768] drawn as bench.py draws them
+    (numpy default_rng(4)), one batched launch planned for 32768 positions
+    (64 chunks per sequence, so the merge runs two passes), every sequence
+    against the oracle."""
+    nseq, heads, kv, hd, max_len = 16, 32, 8, 128, 32768
+    lens = np.random.default_rng(4).integers(4096, max_len + 1, nseq)
+    print(f"[attention cfg4] lengths {lens.tolist()}", flush=True)
+    assert hip.device.attention_plan_info(max_len, nseq, heads, kv, hd) == (512, 64)
+    stride = max_len * kv * hd
+    gen = np.random.default_rng(40)
+    k = np.zeros(nseq * stride, np.uint16)
+    v = np.zeros(nseq * stride, np.uint16)
+    for s, L in enumerate(lens):   # positions past a sequence's length stay zero and are never read
+        n = int(L) * kv * hd
+        k[s * stride:s * stride + n] = gen.standard_normal(n, dtype=np.float32).astype(np.float16).view(np.uint16)
+        v[s * stride:s * stride + n] = gen.standard_normal(n, dtype=np.float32).astype(np.float16).view(np.uint16)
+    q = gen.standard_normal(nseq * heads * hd, dtype=np.float32).astype(np.float16).view(np.uint16)
+    pos = (lens - 1).astype(np.int32)
+    ws_bytes = hip.device.attention_workspace_bytes(max_len, nseq, heads, kv, hd)
+    dws = hip.DeviceArray(ws_bytes)
+    dq, dk, dv = (hip.DeviceArray.from_numpy(a) for a in (q, k, v))
+    dpos = hip.DeviceArray.from_numpy(pos)
+    do = hip.DeviceArray(nseq * heads * hd * 2)
+    hip.device.attention_batched(dq, dk, dv, stride, dpos, max_len, nseq, heads, kv, hd, dws, ws_bytes, do)
+    got = do.download(np.uint16).view(np.float16).astype(np.float64).reshape(nseq, heads * hd)
+    for a in (dq, dk, dv, dpos, do, dws):
+        a.close()
+    for s in range(nseq):
+        sl = slice(s * stride, (s + 1) * stride)
+        ref = orc.attention(q[s * heads * hd:(s + 1) * heads * hd], k[sl], v[sl], int(pos[s]), heads, kv, hd)
+        assert np.all(tol_ok(got[s], ref)), f"sequence {s} (L={lens[s]}): max err {np.abs(got[s] - ref).max()}"
+        assert np.all(np.abs(got[s] - ref) <= np.abs(ref) * 2 ** -10 + 1e-4), f"sequence {s} (L={lens[s]})"
+
+
 def test_attention_without_scores_buffer(hip, orc):
     heads, kv, hd, L = 32, 8, 128, 4096
     k, v = _cache(hip, 5, L, kv, hd)

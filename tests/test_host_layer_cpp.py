@@ -9,9 +9,9 @@ import pytest
 BIN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "test_host_layer")
 
 
-def _run(mode, timeout):
+def _run(mode, timeout, *extra):
     assert os.path.exists(BIN), "tests/cpp/test_host_layer is not built: run __graft_entry__.build()"
-    p = subprocess.run([BIN, mode], capture_output=True, text=True, timeout=timeout)
+    p = subprocess.run([BIN, mode, *extra], capture_output=True, text=True, timeout=timeout)
     print(p.stdout)
     assert p.returncode == 0, p.stdout[-2000:] + p.stderr[-2000:]
     assert f"{mode}: " in p.stdout and "checks passed" in p.stdout
@@ -38,3 +38,14 @@ def test_host_layer_model(mode):
     greedy2: the model forms in two halves), decode_greedy's graph replay
     against the forward_token loop (graph), loading from a GGUF file (gguf)."""
     _run(mode, 300)
+
+
+@pytest.mark.gpu
+def test_host_layer_config5_greedy():
+    """BASELINE config 5 at its full shape (the benchmark's synthetic
+    Qwen3-8B: 36 layers with their own weights, vocab 151936): QwenModel's 64
+    greedy tokens after an 8-token prompt equal the oracle's
+    (tests/golden/cfg5_greedy.txt, from tests/golden/make_cfg5_greedy),
+    through the forward_token loop and the graph-replayed decode_greedy."""
+    fixture = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cfg5_greedy.txt")
+    _run("cfg5", 300, fixture)
