@@ -96,6 +96,54 @@ int workspace_for(size_t bytes, float** out) {
 
 constexpr int kAttnTargetBlocks = 256;   // one workgroup per CU
 
+// ---- scratch of the entry point that allocates nothing ----------------------
+// citlali_hip_attention_noalloc keeps its split-KV partials in this array:
+// one copy per GPU, held from the library's first use on that GPU until the
+// process ends.  In host code `scratch` names a host-side stand-in, not
+// device memory; the device address of each GPU's copy comes from
+// hipGetSymbolAddress with that GPU current, and only that address is given
+// to kernels.
+constexpr size_t kScratchBytes = CITLALI_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+void* g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// This device's copy of `scratch` (the current device), resolved once.
+int scratch_for_current_device(void** out) {
+    int dev = 0;
+    HIP_TRY(hipGetDevice(&dev));
+    REQUIRE(dev >= 0 && dev < kMaxDevices, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        REQUIRE(p != nullptr && aligned(p, 256), "scratch: no device address for device %d", dev);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return CITLALI_OK;
+}
+
+// The arguments of a single-sequence decode attention at `position`
+// (citlali_hip_attention and its no-allocation form).
+citlali::hip::AttnArgs scalar_attention_args(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, uint16_t* out,
+                               int position, int heads, int kv_heads, int head_dim) {
+    citlali::hip::AttnArgs a{};
+    a.q = q;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.seq_stride = 0;
+    a.positions = nullptr;
+    a.position = position;
+    a.max_len = position + 1;
+    a.nseq = 1;
+    a.heads = heads;
+    a.kv_heads = kv_heads;
+    a.head_dim = head_dim;
+    a.out = out;
+    return a;
+}
+
 }  // namespace
 
 namespace citlali::hip {
@@ -114,7 +162,8 @@ CITLALI_EXPORT int citlali_hip_abi_version(void) { return CITLALI_HIP_ABI_VERSIO
 CITLALI_EXPORT int citlali_hip_init(int device) {
     REQUIRE(device >= 0, "device index must be non-negative");
     HIP_TRY(hipSetDevice(device));
-    return CITLALI_OK;
+    void* s = nullptr;   // this device's no-allocation scratch, resolved at set-up
+    return scratch_for_current_device(&s);
 }
 
 CITLALI_EXPORT int citlali_hip_device_count(int* count) {
@@ -308,19 +357,7 @@ CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_ca
     if (st) return st;
     REQUIRE(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16), "attention: q and caches must be 16-byte aligned");
 
-    AttnArgs a{};
-    a.q = q;
-    a.k_cache = k_cache;
-    a.v_cache = v_cache;
-    a.seq_stride = 0;
-    a.positions = nullptr;
-    a.position = position;
-    a.max_len = position + 1;
-    a.nseq = 1;
-    a.heads = heads;
-    a.kv_heads = kv_heads;
-    a.head_dim = head_dim;
-    a.out = out;
+    AttnArgs a = scalar_attention_args(q, k_cache, v_cache, out, position, heads, kv_heads, head_dim);
     // planned for the length's bucket, so every step of a bucket launches the
     // same kernels (as a captured step with the position in device memory)
     const AttnPlan p = plan_attention(attention_plan_length(position + 1, max_context), 1, kv_heads, heads, head_dim,
@@ -334,6 +371,35 @@ CITLALI_EXPORT int citlali_hip_attention(const uint16_t* q, const uint16_t* k_ca
     } else {
         st = workspace_for(need, &a.workspace);
         if (st) return st;
+    }
+    HIP_TRY(launch_attention(a, p, g_stream));
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_attention_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                                 uint16_t* out, int position, int max_context, int heads,
+                                                 int kv_heads, int head_dim) {
+    REQUIRE(q && k_cache && v_cache && out, "attention_noalloc received a null buffer");
+    REQUIRE(position >= 0 && position < max_context, "position exceeds max_context");
+    int st = check_attn_shape(heads, kv_heads, head_dim);
+    if (st) return st;
+    REQUIRE(aligned(q, 16) && aligned(k_cache, 16) && aligned(v_cache, 16),
+            "attention_noalloc: q and caches must be 16-byte aligned");
+    AttnArgs a = scalar_attention_args(q, k_cache, v_cache, out, position, heads, kv_heads, head_dim);
+    // the plan of citlali_hip_attention, so the same kernels and results
+    const AttnPlan p = plan_attention(attention_plan_length(position + 1, max_context), 1, kv_heads, heads, head_dim,
+                                      kAttnTargetBlocks);
+    const size_t need = attention_workspace_bytes(p, 1, heads, head_dim);
+    REQUIRE(need <= kScratchBytes,
+            "attention_noalloc: the split partials of %d chunks x %d heads need %zu bytes, more than the %zu-byte "
+            "scratch (CITLALI_NOALLOC_SCRATCH_BYTES)",
+            p.n_splits, heads, need, kScratchBytes);
+    a.workspace = nullptr;
+    if (need > 0) {
+        void* s = nullptr;
+        st = scratch_for_current_device(&s);
+        if (st) return st;
+        a.workspace = static_cast<float*>(s);
     }
     HIP_TRY(launch_attention(a, p, g_stream));
     return CITLALI_OK;

@@ -78,6 +78,7 @@ SIGNATURES = [
     ("citlali_hip_matvec_gate_up_swiglu", c_int, [c_int, _P, _P, _P, _P, c_int, c_int]),
     ("citlali_hip_matvec_group", c_int, [c_int, POINTER(c_int), POINTER(c_void_p), _P, POINTER(c_void_p),
                                          POINTER(c_int), c_int]),
+    ("citlali_hip_attention_noalloc", c_int, [_P, _P, _P, _P, c_int, c_int, c_int, c_int, c_int]),
     ("citlali_hip_attention_plan_length", c_int, [c_int, c_int]),
     ("citlali_hip_attention_plan_info", c_int, [c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
     ("citlali_hip_argmax_advance", c_int, [_P, c_int, _P, _P, c_int]),

@@ -143,6 +143,14 @@ def attention(q, k_cache, v_cache, scores, out, position: int, max_context: int,
               int(heads), int(kv_heads), int(head_dim))
 
 
+def attention_noalloc(q, k_cache, v_cache, out, position: int, max_context: int, heads: int, kv_heads: int,
+                      head_dim: int) -> None:
+    """citlali_hip_attention with the split partials in the library's static
+    per-GPU scratch: allocates nothing."""
+    _lib.call("citlali_hip_attention_noalloc", _vp(q), _vp(k_cache), _vp(v_cache), _vp(out), int(position),
+              int(max_context), int(heads), int(kv_heads), int(head_dim))
+
+
 def attention_workspace_bytes(max_positions_bound: int, nseq: int, heads: int, kv_heads: int, head_dim: int) -> int:
     return int(_lib.load().citlali_hip_attention_workspace_bytes(int(max_positions_bound), int(nseq), int(heads),
                                                                  int(kv_heads), int(head_dim)))

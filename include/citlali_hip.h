@@ -112,6 +112,25 @@ int citlali_hip_embed_q6k(const uint8_t* table, int32_t token_id, uint16_t* out,
 int citlali_hip_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, float* scores,
                           uint16_t* out, int position, int max_context, int heads, int kv_heads, int head_dim);
 
+/* Attention that allocates nothing.  No counterpart in the reference: for
+ * callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments and results as citlali_hip_attention (bit for bit, same
+ * launches) without `scores`: the split-KV partials go to a file-scope
+ * device array of the library, CITLALI_NOALLOC_SCRATCH_BYTES per GPU, whose
+ * device address citlali_hip_init resolves (or the first call on a GPU that
+ * init did not select); the GPU holds it until the process ends.  A plan
+ * whose partials (heads * chunks * (head_dim + 4) * 4 bytes) exceed it --
+ * more than 496 chunks at 64 query heads of head_dim 128; every plan of at
+ * most 32 query heads fits (at most 512 chunks) -- is rejected with
+ * CITLALI_ERR_INVALID before anything launches.  Every call on a GPU shares that GPU's array,
+ * which keeps the last call's partials: calls that overlap on one GPU (from
+ * several streams or threads) race. */
+#define CITLALI_NOALLOC_SCRATCH_BYTES (16u << 20)
+int citlali_hip_attention_noalloc(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                                  uint16_t* out, int position, int max_context, int heads, int kv_heads,
+                                  int head_dim);
+
 /* Many independent sequences in one launch (no reference counterpart: the
  * reference decodes one sequence; per sequence the result equals
  * launch_attention).  q/out [nseq][heads][head_dim]; sequence s uses the
