@@ -37,12 +37,22 @@ public:
         key(k, 8);
         text(kv_, v);
     }
+    void boolean(const std::string& k, bool v) {
+        key(k, 7);
+        put<uint8_t>(kv_, v ? 1 : 0);
+    }
     // tokenizer.ggml.tokens-style array of n placeholder strings
     void strings(const std::string& k, int n) {
         key(k, 9);
         put<uint32_t>(kv_, 8);
         put<uint64_t>(kv_, (uint64_t)n);
         for (int i = 0; i < n; ++i) text(kv_, "t" + std::to_string(i));
+    }
+    void strings(const std::string& k, const std::vector<std::string>& v) {
+        key(k, 9);
+        put<uint32_t>(kv_, 8);
+        put<uint64_t>(kv_, (uint64_t)v.size());
+        for (const std::string& s : v) text(kv_, s);
     }
 
     // Adds a tensor with its own bytes; returns its index.

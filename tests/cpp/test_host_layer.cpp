@@ -21,12 +21,15 @@
 #include "citlali/io/gguf_reader.h"
 #include "citlali/model/linear_backend.h"
 #include "citlali/model/qwen_model.h"
+#include "citlali/runtime/session.h"
+#include "citlali/tokenizer/tokenizer.h"
 #include "citlali_hip.h"
 #include "citlali_oracle.h"
 #include "gguf_out.hpp"
 #include "synth_qwen3.hpp"
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
@@ -927,7 +930,10 @@ void test_config5_greedy(const std::string& fixture) {
 // ---- the synthetic model as a GGUF file ----------------------------------
 // Matrices keep their Q4_K / Q6_K blocks with dims [in, out]; the norm
 // vectors are stored as F32, as Qwen GGUF files store them.
-void write_synth_gguf(const SynthModel& s, const std::string& path) {
+// With `tokenizer`, its tokens, merges, ids and add_bos_token go into the
+// file (the vocabulary size must be the model's); eos >= 0 replaces its EOS id.
+void write_synth_gguf(const SynthModel& s, const std::string& path, const io::GgufFile* tokenizer = nullptr,
+                      int64_t eos = -1) {
     bench::GgufOut o;
     std::vector<std::vector<float>> norms;   // borrowed by `o` until write()
     norms.reserve(1 + 11 * s.layers.size());
@@ -942,7 +948,19 @@ void write_synth_gguf(const SynthModel& s, const std::string& path) {
     const model::QwenConfig& c = s.cfg;
     const std::string a = c.architecture;
     o.str("general.architecture", a);
-    o.strings("tokenizer.ggml.tokens", (int)c.vocab_size);
+    if (tokenizer) {
+        const std::vector<std::string> tokens = tokenizer->get_string_array("tokenizer.ggml.tokens");
+        check(tokens.size() == c.vocab_size, "tokenizer vocabulary size equals the model's");
+        o.strings("tokenizer.ggml.tokens", tokens);
+        o.strings("tokenizer.ggml.merges", tokenizer->get_string_array("tokenizer.ggml.merges"));
+        o.u32("tokenizer.ggml.bos_token_id", (uint32_t)tokenizer->get_u64("tokenizer.ggml.bos_token_id", 151643));
+        o.u32("tokenizer.ggml.eos_token_id",
+              eos >= 0 ? (uint32_t)eos : (uint32_t)tokenizer->get_u64("tokenizer.ggml.eos_token_id", 151645));
+        o.u32("tokenizer.ggml.padding_token_id", (uint32_t)tokenizer->get_u64("tokenizer.ggml.padding_token_id", 151643));
+        o.boolean("tokenizer.ggml.add_bos_token", tokenizer->get_bool("tokenizer.ggml.add_bos_token", false));
+    } else {
+        o.strings("tokenizer.ggml.tokens", (int)c.vocab_size);
+    }
     o.u32(a + ".context_length", c.context_length);
     o.u32(a + ".embedding_length", c.embedding_length);
     o.u32(a + ".block_count", c.block_count);
@@ -1067,6 +1085,191 @@ void test_load_from_gguf(bool biased) {
     check(mismatched == 0, "fp16-path greedy tokens identical");
 }
 
+// ---- InferenceSession over the synthetic model ----------------------------
+// The reference's generation loop (session.cpp:61-104) restated over
+// forward_token, one token at a time: what the session must reproduce with
+// its chunked decode_greedy.
+struct Manual {
+    runtime::GenerationResult r;
+    std::vector<std::string> pieces;
+    std::vector<int32_t> ids;   // every greedy token computed, emitted or not
+};
+Manual manual_generate(model::QwenModel& m, const tokenizer::Tokenizer& t, const std::string& prompt,
+                       uint32_t max_new) {
+    Manual out;
+    const std::vector<int32_t> toks = t.encode(prompt, true);
+    check(!toks.empty() && toks.size() + max_new < m.max_context(), "manual loop: prompt fits");
+    uint32_t pos = 0;
+    int32_t next = 0;
+    for (size_t i = 0; i < toks.size(); ++i) next = m.forward_token(toks[i], pos++, i + 1 == toks.size());
+    for (uint32_t i = 0; i < max_new; ++i) {
+        out.ids.push_back(next);
+        if (next == t.eos_id()) {
+            out.r.stop_reason = runtime::StopReason::Eos;
+            break;
+        }
+        out.pieces.push_back(t.decode_token(next));
+        out.r.text += out.pieces.back();
+        ++out.r.generated_tokens;
+        next = m.forward_token(next, pos++);
+        if (pos >= m.max_context()) {
+            out.r.stop_reason = runtime::StopReason::ContextLimit;
+            break;
+        }
+    }
+    return out;
+}
+
+const char* stop_name(runtime::StopReason r) {
+    return r == runtime::StopReason::Eos ? "eos" : r == runtime::StopReason::MaxNewTokens ? "max_new" : "context";
+}
+
+void check_same(const runtime::GenerationResult& got, const std::vector<std::string>& got_pieces, const Manual& want,
+                const std::string& what) {
+    check(got.text == want.r.text && got.generated_tokens == want.r.generated_tokens &&
+              got.stop_reason == want.r.stop_reason && got_pieces == want.pieces,
+          what + ": session = forward_token loop (" + std::to_string(got.generated_tokens) + " vs " +
+              std::to_string(want.r.generated_tokens) + " tokens, stop " + stop_name(got.stop_reason) + " vs " +
+              stop_name(want.r.stop_reason) + ")");
+}
+
+void test_session(const std::string& tok_path) {
+    io::GgufFile tg;
+    tg.load(tok_path);
+    tokenizer::Tokenizer tok;
+    tok.load_from_gguf(tg);
+    const int vocab = tok.vocab_size(), ctx = 256;
+    SynthModel s = make_model(41, 1024, 8, 4, 2048, 2, vocab);
+    const std::string path = temp_path("session.gguf");
+    write_synth_gguf(s, path, &tg);
+
+    runtime::InferenceSession sess;
+    sess.load_model(path, ctx, /*quantized=*/true);
+    io::GgufFile g;
+    g.load(path);
+    model::QwenModel ref;
+    ref.load(g, ctx, true);
+    check(sess.tokenizer().vocab_size() == vocab && sess.tokenizer().eos_id() == tok.eos_id() &&
+              sess.config().vocab_size == (uint32_t)vocab,
+          "session: tokenizer and config from the GGUF file");
+
+    const std::vector<std::string> prompts = {"The quick brown fox", "人工智能正在改变世界。",
+                                              "<|im_start|>user\nhi<|im_end|>\n<|im_start|>assistant\n", "a"};
+    runtime::GenerationOptions opt;
+    opt.max_new_tokens = 40;
+    const auto distinct = [](std::vector<int32_t> v) {
+        std::sort(v.begin(), v.end());
+        return (size_t)(std::unique(v.begin(), v.end()) - v.begin());
+    };
+    std::vector<int32_t> seen;   // greedy ids of the most varied prompt, for the EOS case
+    std::string eos_prompt;
+    for (const std::string& p : prompts) {
+        const Manual want = manual_generate(ref, tok, p, opt.max_new_tokens);
+        if (distinct(want.ids) > distinct(seen)) {
+            seen = want.ids;
+            eos_prompt = p;
+        }
+        for (uint32_t chunk : {1u, 5u, 16u, 64u}) {
+            sess.set_decode_chunk(chunk);
+            std::vector<std::string> pieces;
+            const runtime::GenerationResult r =
+                sess.generate_once_result(p, opt, [&](const std::string& x) { pieces.push_back(x); });
+            check_same(r, pieces, want, "generate, prompt of " + std::to_string(p.size()) + " bytes, chunk " +
+                                            std::to_string(chunk));
+        }
+        std::printf("  prompt %zu bytes -> %u tokens, stop %s, text %zu bytes: same for chunks 1/5/16/64\n", p.size(),
+                    want.r.generated_tokens, stop_name(want.r.stop_reason), want.r.text.size());
+    }
+    check(sess.generate_once("The quick brown fox", opt) == manual_generate(ref, tok, "The quick brown fox", 40).r.text,
+          "generate_once returns the result's text");
+
+    // EOS: a greedy token of the most varied prompt made the EOS id, the one
+    // whose first appearance is latest (so that the stop falls inside a
+    // chunk when the model varies enough)
+    check(seen.size() >= 8, "the prompt ran 8 steps");
+    int32_t eos = seen[0];
+    size_t first = 0;
+    for (size_t k = 0; k < seen.size(); ++k)
+        if (std::find(seen.begin(), seen.begin() + k, seen[k]) == seen.begin() + k && seen[k] != tok.eos_id()) {
+            eos = seen[k];
+            first = k;
+        }
+    const std::string path_eos = temp_path("session_eos.gguf");
+    write_synth_gguf(s, path_eos, &tg, eos);
+    runtime::InferenceSession se;
+    se.load_model(path_eos, ctx, true);
+    // chunks that end just before, at and after the EOS step, and a long one
+    const uint32_t at = (uint32_t)std::max<size_t>(first, 1);
+    for (uint32_t chunk : {1u, at, at + 1, 16u}) {
+        se.set_decode_chunk(chunk);
+        std::vector<std::string> pieces;
+        const runtime::GenerationResult r =
+            se.generate_once_result(eos_prompt, opt, [&](const std::string& x) { pieces.push_back(x); });
+        check(r.stop_reason == runtime::StopReason::Eos && r.generated_tokens == first &&
+                  pieces.size() == first,
+              "EOS id " + std::to_string(eos) + " stops generation before it, after " + std::to_string(first) +
+                  " tokens (chunk " + std::to_string(chunk) + ")");
+        std::string text;
+        for (size_t i = 0; i < first; ++i) text += tok.decode_token(seen[i]);
+        check(r.text == text, "EOS: text of the tokens before it");
+    }
+    std::printf("  EOS id %d: stops after %zu tokens for chunks 1/%u/%u/16 (%zu distinct ids among %zu)\n", eos,
+                first, at, at + 1, distinct(seen), seen.size());
+    std::remove(path_eos.c_str());
+
+    // chat: the history grows by the user message and the reply
+    sess.set_decode_chunk(16);
+    sess.reset_conversation();
+    std::vector<std::pair<std::string, std::string>> hist;
+    for (const std::string& msg : {std::string("Hello there"), std::string("And again?")}) {
+        hist.emplace_back("user", msg);
+        const Manual want = manual_generate(ref, tok, tok.apply_chat_template(hist, true), 24);
+        opt.max_new_tokens = 24;
+        std::vector<std::string> pieces;
+        const runtime::GenerationResult r =
+            sess.chat_once_result(msg, opt, [&](const std::string& x) { pieces.push_back(x); });
+        check_same(r, pieces, want, "chat turn " + std::to_string(hist.size() / 2 + 1));
+        hist.emplace_back("assistant", want.r.text);
+        check(sess.history() == hist, "chat history holds the user messages and replies");
+    }
+    sess.reset_conversation();
+    check(sess.history().empty(), "reset_conversation clears the history");
+    const std::string fresh = tok.apply_chat_template({{"user", "Hello there"}}, true);
+    check(sess.chat_once("Hello there", opt) == manual_generate(ref, tok, fresh, 24).r.text,
+          "after reset, chat starts from the new message alone");
+
+    // the prompt-length rule: prompt + max_new must stay below max_context
+    const size_t n_prompt = tok.encode(prompts[0], true).size();
+    opt.max_new_tokens = (uint32_t)(ctx - n_prompt);
+    bool threw = false;
+    try {
+        sess.generate_once_result(prompts[0], opt);
+    } catch (const Error& e) {
+        threw = std::string(e.what()).find("prompt plus generation exceeds max_context") != std::string::npos;
+    }
+    check(threw, "prompt + max_new == max_context is refused");
+    opt.max_new_tokens = (uint32_t)(ctx - n_prompt - 1);
+    const Manual want = manual_generate(ref, tok, prompts[0], opt.max_new_tokens);
+    std::vector<std::string> pieces;
+    const runtime::GenerationResult r =
+        sess.generate_once_result(prompts[0], opt, [&](const std::string& x) { pieces.push_back(x); });
+    check_same(r, pieces, want, "generation to the last position");
+    std::printf("  %zu-token prompt + %u new tokens in a %d-position context: same, stop %s\n", n_prompt,
+                opt.max_new_tokens, ctx, stop_name(r.stop_reason));
+
+    // wall time of that generation per decode chunk (not a check)
+    for (uint32_t chunk : {1u, 4u, 16u, 64u}) {
+        sess.set_decode_chunk(chunk);
+        sess.generate_once_result(prompts[0], opt);   // graphs captured
+        const auto t0 = std::chrono::steady_clock::now();
+        const runtime::GenerationResult g = sess.generate_once_result(prompts[0], opt);
+        const double s_ = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        std::printf("  chunk %2u: %u tokens in %.2f ms, %.0f tok/s (prompt included)\n", chunk, g.generated_tokens,
+                    s_ * 1e3, g.generated_tokens / s_);
+    }
+    std::remove(path.c_str());
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -1079,7 +1282,7 @@ int main(int argc, char** argv) {
             test_oracle_forward_pins();
             test_model_load_errors();
         } else if (mode == "gpu" || mode == "greedy" || mode == "greedy2" || mode == "graph" || mode == "gguf" ||
-                   mode == "cfg5") {
+                   mode == "cfg5" || mode == "session") {
             // GPU modes, each a part of a length that one test run prints
             // progress within
             if (citlali_hip_init(0) != CITLALI_OK) {
@@ -1104,6 +1307,9 @@ int main(int argc, char** argv) {
                 test_decode_greedy_graph(4096, 32);
                 test_decode_greedy_graph(4096, 32, /*fp16=*/true);
                 test_long_context_buckets();
+            } else if (mode == "session") {
+                check(argc > 2, "session needs a tokenizer GGUF file");
+                test_session(argv[2]);
             } else if (mode == "cfg5") {
                 check(argc > 2, "cfg5 needs the fixture path");
                 test_config5_greedy(argv[2]);
@@ -1113,7 +1319,7 @@ int main(int argc, char** argv) {
             }
             compute::synchronize();
         } else {
-            std::printf("usage: %s cpu|gpu|greedy|greedy2|graph|gguf|cfg5 FIXTURE\n", argv[0]);
+            std::printf("usage: %s cpu|gpu|greedy|greedy2|graph|gguf|cfg5 FIXTURE|session TOKENIZER_GGUF\n", argv[0]);
             return 2;
         }
     } catch (const std::exception& e) {

@@ -49,3 +49,14 @@ def test_host_layer_config5_greedy():
     through the forward_token loop and the graph-replayed decode_greedy."""
     fixture = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "cfg5_greedy.txt")
     _run("cfg5", 300, fixture)
+
+
+@pytest.mark.gpu
+def test_host_layer_session():
+    """InferenceSession (the reference's session.cpp:61-104) over a synthetic
+    2-layer model whose GGUF file carries the qwen_like tokenizer fixture:
+    text, token count, stop reason and on_token pieces equal the reference's
+    loop restated over forward_token, for decode chunks 1-64; EOS, chat
+    history, reset, and the max_context rule."""
+    tok = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tokenizer", "qwen_like.gguf")
+    _run("session", 300, tok)
