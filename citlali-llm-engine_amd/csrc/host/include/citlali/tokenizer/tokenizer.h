@@ -61,6 +61,8 @@ private:
         int rank = 0;
     };
 
+    // the pieces of a tokenizer that has no vocabulary: every byte as itself
+    static std::vector<std::string> raw_byte_pieces();
     // initial piece for one byte of text
     const std::string& byte_piece(uint8_t byte) const;
     std::vector<std::string> initial_pieces(const std::string& text) const;
@@ -71,8 +73,7 @@ private:
     std::unordered_map<std::string, int32_t> ids_;
     // keyed "left\nright", the form the reference looks pairs up in
     std::unordered_map<std::string, Rule> rules_;
-    std::vector<std::string> byte_pieces_;   // [256], chosen at load
-    std::vector<int> specials_in_vocab_;      // indices into the control-token list
+    std::vector<std::string> byte_pieces_ = raw_byte_pieces();   // [256], chosen at load
 
     int32_t bos_id_ = 151643;
     int32_t eos_id_ = 151645;

@@ -137,6 +137,12 @@ void Tokenizer::load_from_gguf(const io::GgufFile& gguf) {
     chat_template_ = gguf.get_string("tokenizer.chat_template", "");
 }
 
+std::vector<std::string> Tokenizer::raw_byte_pieces() {
+    std::vector<std::string> pieces(256);
+    for (int b = 0; b < 256; ++b) pieces[b] = std::string(1, static_cast<char>(b));
+    return pieces;
+}
+
 const std::string& Tokenizer::byte_piece(uint8_t byte) const {
     return byte_pieces_[byte];
 }

@@ -20,7 +20,8 @@
 //   dec K HEX(decode(encode(text, false)))
 //   chat K HEX(apply_chat_template({("system", text), ("user", text)}, true))
 //   chat0 K HEX(apply_chat_template({("user", text)}, false))
-// reload() is the state left by loading two files into one object.
+// reload() is the state left by loading two files into one object;
+// dump_fresh() the same dump for a tokenizer that never loaded one.
 #pragma once
 
 #include <cstdint>
@@ -68,6 +69,9 @@ inline std::string ids(const std::vector<int32_t>& v) {
     return out;
 }
 
+template <class Tokenizer>
+std::string dump_state(const Tokenizer& t, const std::vector<std::string>& texts);
+
 template <class GgufFile, class Tokenizer>
 std::string dump(const std::string& gguf_path, const std::vector<std::string>& texts) {
     GgufFile g;
@@ -78,6 +82,18 @@ std::string dump(const std::string& gguf_path, const std::vector<std::string>& t
     } catch (const std::exception&) {
         return "load error\n";
     }
+    return dump_state(t, texts);
+}
+
+// A tokenizer that never loaded a file (its defaults, no vocabulary).
+template <class Tokenizer>
+std::string dump_fresh(const std::vector<std::string>& texts) {
+    const Tokenizer t;
+    return dump_state(t, texts);
+}
+
+template <class Tokenizer>
+std::string dump_state(const Tokenizer& t, const std::vector<std::string>& texts) {
     std::string out;
     const int32_t n = t.vocab_size();
     out += "vocab " + std::to_string(n) + " bos " + std::to_string(t.bos_id()) + " eos " +

@@ -8,6 +8,7 @@
 //                                       the vocabulary, print ms and tokens,
 //                                       check decode(encode(text)) == text
 //   test_tokenizer reload A B           tok_dump::reload of A then B
+//   test_tokenizer fresh TEXTS          tok_dump::dump_fresh
 // No GPU.
 #include "citlali/common.h"
 #include "citlali/io/gguf_reader.h"
@@ -55,6 +56,11 @@ int main(int argc, char** argv) {
             citlali::require(t.decode(t.encode(text, false)) == text, "decode(encode(text)) == text");
             return 0;
         }
+        if (mode == "fresh" && argc == 3) {
+            const std::string d = tok_dump::dump_fresh<Tokenizer>(tok_dump::read_texts(argv[2]));
+            std::fwrite(d.data(), 1, d.size(), stdout);
+            return 0;
+        }
         if (mode == "reload" && argc == 4) {
             const std::string d = tok_dump::reload<GgufFile, Tokenizer>(argv[2], argv[3]);
             std::fwrite(d.data(), 1, d.size(), stdout);
@@ -64,6 +70,6 @@ int main(int argc, char** argv) {
         std::fprintf(stderr, "error: %s\n", e.what());
         return 1;
     }
-    std::fprintf(stderr, "usage: test_tokenizer dump TEXTS FILE... | time FILE BYTES | reload A B\n");
+    std::fprintf(stderr, "usage: test_tokenizer dump TEXTS FILE... | time FILE BYTES | reload A B | fresh TEXTS\n");
     return 2;
 }

@@ -3,7 +3,8 @@ tok_cases.py as <case>.gguf, the texts as texts.hex (one hex line each), and
 the reference's own tokenizer's view of them -- src/tokenizer/tokenizer.cpp
 and its GGUF reader compiled from /root/reference into
 oracle/_ref/ref_tok_dump by oracle/Makefile -- as <case>.dump (the canonical
-text of oracle/tok_dump.hpp).
+text of oracle/tok_dump.hpp), and its view of a tokenizer that never loaded
+a file as fresh.dump.
 
     make -C oracle && python tests/golden/make_tok_golden.py
 """
@@ -30,6 +31,9 @@ def main() -> None:
     texts = os.path.join(OUT, "texts.hex")
     with open(texts, "w") as f:
         f.write("".join(t.hex() + "\n" for t in TEXTS))
+    fresh = subprocess.run([REF, "--fresh", texts], capture_output=True, check=True).stdout
+    with open(os.path.join(OUT, "fresh.dump"), "wb") as f:
+        f.write(fresh)
     for name, make in CASES.items():
         path = os.path.join(OUT, name + ".gguf")
         with open(path, "wb") as f:

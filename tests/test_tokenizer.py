@@ -79,6 +79,15 @@ def test_fixture_texts_cover_the_fallbacks():
     assert dump["missing_tokens"] == "load error\n" and dump["empty_tokens"] == "load error\n"
 
 
+def test_tokenizer_that_never_loaded():
+    """Defaults and no vocabulary: every byte is its own piece and the
+    unknown id 0, nothing decodes, the template still applies."""
+    got = subprocess.run([BIN, "fresh", TEXTS], capture_output=True, check=True, timeout=60).stdout
+    with open(os.path.join(GOLD, "fresh.dump"), "rb") as f:
+        want = f.read()
+    assert got == want, first_difference(got, want)
+
+
 def test_reload_keeps_ids_the_second_file_lacks():
     a, b = os.path.join(GOLD, "qwen_like.gguf"), os.path.join(GOLD, "no_merges.gguf")
     got = subprocess.run([BIN, "reload", a, b], capture_output=True, check=True, timeout=60).stdout
