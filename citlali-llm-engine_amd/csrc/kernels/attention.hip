@@ -302,13 +302,22 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
 // head_dim 128, GQA group 2..8: the same chunk / merge structure with both
 // products on the matrix cores (v_mfma_f32_16x16x16f16).  The group's heads
 // are the 16 MFMA columns (padding heads have q = 0 and are never written).
-// Per wave, a tile of 16 positions:
-//  * scores S[pos][head] = K[pos][:] . q[head][:]: K rows go from global
-//    memory straight into the A operand (lane = row `col`, a 64-byte slab
-//    `grp` of it; the 128 dims in 8 steps of 16, dim 32t + 8grp + 4h + j of
-//    step (t, h) being operand k = 4grp + j), q is the B operand in the same
-//    dim order; lane (col, grp) gets the scores of positions 4grp + i for
-//    head col.
+// Per wave, a tile of 16 positions, one tile's loads in flight:
+//  * loads, two forms (kRows, chosen by the plan):
+//    - direct: lane = (row col, 64-byte slab grp), 16 rows x 64 bytes per
+//      instruction, K straight into the A operand, V into an LDS tile; the
+//      refill is issued once the scores are in;
+//    - rows (launches of more than two workgroups per CU, where HBM
+//      saturates): each nontemporal instruction reads four whole 256-byte
+//      rows (lane = row 4u + grp, 16-byte slice col), which a probe of the
+//      same shape reads at ~7 TB/s against ~5.9 for 16 rows x 64 bytes;
+//      K and V go to wave-private LDS rows, the refill is issued at once
+//      and K is read back in the A operand layout.
+//  * scores S[pos][head] = K[pos][:] . q[head][:]: the A operand is K row
+//    `col` (lane = row `col`, a 64-byte slab `grp` of it; the 128
+//    dims in 8 steps of 16, dim 32t + 8grp + 4h + j of step (t, h) being
+//    operand k = 4grp + j), q is the B operand in the same dim order; lane
+//    (col, grp) gets the scores of positions 4grp + i for head col.
 //  * online softmax per head column (max and sum over the 16 lanes' groups),
 //    exponentials in base 2 as the VALU kernel.
 //  * out[head][dim] += P[head][pos] V[pos][dim]: the scores' lane layout is
@@ -319,14 +328,16 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
 // ---------------------------------------------------------------------------
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 constexpr int kMTile = 16;                     // positions per MFMA tile
-constexpr int kMStride = 128 + 8;              // V tile row in LDS (halves)
+constexpr int kMStride = 128 + 8;              // K / V tile row in LDS (halves)
 constexpr size_t kMWaveLds = (size_t)kMTile * kMStride * 2;
 // merge: (max, sum)[NW][8], acc[NW][2 row groups][8 blocks][16 cols][4]
-template <int NW>
+// tiles: per wave a V tile, and with row loads a K tile, kMWaveLds each
+template <int NW, bool kRows>
 struct MfmaLds {
     static constexpr size_t kMlFloats = (size_t)NW * 8 * 2;
     static constexpr size_t kMerge = (kMlFloats + (size_t)NW * 2 * 8 * 16 * 4) * sizeof(float);
-    static constexpr size_t kBytes = kMerge > kMWaveLds * NW ? kMerge : kMWaveLds * NW;
+    static constexpr size_t kTiles = (kRows ? 2 : 1) * kMWaveLds * NW;
+    static constexpr size_t kBytes = kMerge > kTiles ? kMerge : kTiles;
     // with the q/k prologue: q' of up to 8 heads, then per wave k' and v of the step
     static constexpr size_t kQs = kBytes;
     static constexpr size_t kKv = kQs + 8 * 128 * 2;
@@ -348,8 +359,13 @@ __device__ __forceinline__ half4 as_half4(uint32_t lo, uint32_t hi) {
 // stores k' and v into the caches and puts them in place of the cache row it
 // loaded for that position (all lanes that load the row, clamped duplicates
 // included), so nothing reads the row before it is written.
-template <int GP, int kDepth, int NW, bool kPrep>
-__global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
+// Occupancy: left alone, the compiler allocates 160-164 registers per lane
+// (VGPRs + accumulation registers), three waves per SIMD.  The row-load form
+// serves launches of many workgroups per CU and is asked for four waves (it
+// fits in 124-128 VGPRs, no spill); the direct form runs at most two
+// workgroups per CU and keeps the allocation it schedules best with.
+template <int GP, bool kRows, int NW, bool kPrep>
+__global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_cache, const uint16_t* __restrict__ v_cache,
     long long seq_stride, const int32_t* __restrict__ positions, int position, int max_len, int heads,
     int kv_heads, int group, int chunk, float scale_log2, float* __restrict__ part, int n_splits,
@@ -378,9 +394,14 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     const int pos_row = L - 1;
     const bool has_pos = kPrep && p_raw >= 0 && p_raw < max_len && w0 <= pos_row && pos_row < w1;
 
-    uint16_t* vt = reinterpret_cast<uint16_t*>(smem + (size_t)wave * kMWaveLds);
-    const uint16_t* kbase = k_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + 8 * grp;
-    const uint16_t* vbase = v_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + 8 * grp;
+    using Lds = MfmaLds<NW, kRows>;
+    uint16_t* vt = reinterpret_cast<uint16_t*>(smem + (size_t)wave * (kRows ? 2 : 1) * kMWaveLds);
+    uint16_t* kt = vt + kMTile * kMStride;   // row loads only
+    // direct: lane = (row col, 64-byte slab grp); rows: lane = (row 4u + grp,
+    // 16-byte slice col of the kv head's 256-byte row)
+    const int lane_off = kRows ? 8 * col : 8 * grp;
+    const uint16_t* kbase = k_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + lane_off;
+    const uint16_t* vbase = v_cache + (size_t)seq * seq_stride + (size_t)kvh * HD + lane_off;
     const size_t row_step = (size_t)kv_heads * HD;
 
     // q of head `col` (zero past the group) as B operands, dims 32t + 8grp + 4h
@@ -423,41 +444,75 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     for (int b = 0; b < 8; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;   // head col
 
-    // kDepth tiles of K and V rows in flight; branch-free (rows past the
-    // range re-read row w1 - 1, in bounds also for an empty range)
-    u32x4 kr[kDepth][4], vr[kDepth][4];
-    auto load_tile = [&](int d, int t0) {
-        const size_t pos = (size_t)min(t0 + col, w1 - 1);
+    // One tile of K and V rows in flight; branch-free (rows past the range
+    // re-read row w1 - 1, in bounds also for an empty range).  Slot u of a
+    // lane: direct, row t0 + col, dims 32u + 8grp .. + 7; rows, row
+    // t0 + 4u + grp, dims 8col .. + 7.
+    u32x4 kr[4], vr[4];
+    auto load_tile = [&](int t0) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            kr[d][t] = *reinterpret_cast<const u32x4*>(kbase + pos * row_step + 32 * t);
-            vr[d][t] = *reinterpret_cast<const u32x4*>(vbase + pos * row_step + 32 * t);
+        for (int u = 0; u < 4; ++u) {
+            if constexpr (kRows) {
+                const size_t pos = (size_t)min(t0 + 4 * u + grp, w1 - 1);
+                kr[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(kbase + pos * row_step));
+                vr[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(vbase + pos * row_step));
+            } else {
+                const size_t pos = (size_t)min(t0 + col, w1 - 1);
+                kr[u] = *reinterpret_cast<const u32x4*>(kbase + pos * row_step + 32 * u);
+                vr[u] = *reinterpret_cast<const u32x4*>(vbase + pos * row_step + 32 * u);
+            }
         }
     };
 
-    const uint16_t* kv_new = reinterpret_cast<const uint16_t*>(smem + MfmaLds<NW>::kKv) + (size_t)wave * 2 * HD;
-    auto process = [&](int d, int t0) {
+    const uint16_t* kv_new = reinterpret_cast<const uint16_t*>(smem + Lds::kKv) + (size_t)wave * 2 * HD;
+    auto process = [&](int t0) {
         if constexpr (kPrep) {
-            if (has_pos && min(t0 + col, w1 - 1) == pos_row) {
+            // the step's row comes from the prologue's k' and v in LDS
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    kr[d][t] = *reinterpret_cast<const u32x4*>(kv_new + 32 * t + 8 * grp);
-                    vr[d][t] = *reinterpret_cast<const u32x4*>(kv_new + HD + 32 * t + 8 * grp);
+            for (int u = 0; u < 4; ++u) {
+                const int row = kRows ? t0 + 4 * u + grp : t0 + col;
+                if (has_pos && min(row, w1 - 1) == pos_row) {
+                    const int dim = kRows ? 8 * col : 32 * u + 8 * grp;
+                    kr[u] = *reinterpret_cast<const u32x4*>(kv_new + dim);
+                    vr[u] = *reinterpret_cast<const u32x4*>(kv_new + HD + dim);
                 }
             }
         }
-#pragma unroll
-        for (int t = 0; t < 4; ++t) *reinterpret_cast<u32x4*>(vt + col * kMStride + 32 * t + 8 * grp) = vr[d][t];
         f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+        if constexpr (kRows) {
+            // both tiles into LDS rows; the slot is then free: refill it with
+            // the next tile, in flight over this tile's whole computation
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            s = mfma16(as_half4(kr[d][t].x, kr[d][t].y), qb[t][0], s);
-            s = mfma16(as_half4(kr[d][t].z, kr[d][t].w), qb[t][1], s);
+            for (int u = 0; u < 4; ++u) {
+                *reinterpret_cast<u32x4*>(vt + (4 * u + grp) * kMStride + 8 * col) = vr[u];
+                *reinterpret_cast<u32x4*>(kt + (4 * u + grp) * kMStride + 8 * col) = kr[u];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            load_tile(t0 + kMTile);
+            __builtin_amdgcn_sched_barrier(0);
+            wave_lds_sync();   // the K and V rows stored above
+            // K row col, dims 32t + 8grp .. + 7: the A operand layout
+            u32x4 kk[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) kk[t] = *reinterpret_cast<const u32x4*>(kt + col * kMStride + 32 * t + 8 * grp);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                s = mfma16(as_half4(kk[t].x, kk[t].y), qb[t][0], s);
+                s = mfma16(as_half4(kk[t].z, kk[t].w), qb[t][1], s);
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) *reinterpret_cast<u32x4*>(vt + col * kMStride + 32 * t + 8 * grp) = vr[t];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                s = mfma16(as_half4(kr[t].x, kr[t].y), qb[t][0], s);
+                s = mfma16(as_half4(kr[t].z, kr[t].w), qb[t][1], s);
+            }
+            // the slot is consumed: refill it with the next tile (the address
+            // waits for the scores, so the load is issued after them)
+            load_tile(issue_after(t0 + kMTile, s[0], s[3]));
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // the slot is consumed: refill it with the tile kDepth ahead (the
-        // address waits for the scores, so the load is issued after them)
-        load_tile(d, issue_after(t0 + kDepth * kMTile, s[0], s[3]));
-        __builtin_amdgcn_sched_barrier(0);
 
         float sv[4];
 #pragma unroll
@@ -490,7 +545,7 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
             ph[j] = h;
             pl[j] = (_Float16)(pv[j] - (float)h);
         }
-        wave_lds_sync();   // the V rows stored above
+        if constexpr (!kRows) wave_lds_sync();   // the V rows stored above
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             uint32_t w[4][2];   // rows 4grp + j, dims 64c + 4col .. + 3
@@ -513,13 +568,10 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
     };
 
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int d = 0; d < kDepth; ++d) {
-        load_tile(d, w0 + d * kMTile);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    load_tile(w0);
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (kPrep) {
-        uint16_t* qs = reinterpret_cast<uint16_t*>(smem + MfmaLds<NW>::kQs);   // [GP][HD]
+        uint16_t* qs = reinterpret_cast<uint16_t*>(smem + Lds::kQs);   // [GP][HD]
 #pragma unroll
         for (int j = 0; j < kHeadsPerWave; ++j) {
             const int h = wave + j * NW;
@@ -553,7 +605,7 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
             prep.k_cache[row + 64 + lane] = r1;
             prep.v_cache[row + lane] = pv[0];
             prep.v_cache[row + 64 + lane] = pv[1];
-            uint16_t* kvw = reinterpret_cast<uint16_t*>(smem + MfmaLds<NW>::kKv) + (size_t)wave * 2 * HD;
+            uint16_t* kvw = reinterpret_cast<uint16_t*>(smem + Lds::kKv) + (size_t)wave * 2 * HD;
             kvw[lane] = r0;
             kvw[64 + lane] = r1;
             kvw[HD + lane] = pv[0];
@@ -576,15 +628,12 @@ __global__ __launch_bounds__(NW * kWave) void attn_mfma_kernel(
             qb[t][1] = as_half4(q_raw[t].z & keep, q_raw[t].w & keep);
         }
     }
-    for (int t0 = w0; t0 < w1; t0 += kDepth * kMTile) {
-#pragma unroll
-        for (int d = 0; d < kDepth; ++d) process(d, t0 + d * kMTile);
-    }
+    for (int t0 = w0; t0 < w1; t0 += kMTile) process(t0);
 
     // ---- merge the waves in LDS ----
     __syncthreads();   // every wave is done with its V tile
     float* ml = reinterpret_cast<float*>(smem);   // [NW][8] (max, sum)
-    float* ms = ml + MfmaLds<NW>::kMlFloats;      // [NW][2][8][16][4]
+    float* ms = ml + Lds::kMlFloats;              // [NW][2][8][16][4]
     if (grp == 0 && col < GP) {
         ml[(wave * 8 + col) * 2] = m_run;
         ml[(wave * 8 + col) * 2 + 1] = l_run;
@@ -717,18 +766,18 @@ hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream
     return hipGetLastError();
 }
 
-template <int GP, int kDepth, int NW = kWaves>
+template <int GP, bool kRows, int NW = kWaves>
 hipError_t launch_mfma(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
     const float scale_log2 = (float)(1.4426950408889634 / sqrt(128.0));
     const dim3 grid(p.n_splits, a.kv_heads, a.nseq);
     if (a.prep != nullptr) {
-        launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth, NW, true>), grid, dim3(NW * kWave),
-                              MfmaLds<NW>::kPrepBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
+        launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kRows, NW, true>), grid, dim3(NW * kWave),
+                              MfmaLds<NW, kRows>::kPrepBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
                               a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
                               a.workspace, p.n_splits, a.out, *a.prep);
     } else {
-        launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kDepth, NW, false>), grid, dim3(NW * kWave),
-                              MfmaLds<NW>::kBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
+        launch_kernel_in_call(p.n_splits <= 1, (attn_mfma_kernel<GP, kRows, NW, false>), grid, dim3(NW * kWave),
+                              MfmaLds<NW, kRows>::kBytes, stream, a.q, a.k_cache, a.v_cache, a.seq_stride, a.positions,
                               a.position, a.max_len, a.heads, a.kv_heads, a.heads / a.kv_heads, p.chunk, scale_log2,
                               a.workspace, p.n_splits, a.out, QkPrep{});
     }
@@ -742,11 +791,9 @@ hipError_t launch_mfma(const AttnArgs& a, const AttnPlan& p, hipStream_t stream)
 template <int HD, int GP>
 hipError_t launch_depth(const AttnArgs& a, const AttnPlan& p, hipStream_t s) {
     if constexpr (HD == 128 && GP >= 2) {
-        switch (p.depth) {
-            case 1: return launch_mfma<GP, 1>(a, p, s);
-            case 2: return launch_mfma<GP, 2>(a, p, s);
-            default: return hipErrorInvalidValue;
-        }
+        // one tile in flight per wave; the plan picks the load form
+        if (p.depth != 1) return hipErrorInvalidValue;
+        return p.rows ? launch_mfma<GP, true>(a, p, s) : launch_mfma<GP, false>(a, p, s);
     }
     if (a.prep != nullptr) return hipErrorInvalidValue;   // the q/k prologue exists only in the MFMA kernel
     switch (p.depth) {
@@ -806,6 +853,10 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     // one tile in flight per wave: deeper rings measured no faster on
     // gfx950 (the per-tile work, not the load latency, bounds a wave)
     p.depth = 1;
+    // whole-row loads once the launch holds more than two workgroups per CU
+    // (HBM saturates; measured at config 4: 251 against 298-308 us), direct
+    // loads below (latency-bound launches: 0.1-0.2 us faster)
+    p.rows = mfma && units * p.n_splits > 2LL * target_blocks;
     return p;
 }
 

@@ -92,7 +92,8 @@ struct AttnPlan {
     int gp;        // padded GQA group (1, 2, 4, 8)
     int chunk;     // positions per workgroup
     int n_splits;  // chunks of the longest sequence
-    int depth;     // K/V tiles in flight per wave (1 or 2)
+    int depth;     // K/V tiles in flight per wave (1 or 2; the matrix-core kernel takes 1)
+    bool rows;     // matrix-core kernel: whole-row nontemporal tile loads through LDS
 };
 bool attention_supported(int head_dim, int group);
 // The length a decode step's attention is planned for: the smallest power
