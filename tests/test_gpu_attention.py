@@ -189,6 +189,38 @@ def test_batched_matches_single_sequence_calls(hip, orc):
         assert np.all(np.abs(single - got[s]) <= np.abs(ref) * 2 ** -10 + 1e-4)
 
 
+@pytest.mark.parametrize("heads,kv,nseq", [(16, 8, 16), (64, 8, 16), (32, 4, 32)])
+def test_batched_row_loads_each_group(hip, orc, heads, kv, nseq):
+    """Launches of more than 512 workgroups read K and V as whole rows
+    through LDS (the planned load form for saturating launches); GQA groups
+    2, 8 and 8-of-4 through that form against the oracle, lengths up to
+    3000 with the extremes 1 and 3000."""
+    hd, max_ctx = 128, 3000
+    chunk, splits = hip.device.attention_plan_info(max_ctx, nseq, heads, kv, hd)
+    assert nseq * kv * splits > 512, "the case must plan the row-load form"
+    rng = hip.synth.Rng(77 + heads + nseq)
+    lens = (rng.u64(nseq) % np.uint64(max_ctx)).astype(np.int64) + 1
+    lens[0], lens[1] = 1, max_ctx
+    stride = max_ctx * kv * hd
+    k = hip.synth.normal_f16(rng, nseq * stride)
+    v = hip.synth.normal_f16(rng, nseq * stride)
+    q = hip.synth.normal_f16(rng, nseq * heads * hd)
+    pos = (lens - 1).astype(np.int32)
+    ws_bytes = hip.device.attention_workspace_bytes(max_ctx, nseq, heads, kv, hd)
+    dws = hip.DeviceArray(max(ws_bytes, 16))
+    dq, dk, dv = (hip.DeviceArray.from_numpy(a) for a in (q, k, v))
+    dpos = hip.DeviceArray.from_numpy(pos)
+    do = hip.DeviceArray(nseq * heads * hd * 2)
+    hip.device.attention_batched(dq, dk, dv, stride, dpos, max_ctx, nseq, heads, kv, hd, dws, ws_bytes, do)
+    got = do.download(np.uint16).view(np.float16).astype(np.float64).reshape(nseq, heads * hd)
+    for a in (dq, dk, dv, dpos, do, dws):
+        a.close()
+    for s in range(nseq):
+        sl = slice(s * stride, (s + 1) * stride)
+        ref = orc.attention(q[s * heads * hd:(s + 1) * heads * hd], k[sl], v[sl], int(pos[s]), heads, kv, hd)
+        assert np.all(tol_ok(got[s], ref)), f"sequence {s} (L={lens[s]}): max err {np.abs(got[s] - ref).max()}"
+
+
 def test_batched_rejects_small_workspace(hip):
     heads, kv, hd, nseq, max_ctx = 32, 8, 128, 4, 4096
     need = hip.device.attention_workspace_bytes(max_ctx, nseq, heads, kv, hd)
