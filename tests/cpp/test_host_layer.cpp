@@ -1133,7 +1133,7 @@ void check_same(const runtime::GenerationResult& got, const std::vector<std::str
               stop_name(want.r.stop_reason) + ")");
 }
 
-void test_session(const std::string& tok_path) {
+void test_session(const std::string& tok_path, bool quantized) {
     io::GgufFile tg;
     tg.load(tok_path);
     tokenizer::Tokenizer tok;
@@ -1144,11 +1144,11 @@ void test_session(const std::string& tok_path) {
     write_synth_gguf(s, path, &tg);
 
     runtime::InferenceSession sess;
-    sess.load_model(path, ctx, /*quantized=*/true);
+    sess.load_model(path, ctx, quantized);
     io::GgufFile g;
     g.load(path);
     model::QwenModel ref;
-    ref.load(g, ctx, true);
+    ref.load(g, ctx, quantized);
     check(sess.tokenizer().vocab_size() == vocab && sess.tokenizer().eos_id() == tok.eos_id() &&
               sess.config().vocab_size == (uint32_t)vocab,
           "session: tokenizer and config from the GGUF file");
@@ -1197,7 +1197,7 @@ void test_session(const std::string& tok_path) {
     const std::string path_eos = temp_path("session_eos.gguf");
     write_synth_gguf(s, path_eos, &tg, eos);
     runtime::InferenceSession se;
-    se.load_model(path_eos, ctx, true);
+    se.load_model(path_eos, ctx, quantized);
     // chunks that end just before, at and after the EOS step, and a long one
     const uint32_t at = (uint32_t)std::max<size_t>(first, 1);
     for (uint32_t chunk : {1u, at, at + 1, 16u}) {
@@ -1309,7 +1309,10 @@ int main(int argc, char** argv) {
                 test_long_context_buckets();
             } else if (mode == "session") {
                 check(argc > 2, "session needs a tokenizer GGUF file");
-                test_session(argv[2]);
+                std::printf("KeepQuantized weights:\n");
+                test_session(argv[2], true);
+                std::printf("DequantizeToFp16 weights:\n");
+                test_session(argv[2], false);
             } else if (mode == "cfg5") {
                 check(argc > 2, "cfg5 needs the fixture path");
                 test_config5_greedy(argv[2]);

@@ -57,6 +57,7 @@ def test_host_layer_session():
     2-layer model whose GGUF file carries the qwen_like tokenizer fixture:
     text, token count, stop reason and on_token pieces equal the reference's
     loop restated over forward_token, for decode chunks 1-64; EOS, chat
-    history, reset, and the max_context rule."""
+    history, reset, and the max_context rule; with KeepQuantized and with
+    DequantizeToFp16 weights."""
     tok = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "tokenizer", "qwen_like.gguf")
     _run("session", 300, tok)
