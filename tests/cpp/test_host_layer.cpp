@@ -1270,6 +1270,33 @@ void test_session(const std::string& tok_path, bool quantized) {
     std::remove(path.c_str());
 }
 
+// The session test's model (2 layers, hidden 1024, the tokenizer of
+// `tok_path`) written to `path`, for the command-line tests.
+void write_session_model(const std::string& tok_path, const std::string& path) {
+    io::GgufFile tg;
+    tg.load(tok_path);
+    const int vocab = (int)tg.get_string_array("tokenizer.ggml.tokens").size();
+    write_synth_gguf(make_model(41, 1024, 8, 4, 2048, 2, vocab), path, &tg);
+    std::printf("wrote %s (vocab %d)\n", path.c_str(), vocab);
+}
+
+// One InferenceSession generation, printed as "tokens N stop S text HEX".
+void session_text(const std::string& model, const std::string& prompt, uint32_t max_new, bool chat, bool quantized) {
+    runtime::InferenceSession sess;
+    sess.load_model(model, 256, quantized);
+    runtime::GenerationOptions opt;
+    opt.max_new_tokens = max_new;
+    const runtime::GenerationResult r =
+        chat ? sess.chat_once_result(prompt, opt) : sess.generate_once_result(prompt, opt);
+    std::string hex;
+    for (unsigned char c : r.text) {
+        char b[4];
+        std::snprintf(b, sizeof b, "%02x", c);
+        hex += b;
+    }
+    std::printf("tokens %u stop %s text %s\n", r.generated_tokens, stop_name(r.stop_reason), hex.c_str());
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
@@ -1281,6 +1308,17 @@ int main(int argc, char** argv) {
             test_dispatch_errors();
             test_oracle_forward_pins();
             test_model_load_errors();
+        } else if (mode == "write_session_model") {
+            check(argc > 3, "write_session_model TOKENIZER_GGUF OUT");
+            write_session_model(argv[2], argv[3]);
+        } else if (mode == "session_text") {
+            check(argc > 6, "session_text MODEL PROMPT MAX_NEW CHAT QUANTIZED");
+            if (citlali_hip_init(0) != CITLALI_OK) {
+                std::printf("FAIL: no GPU: %s\n", citlali_hip_last_error());
+                return 1;
+            }
+            session_text(argv[2], argv[3], (uint32_t)std::atoi(argv[4]), std::atoi(argv[5]) != 0,
+                         std::atoi(argv[6]) != 0);
         } else if (mode == "gpu" || mode == "greedy" || mode == "greedy2" || mode == "graph" || mode == "gguf" ||
                    mode == "cfg5" || mode == "session") {
             // GPU modes, each a part of a length that one test run prints
@@ -1322,7 +1360,9 @@ int main(int argc, char** argv) {
             }
             compute::synchronize();
         } else {
-            std::printf("usage: %s cpu|gpu|greedy|greedy2|graph|gguf|cfg5 FIXTURE|session TOKENIZER_GGUF\n", argv[0]);
+            std::printf("usage: %s cpu|gpu|greedy|greedy2|graph|gguf|cfg5 FIXTURE|session TOKENIZER_GGUF|\n"
+                        "       write_session_model TOKENIZER_GGUF OUT|session_text MODEL PROMPT MAX_NEW CHAT QUANTIZED\n",
+                        argv[0]);
             return 2;
         }
     } catch (const std::exception& e) {
