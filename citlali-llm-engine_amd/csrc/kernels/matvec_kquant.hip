@@ -22,6 +22,7 @@
 //    sum(x) over each group; the block computes those sums while staging x.
 //  * No MFMA: M = 1 is not a dense contraction.  The bound is HBM.
 #include <algorithm>
+#include <type_traits>
 
 #include "device_common.hpp"
 #include "launch.hpp"
@@ -423,11 +424,11 @@ struct RowSet {
 // the current one (a ring of D register slots, indices fixed at compile time
 // by unrolling M rows).  x is loaded before the first fragments and staged
 // in LDS behind them.  Loads are branch-free (rows past the end re-read the
-// last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave
-// computes its M rows (all loaded up front) and stops; the grid then has
-// M * W >= rows.  NB (an even block count that is not a multiple of 16,
-// S = ceil(NB / 16)): rows ending in a partial wave step; in that step the
-// lanes of blocks NB.. load block NB - 1 (in bounds) and add nothing.
+// last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave computes its M rows
+// (all loaded up front) and stops; the grid then has M * W >= rows.  NB (an
+// even block count that is not a multiple of 16, S = ceil(NB / 16)): rows
+// ending in a partial wave step; in that step the lanes of blocks NB.. load
+// block NB - 1 (in bounds) and add nothing.
 template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false, int NB = 0>
 __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __restrict__ x, int K, uint8_t* smem,
                                             int gw, int W, const NormIn& nrm) {
@@ -537,79 +538,113 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_group_kernel(Row
 // does (same lane mapping and summation order), rounds both to fp16 where
 // the separate GEMVs store, and writes act[r] = fp16(silu(g) * u) with the
 // swiglu_kernel expression -- the separate launches' results bit for bit.
-template <class QT, int S, int M, bool kNorm = false, int NB = 0>
-__global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_gate_up_kernel(const uint8_t* __restrict__ wg,
-                                                                const uint8_t* __restrict__ wu,
-                                                                const uint16_t* __restrict__ x,
-                                                                uint16_t* __restrict__ act, int K, int N, NormIn nrm) {
+//
+// Rows are handed out at run time.  One workgroup of eight waves per CU
+// (two per SIMD) owns a contiguous range of rows; a wave starts on row
+// `wave` of the range and takes each further row from an LDS counter when it
+// starts the dots of its current one, so the refill goes out as soon as a
+// slot is consumed.  A wave whose loads come back earlier computes more rows.
+// With two four-wave workgroups per CU and rows fixed in advance, the
+// workgroup dispatched second had its loads served after the first one's
+// and finished about 2 us later at config 3, the CU running on half its
+// waves meanwhile.  Waves 0-3 stage x (the 256-thread order of the other
+// GEMVs and of the norm prologue); waves 4-7 only pass the same barriers.
+constexpr int kGateUpWaves = 8;
+constexpr int kGateUpBlock = kGateUpWaves * kWave;
+
+template <class QT, int S, bool kNorm = false, int NB = 0>
+__global__ __launch_bounds__(kGateUpBlock, 2) void matvec_gate_up_kernel(const uint8_t* __restrict__ wg,
+                                                                         const uint8_t* __restrict__ wu,
+                                                                         const uint16_t* __restrict__ x,
+                                                                         uint16_t* __restrict__ act, int K, int N,
+                                                                         NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
+    static_assert(NB == 0 || (NB % 2 == 0 && (NB + QT::kSbPerStep - 1) / QT::kSbPerStep == S), "partial last step");
+    constexpr int nb = NB ? NB : S * QT::kSbPerStep;
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
+    // the row counter follows the x tables and the 4 floats of norm scratch
+    int* next = reinterpret_cast<int*>(smem + (size_t)nb * kQK * 2 + (size_t)nb * QT::kSxPerBlock * sizeof(float) +
+                                       4 * sizeof(float));
 
-    static_assert(NB == 0 || (NB % 2 == 0 && (NB + QT::kSbPerStep - 1) / QT::kSbPerStep == S), "partial last step");
     const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
     const int l4 = lane % QT::kLanesPerSb;
-    constexpr int nb = NB ? NB : S * QT::kSbPerStep;
     const int sub = lane / QT::kLanesPerSb;
     auto blk = [&](int t) { return NB ? min(t * QT::kSbPerStep + sub, nb - 1) : t * QT::kSbPerStep + sub; };
     auto live = [&](int t) { return NB == 0 || t * QT::kSbPerStep + sub < nb; };
-    constexpr int D = S * M;
-    const int W = gridDim.x * kWavesPerBlock;
-    const int gw = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+    const int span = (N + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int r0 = (int)blockIdx.x * span;
+    const int nrows = max(0, min(span, N - r0));
 
     auto frag_at = [&](const uint8_t* w, int row, int t) {
         const size_t f = (size_t)min(row, N - 1) * nb + blk(t);
         return QT::load(w + f * QT::kBytes, l4);
     };
 
+    if (threadIdx.x == 0) *next = kGateUpWaves;   // read only after the x barrier
     XStage<QT::kSumLayout, nb * 32, kNorm> xs;   // K = 256 nb
-    xs.load(x, nrm);
+    if (wave < kWavesPerBlock) xs.load(x, nrm);
     __builtin_amdgcn_sched_barrier(0);
-    typename QT::Frag fg[D], fu[D];
+    int k = wave;   // this wave's row r0 + k
+    typename QT::Frag fg[S], fu[S];
 #pragma unroll
-    for (int m = 0; m < M; ++m)
-#pragma unroll
-        for (int t = 0; t < S; ++t) {
-            fg[m * S + t] = frag_at(wg, gw + m * W, t);
-            fu[m * S + t] = frag_at(wu, gw + m * W, t);
-            __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
-        }
-    xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
+    for (int t = 0; t < S; ++t) {
+        fg[t] = frag_at(wg, r0 + k, t);
+        fu[t] = frag_at(wu, r0 + k, t);
+        __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
+    }
+    if (wave < kWavesPerBlock) {
+        xs.store(xp, sx, sx + nb * QT::kSxPerBlock, nrm);
+    } else {
+        if constexpr (kNorm) lds_barrier();   // norm_block_sum's
+        lds_barrier();                        // the staging barrier
+    }
     static_assert(S <= QT::kHoistSteps, "gate/up holds x in registers");
     typename QT::XRegs xr[S];   // this lane's x, the same for every row
 #pragma unroll
     for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, blk(t));
 
-    for (int row = gw; row < N; row += M * W) {
+    while (k < nrows) {   // wave-uniform
+        int kn = 0;
+        if (lane == 0) kn = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        kn = __builtin_amdgcn_readfirstlane(kn);
+        const bool more = kn < nrows;
+        const int r = r0 + k;
+        // Each slot is reloaded with the next row once its dots have read it
+        // (issue_after), in slot order.  A one-step row (S = 1) reloads after
+        // both dots and skips the reload on its last row; longer rows reload
+        // unconditionally (their last row re-reads itself), since a branch
+        // there let the compiler move every reload behind the last dot.
+        const int rn = more ? r0 + kn : r;
+        float ag = 0.f, au = 0.f;
 #pragma unroll
-        for (int m = 0; m < M; ++m) {
-            const int r = row + m * W;
-            float ag = 0.f, au = 0.f;
-#pragma unroll
-            for (int t = 0; t < S; ++t) {
-                float cg = QT::dot(fg[m * S + t], l4, xr[t]);
-                float cu = QT::dot(fu[m * S + t], l4, xr[t]);
-                if (NB != 0 && t == S - 1) {
-                    cg = live(t) ? cg : 0.f;
-                    cu = live(t) ? cu : 0.f;
-                }
-                ag += cg;
-                au += cu;
-                const int nr = issue_after(r + M * W, cg, cu);   // refill after the dots, in slot order
-                fg[m * S + t] = frag_at(wg, nr, t);
-                fu[m * S + t] = frag_at(wu, nr, t);
-                __builtin_amdgcn_sched_barrier(0);
+        for (int t = 0; t < S; ++t) {
+            float cg = QT::dot(fg[t], l4, xr[t]);
+            float cu = QT::dot(fu[t], l4, xr[t]);
+            if (NB != 0 && t == S - 1) {
+                cg = live(t) ? cg : 0.f;
+                cu = live(t) ? cu : 0.f;
             }
-            ag = wave_sum(ag);
-            au = wave_sum(au);
-            // computed in every lane, so the branch holds only the store (a
-            // longer branch region keeps the fragment registers from being
-            // reused across iterations: the loop edge then copies them and
-            // waits for every refill)
-            const float g = h2f(f2h_rne(ag)), u = h2f(f2h_rne(au));
-            const uint16_t a = f2h_rne(g / (1.0f + expf(-g)) * u);
-            if (lane == 0 && r < N) act[r] = a;
+            ag += cg;
+            au += cu;
+            if (S > 1 || more) {
+                const int nr = issue_after(rn, cg, cu);
+                fg[t] = frag_at(wg, nr, t);
+                fu[t] = frag_at(wu, nr, t);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
+        ag = wave_sum(ag);
+        au = wave_sum(au);
+        // computed in every lane, so the branch holds only the store (a
+        // longer branch region keeps the fragment registers from being
+        // reused across rows: the loop edge then copies them and waits for
+        // every refill)
+        const float g = h2f(f2h_rne(ag)), u = h2f(f2h_rne(au));
+        const uint16_t a = f2h_rne(g / (1.0f + expf(-g)) * u);
+        if (lane == 0) act[r] = a;
+        k = kn;
     }
 }
 
@@ -676,19 +711,24 @@ int device_cus() {
     return cus;
 }
 
-// Two workgroups per CU, never more waves than rows.
-int stream_grid(int rows) {
-    const int grid = 2 * device_cus();
+// `per_cu` workgroups per CU (two: two waves per SIMD), never more waves than
+// rows.
+int stream_grid(int rows, int per_cu = 2) {
+    const int grid = per_cu * device_cus();
     const int need = (rows + kWavesPerBlock - 1) / kWavesPerBlock;
     return grid > need ? need : grid;
 }
 
-// K = 256 nb, nb = NB (short rows) or 16 S
+// K = 256 nb, nb = NB (short rows) or 16 S.  Rows of two or more wave steps
+// run one workgroup per CU: ffn_down at config 3 (Q6_K, 48 super-blocks, two
+// rows per wave with two workgroups per CU) measured 9.5 us this way against
+// 9.7-10.4 us with two, whose second workgroup has its loads served after the
+// first's and finishes last.
 template <class QT, bool kF32, int S, int M, int kSegs, bool kNorm, int NB = 0>
 void launch_stream(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
     constexpr int K = (NB ? NB : S * QT::kSbPerStep) * kQK;
     launch_kernel((matvec_stream_kernel<QT, kF32, S, M, kSegs, true, kNorm, NB>),
-                  dim3(stream_grid(rs.end[kSegs - 1])), dim3(kBlock), lds, stream, rs, x, K, nrm);
+                  dim3(stream_grid(rs.end[kSegs - 1], S >= 2 ? 1 : 2)), dim3(kBlock), lds, stream, rs, x, K, nrm);
 }
 
 // Rows of one wave step (K <= 4096), few rows: every wave loads its M rows
@@ -857,39 +897,21 @@ bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], bool f16, const
 template <class QT, bool kNorm>
 hipError_t launch_gate_up_t(const uint8_t* wg, const uint8_t* wu, const uint16_t* x, uint16_t* act, int K, int N,
                           const NormIn& nrm, hipStream_t stream) {
-    const size_t lds = lds_bytes<QT>(K);
-    int grid = 2 * device_cus();
-    const int need = (N + kWavesPerBlock - 1) / kWavesPerBlock;
+    const size_t lds = lds_bytes<QT>(K) + sizeof(int);   // + the row counter
+    int grid = device_cus();
+    const int need = (N + kGateUpWaves - 1) / kGateUpWaves;
     if (grid > need) grid = need;
+    const dim3 g(grid), b(kGateUpBlock);
     switch (K / kQK) {
-        case 16:   // M = 1: measured faster than 2 at 12288 x 4096 on MI355X
-            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x,
-                          act, K, N, nrm);
-            break;
-        case 32:
-            launch_kernel((matvec_gate_up_kernel<QT, 2, 1, kNorm>), dim3(grid), dim3(kBlock), lds, stream, wg, wu, x,
-                          act, K, N, nrm);
-            break;
-        case 4:   // rows shorter than one wave step (Qwen3-0.6B: hidden 1024)
-            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 4>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
-                          x, act, K, N, nrm);
-            break;
-        case 8:
-            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 8>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
-                          x, act, K, N, nrm);
-            break;
-        case 12:
-            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 12>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
-                          x, act, K, N, nrm);
-            break;
-        case 10:   // hidden 2560 (Qwen3-4B)
-            launch_kernel((matvec_gate_up_kernel<QT, 1, 1, kNorm, 10>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
-                          x, act, K, N, nrm);
-            break;
-        case 20:   // hidden 5120 (Qwen3-14B / 32B)
-            launch_kernel((matvec_gate_up_kernel<QT, 2, 1, kNorm, 20>), dim3(grid), dim3(kBlock), lds, stream, wg, wu,
-                          x, act, K, N, nrm);
-            break;
+        case 16: launch_kernel((matvec_gate_up_kernel<QT, 1, kNorm>), g, b, lds, stream, wg, wu, x, act, K, N, nrm); break;
+        case 32: launch_kernel((matvec_gate_up_kernel<QT, 2, kNorm>), g, b, lds, stream, wg, wu, x, act, K, N, nrm); break;
+        // rows shorter than one wave step (Qwen3-0.6B: hidden 1024; 1.7B: 2048;
+        // 4B: 2560), and hidden 5120 (Qwen3-14B / 32B)
+        case 4: launch_kernel((matvec_gate_up_kernel<QT, 1, kNorm, 4>), g, b, lds, stream, wg, wu, x, act, K, N, nrm); break;
+        case 8: launch_kernel((matvec_gate_up_kernel<QT, 1, kNorm, 8>), g, b, lds, stream, wg, wu, x, act, K, N, nrm); break;
+        case 12: launch_kernel((matvec_gate_up_kernel<QT, 1, kNorm, 12>), g, b, lds, stream, wg, wu, x, act, K, N, nrm); break;
+        case 10: launch_kernel((matvec_gate_up_kernel<QT, 1, kNorm, 10>), g, b, lds, stream, wg, wu, x, act, K, N, nrm); break;
+        case 20: launch_kernel((matvec_gate_up_kernel<QT, 2, kNorm, 20>), g, b, lds, stream, wg, wu, x, act, K, N, nrm); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
