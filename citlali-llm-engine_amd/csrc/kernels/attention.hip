@@ -32,6 +32,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace citlali::hip {
 namespace {
 
@@ -318,19 +320,22 @@ __global__ __launch_bounds__(kBlock) void attn_split_kernel(
 //    dims in 8 steps of 16, dim 32t + 8grp + 4h + j of step (t, h) being
 //    operand k = 4grp + j), q is the B operand in the same dim order; lane
 //    (col, grp) gets the scores of positions 4grp + i for head col.
-//  * online softmax per head column (max and sum over the 16 lanes' groups),
-//    exponentials in base 2 as the VALU kernel.
-//  * out[head][dim] += P[head][pos] V[pos][dim]: the scores' lane layout is
-//    the A operand of P as it stands; P goes in as fp16 hi + lo halves (two
-//    MFMAs), so its fp32 value counts to about 2^-22.  V rows are staged in a
-//    wave-private LDS tile and gathered per lane as 4 positions x 4 dims
-//    (dims 64c + 4col + e feed output block 4c + e).
+//  * online softmax per head column (max and sum over the column's four lane
+//    groups by permlane swaps), exponentials in base 2 as the VALU kernel.
+//  * out^T[dim][head] += V^T[dim][pos] P^T[pos][head]: the scores' lane
+//    layout is the B operand P^T as it stands, so every accumulator of a
+//    lane belongs to the lane's head column and the online-softmax rescale
+//    needs no lane moves (none on a wave's first tile).  P goes in as
+//    fp16 hi + lo halves (two MFMAs), so its fp32 value counts to about
+//    2^-22.  V rows are staged in a wave-private LDS tile and gathered per
+//    lane as 4 positions x 4 dims, the A operand (dims 64c + 4col + e feed
+//    output block 4c + e, rows 4grp + i of which are dims 64c + 16grp + 4i + e).
 // ---------------------------------------------------------------------------
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 constexpr int kMTile = 16;                     // positions per MFMA tile
 constexpr int kMStride = 128 + 8;              // K / V tile row in LDS (halves)
 constexpr size_t kMWaveLds = (size_t)kMTile * kMStride * 2;
-// merge: (max, sum)[NW][8], acc[NW][2 row groups][8 blocks][16 cols][4]
+// merge: (max, sum)[NW][8], acc[NW][8 blocks][8 heads][4 lane groups][4]
 // tiles: per wave a V tile, and with row loads a K tile, kMWaveLds each
 template <int NW, bool kRows>
 struct MfmaLds {
@@ -439,7 +444,7 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
         for (int t = 0; t < 4; ++t) q_raw[t] = *reinterpret_cast<const u32x4*>(qh + 32 * t);
     }
     half4 qb[4][2];
-    f32x4 o[8];   // o[4c + e][i]: head 4grp + i, dim 64c + 4col + e
+    f32x4 o[8];   // o[4c + e][i]: dim 64c + 16grp + 4i + e of head col
 #pragma unroll
     for (int b = 0; b < 8; ++b) o[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.f;   // head col
@@ -465,7 +470,7 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
     };
 
     const uint16_t* kv_new = reinterpret_cast<const uint16_t*>(smem + Lds::kKv) + (size_t)wave * 2 * HD;
-    auto process = [&](int t0) {
+    auto process = [&](int t0, auto first_tile) {
         if constexpr (kPrep) {
             // the step's row comes from the prologue's k' and v in LDS
 #pragma unroll
@@ -531,12 +536,19 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
         l_run = l_run * alpha + column_sum<16>(ps);
         m_run = m_new;
 
-        // rescale the heads this lane accumulates (head 4grp + i: alpha of column 4grp + i)
+        // rescale this lane's head (column col); not on the wave's first tile,
+        // where o is still zero.  The decode launch (kPrep: one or two tiles
+        // per wave) also skips it when no column's max moved; in the launches
+        // of longer ranges that branch inside the loop measured slower
+        // (config 3: 14.5 against 13.8 us), so they peel the first tile.
+        if constexpr (kPrep) {
+            if (t0 != w0 && __builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float a = __shfl(alpha, 4 * grp + i, kWave);
+                for (int b = 0; b < 8; ++b) o[b] *= alpha;
+            }
+        } else if constexpr (!decltype(first_tile)::value) {
 #pragma unroll
-            for (int b = 0; b < 8; ++b) o[b][i] *= a;
+            for (int b = 0; b < 8; ++b) o[b] *= alpha;
         }
         half4 ph, pl;
 #pragma unroll
@@ -560,8 +572,10 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
                 const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
                 const half4 vb = as_half4(__builtin_amdgcn_perm(w[1][e >> 1], w[0][e >> 1], sel),
                                           __builtin_amdgcn_perm(w[3][e >> 1], w[2][e >> 1], sel));
-                o[4 * c + e] = mfma16(ph, vb, o[4 * c + e]);
-                o[4 * c + e] = mfma16(pl, vb, o[4 * c + e]);
+                // V^T P^T: dims x heads, so a lane's accumulators belong to
+                // one head (its column) and the rescale needs no lane moves
+                o[4 * c + e] = mfma16(vb, ph, o[4 * c + e]);
+                o[4 * c + e] = mfma16(vb, pl, o[4 * c + e]);
             }
         }
         wave_lds_sync();   // before the next tile overwrites the rows
@@ -628,27 +642,32 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
             qb[t][1] = as_half4(q_raw[t].z & keep, q_raw[t].w & keep);
         }
     }
-    for (int t0 = w0; t0 < w1; t0 += kMTile) process(t0);
+    if constexpr (kPrep) {
+        for (int t0 = w0; t0 < w1; t0 += kMTile) process(t0, std::false_type{});
+    } else {
+        if (w0 < w1) process(w0, std::true_type{});
+        for (int t0 = w0 + kMTile; t0 < w1; t0 += kMTile) process(t0, std::false_type{});
+    }
 
     // ---- merge the waves in LDS ----
     __syncthreads();   // every wave is done with its V tile
     float* ml = reinterpret_cast<float*>(smem);   // [NW][8] (max, sum)
-    float* ms = ml + Lds::kMlFloats;              // [NW][2][8][16][4]
+    float* ms = ml + Lds::kMlFloats;              // [NW][8 b][8 heads][4 grp][4 i]
     if (grp == 0 && col < GP) {
         ml[(wave * 8 + col) * 2] = m_run;
         ml[(wave * 8 + col) * 2 + 1] = l_run;
     }
-    if (grp < (GP + 3) / 4) {
+    if (col < GP) {
 #pragma unroll
         for (int b = 0; b < 8; ++b)
-            *reinterpret_cast<f32x4*>(ms + ((((size_t)wave * 2 + grp) * 8 + b) * 16 + col) * 4) = o[b];
+            *reinterpret_cast<f32x4*>(ms + ((((size_t)wave * 8 + b) * 8 + col) * 4 + grp) * 4) = o[b];
     }
     __syncthreads();
 
     for (int idx = threadIdx.x; idx < group * HD; idx += NW * kWave) {
         const int h = idx / HD, dim = idx - h * HD;
-        const int hg = h >> 2, hi = h & 3;
-        const int b = 4 * (dim >> 6) + (dim & 3), c16 = (dim & 63) >> 2;
+        // dim = 64c + 16g + 4i + e lives in o[4c + e][i] of lane group g
+        const int b = 4 * (dim >> 6) + (dim & 3), g4 = (dim >> 4) & 3, i4 = (dim >> 2) & 3;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < NW; ++w) M = fmaxf(M, ml[(w * 8 + h) * 2]);
@@ -658,7 +677,7 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
             const float mw = ml[(w * 8 + h) * 2];
             const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
             Ls += ml[(w * 8 + h) * 2 + 1] * f;
-            A += ms[((((size_t)w * 2 + hg) * 8 + b) * 16 + c16) * 4 + hi] * f;
+            A += ms[((((size_t)w * 8 + b) * 8 + h) * 4 + g4) * 4 + i4] * f;
         }
         const int hq = kvh * group + h;
         if (n_valid == 1) {

@@ -75,12 +75,40 @@ template <int Ctrl>
 __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), Ctrl, 0xF, 0xF, false));
 }
-// value of lane ^ 16 (ds_swizzle SWAP16, no LDS memory access)
-__device__ __forceinline__ float xor16(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+// Permlane swaps: v_permlane16_swap exchanges the odd 16-lane rows of its
+// first operand with the even rows of its second, v_permlane32_swap lanes
+// 32-63 of the first with lanes 0-31 of the second.  Called with a = b = v,
+// afterwards {a, b} holds v and its lane ^ 16 (^ 32) partner in every lane,
+// so a + b and max(a, b) are the pairwise reductions, on the VALU.  Inline
+// asm because this compiler reads the builtins' second result back as the
+// first (a + b came out as 2a on the box); s_nop 1 covers the wait states
+// between the VALU write of an operand and the permlane read.
+__device__ __forceinline__ void swap16(float& a, float& b) {
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
-// value of lane ^ 32
-__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, kWave); }
+__device__ __forceinline__ void swap32(float& a, float& b) {
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float sum16(float v) {
+    float a = v, b = v;
+    swap16(a, b);
+    return a + b;
+}
+__device__ __forceinline__ float sum32(float v) {
+    float a = v, b = v;
+    swap32(a, b);
+    return a + b;
+}
+__device__ __forceinline__ float max16(float v) {
+    float a = v, b = v;
+    swap16(a, b);
+    return fmaxf(a, b);
+}
+__device__ __forceinline__ float max32(float v) {
+    float a = v, b = v;
+    swap32(a, b);
+    return fmaxf(a, b);
+}
 
 // Sum over all 64 lanes; every lane gets the same (wave-uniform) result.
 __device__ __forceinline__ float wave_sum(float v) {
@@ -88,7 +116,7 @@ __device__ __forceinline__ float wave_sum(float v) {
     v += dpp<kDppXor2>(v);
     v += dpp<DppRor<4>::value>(v);
     v += dpp<DppRor<8>::value>(v);
-    v += xor16(v);
+    v = sum16(v);
     const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
     const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
     return lo + hi;
@@ -98,7 +126,7 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, dpp<kDppXor2>(v));
     v = fmaxf(v, dpp<DppRor<4>::value>(v));
     v = fmaxf(v, dpp<DppRor<8>::value>(v));
-    v = fmaxf(v, xor16(v));
+    v = max16(v);
     const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
     const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
     return fmaxf(lo, hi);
@@ -112,8 +140,7 @@ __device__ __forceinline__ float column_sum(float v) {
     if constexpr (G < 4) v += dpp<kDppXor2>(v);
     if constexpr (G < 8) v += dpp<DppRor<4>::value>(v);
     if constexpr (G < 16) v += dpp<DppRor<8>::value>(v);
-    v += xor16(v);
-    return v + xor32(v);
+    return sum32(sum16(v));
 }
 template <int G>
 __device__ __forceinline__ float column_max(float v) {
@@ -121,8 +148,7 @@ __device__ __forceinline__ float column_max(float v) {
     if constexpr (G < 4) v = fmaxf(v, dpp<kDppXor2>(v));
     if constexpr (G < 8) v = fmaxf(v, dpp<DppRor<4>::value>(v));
     if constexpr (G < 16) v = fmaxf(v, dpp<DppRor<8>::value>(v));
-    v = fmaxf(v, xor16(v));
-    return fmaxf(v, xor32(v));
+    return max32(max16(v));
 }
 
 // Waits until every earlier vector memory operation of this wave has
