@@ -586,6 +586,10 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (kPrep) {
         uint16_t* qs = reinterpret_cast<uint16_t*>(smem + Lds::kQs);   // [GP][HD]
+        // the RoPE angle of this lane's dim pair at the step's position: the
+        // same for every head, and independent of the loads in flight
+        float rsn, rcs;
+        rope_angle(lane, HD, p_raw, prep.theta, rsn, rcs);
 #pragma unroll
         for (int j = 0; j < kHeadsPerWave; ++j) {
             const int h = wave + j * NW;
@@ -598,7 +602,7 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
                     y1 = f2h_rne(x1 * inv * h2f(pqw[1]));
                 }
                 uint16_t r0, r1;
-                rope_pair(h2f(y0), h2f(y1), lane, HD, p_raw, prep.theta, r0, r1);
+                rope_rotate(h2f(y0), h2f(y1), rsn, rcs, r0, r1);
                 const bool real = h < group;   // padding heads: q = 0
                 qs[h * HD + lane] = real ? r0 : (uint16_t)0;
                 qs[h * HD + 64 + lane] = real ? r1 : (uint16_t)0;
@@ -613,7 +617,7 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
                 y1 = f2h_rne(x1 * inv * h2f(pkw[1]));
             }
             uint16_t r0, r1;
-            rope_pair(h2f(y0), h2f(y1), lane, HD, p_raw, prep.theta, r0, r1);
+            rope_rotate(h2f(y0), h2f(y1), rsn, rcs, r0, r1);
             const size_t row = (size_t)seq * seq_stride + (size_t)pos_row * row_step + (size_t)kvh * HD;
             prep.k_cache[row + lane] = r0;
             prep.k_cache[row + 64 + lane] = r1;

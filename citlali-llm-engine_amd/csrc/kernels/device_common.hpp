@@ -218,16 +218,25 @@ __device__ __forceinline__ float head_inv_rms(float x_lo, float x_hi, int head_d
 }
 
 // Pair (i, i + head_dim/2) rotated by position * theta^(-2i/head_dim), each
-// result rounded to fp16 (kernels.cu:485-521).
-__device__ __forceinline__ void rope_pair(float x0, float x1, int i, int head_dim, int position, float theta,
-                                          uint16_t& y0, uint16_t& y1) {
+// result rounded to fp16 (kernels.cu:485-521), in two parts: the angle's
+// sine and cosine depend only on the pair and the position, so a caller that
+// rotates several heads at one position computes them once.
+__device__ __forceinline__ void rope_angle(int i, int head_dim, int position, float theta, float& sn, float& cs) {
 #pragma clang fp contract(off)   // the same bits in every kernel that inlines it
     const float inv_freq = powf(theta, -(float)(2 * i) / (float)head_dim);
     const float angle = (float)position * inv_freq;
-    float sn, cs;
     sincosf(angle, &sn, &cs);
+}
+__device__ __forceinline__ void rope_rotate(float x0, float x1, float sn, float cs, uint16_t& y0, uint16_t& y1) {
+#pragma clang fp contract(off)
     y0 = f2h_rne(x0 * cs - x1 * sn);
     y1 = f2h_rne(x0 * sn + x1 * cs);
+}
+__device__ __forceinline__ void rope_pair(float x0, float x1, int i, int head_dim, int position, float theta,
+                                          uint16_t& y0, uint16_t& y1) {
+    float sn, cs;
+    rope_angle(i, head_dim, position, theta, sn, cs);
+    rope_rotate(x0, x1, sn, cs, y0, y1);
 }
 
 // Orders LDS traffic between lanes of one wave (no workgroup barrier): the
