@@ -755,15 +755,25 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restr
     rm[threadIdx.x] = f32x2{m, l};
     __syncthreads();
     if (g == 0) {
+        // every group's (max, sum) and accumulator are read before the
+        // arithmetic, so the combine waits for LDS once
+        f32x2 x[kGroups];
+        f32x4 r[kGroups];
+#pragma unroll
+        for (int gg = 0; gg < kGroups; ++gg) {
+            x[gg] = rm[gg * kQuads + d4];
+            r[gg] = ra[gg * kQuads + d4];
+        }
         float M = m;
-        for (int gg = 1; gg < kGroups; ++gg) M = fmaxf(M, rm[gg * kQuads + d4].x);
+#pragma unroll
+        for (int gg = 1; gg < kGroups; ++gg) M = fmaxf(M, x[gg].x);
         f32x4 A = {0.f, 0.f, 0.f, 0.f};
         float L = 0.f;
+#pragma unroll
         for (int gg = 0; gg < kGroups; ++gg) {
-            const f32x2 x = rm[gg * kQuads + d4];
-            const float f = x.x == -INFINITY ? 0.f : exp2f(x.x - M);
-            A += ra[gg * kQuads + d4] * f;
-            L += x.y * f;
+            const float f = x[gg].x == -INFINITY ? 0.f : exp2f(x[gg].x - M);
+            A += r[gg] * f;
+            L += x[gg].y * f;
         }
         const float inv = 1.f / L;
         uint16_t* o = out + h0 * HD + 4 * d4;
