@@ -668,31 +668,52 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
     }
     __syncthreads();
 
-    for (int idx = threadIdx.x; idx < group * HD; idx += NW * kWave) {
-        const int h = idx / HD, dim = idx - h * HD;
-        // dim = 64c + 16g + 4i + e lives in o[4c + e][i] of lane group g
-        const int b = 4 * (dim >> 6) + (dim & 3), g4 = (dim >> 4) & 3, i4 = (dim >> 2) & 3;
-        float M = -INFINITY;
+    // Thread t merges dims kPer*t .. + kPer - 1 of one head (kPer divides HD):
+    // the head's max, wave factors and sum are formed once, and every LDS
+    // read is issued before the arithmetic.
+    constexpr int kPer = GP * HD / (NW * kWave);
+    static_assert(kPer >= 1 && HD % kPer == 0 && kPer * NW * kWave == GP * HD, "merge split");
+    const int base = (int)threadIdx.x * kPer;
+    if (base >= group * HD) return;
+    const int h = base / HD, dim0 = base - h * HD;
+    f32x2 mlw[NW];
+    float acc[NW][kPer];
 #pragma unroll
-        for (int w = 0; w < NW; ++w) M = fmaxf(M, ml[(w * 8 + h) * 2]);
-        float Ls = 0.f, A = 0.f;
+    for (int w = 0; w < NW; ++w) {
+        mlw[w] = *reinterpret_cast<const f32x2*>(ml + (w * 8 + h) * 2);
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            const float mw = ml[(w * 8 + h) * 2];
-            const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
-            Ls += ml[(w * 8 + h) * 2 + 1] * f;
-            A += ms[((((size_t)w * 8 + b) * 8 + h) * 4 + g4) * 4 + i4] * f;
+        for (int j = 0; j < kPer; ++j) {
+            // dim = 64c + 16g + 4i + e lives in o[4c + e][i] of lane group g
+            const int dim = dim0 + j;
+            const int b = 4 * (dim >> 6) + (dim & 3), g4 = (dim >> 4) & 3, i4 = (dim >> 2) & 3;
+            acc[w][j] = ms[((((size_t)w * 8 + b) * 8 + h) * 4 + g4) * 4 + i4];
         }
-        const int hq = kvh * group + h;
-        if (n_valid == 1) {
-            out[((size_t)seq * heads + hq) * HD + dim] = f2h_rne(A / Ls);
-        } else {
-            float* pe = part + (((size_t)seq * heads + hq) * n_splits + split) * (HD + 4);
-            pe[dim] = A;
-            if (dim == 0) {
-                pe[HD] = M;
-                pe[HD + 1] = Ls;
-            }
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, mlw[w].x);
+    float Ls = 0.f, A[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) A[j] = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        const float f = mlw[w].x == -INFINITY ? 0.f : exp2f(mlw[w].x - M);
+        Ls += mlw[w].y * f;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) A[j] += acc[w][j] * f;
+    }
+    const int hq = kvh * group + h;
+    if (n_valid == 1) {
+        uint16_t* o = out + ((size_t)seq * heads + hq) * HD + dim0;
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) o[j] = f2h_rne(A[j] / Ls);
+    } else {
+        float* pe = part + (((size_t)seq * heads + hq) * n_splits + split) * (HD + 4);
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) pe[dim0 + j] = A[j];
+        if (dim0 == 0) {
+            pe[HD] = M;
+            pe[HD + 1] = Ls;
         }
     }
 }
