@@ -70,8 +70,8 @@ size_t split_lds_bytes() {
     return tiles > C::kMergeLds ? tiles : C::kMergeLds;
 }
 
-// merge kernel: per-thread accumulator (float4) and (max, sum) pair
-constexpr size_t kMergeLds = (size_t)kBlock * (16 + 8);
+// the merge kernel keeps everything in registers
+constexpr size_t kMergeLds = 0;
 
 // Positions a sequence covers and its chunk count.  A position at or beyond
 // the caller's bound `max_len` is cut there, so neither the cache reads nor
@@ -719,16 +719,17 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
 }
 
 // Grid: (query head, seq).  Log-sum-exp merge of one head's chunk partials
-// ([chunk][HD + 4]: acc[HD], max, sum) in one pass: thread = (4 dims, chunk
-// subset) loads its chunks' accumulators and (max, sum) pairs together and
-// merges them with a running max (one global round trip); the subsets then
-// merge in LDS.
-template <int HD>
+// ([chunk][HD + 4]: acc[HD], max, sum) in one global round trip, without
+// LDS: every wave finds the largest chunk max M (lane j reads the maxima of
+// chunks j, j + 64, ...) while thread (dim quad, subset g) loads the
+// accumulators and (max, sum) of its chunks g, g + kSub, ...; it folds them
+// with the factors exp2(max - M) in chunk order, and the kSub consecutive
+// lanes of a dim quad add their folds by DPP.
+template <int HD, int kBatch>
 __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restrict__ part,
                                                             const int32_t* __restrict__ positions, int position,
                                                             int max_len, int heads, int chunk, int n_splits,
                                                             uint16_t* __restrict__ out) {
-    extern __shared__ __align__(16) uint8_t smem[];
     const int hq = blockIdx.x, seq = blockIdx.y;
     const int n_valid = seq_span(positions, position, seq, chunk, max_len).n_valid;
     if (n_valid <= 1) return;   // written by the split kernel
@@ -736,73 +737,75 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restr
     constexpr size_t ent = HD + 4;
     const float* hp = part + h0 * n_splits * ent;
     constexpr int kQuads = HD / 4;
-    constexpr int kGroups = kBlock / kQuads;
-    const int d4 = threadIdx.x % kQuads, g = threadIdx.x / kQuads;
+    constexpr int kSub = kBlock / kQuads;   // lanes per dim quad: 8 (HD 128) or 16 (HD 64)
+    static_assert(kSub == 8 || kSub == 16, "subsets of consecutive lanes");
+    const int lane = threadIdx.x & (kWave - 1);
+    const int g = threadIdx.x % kSub, d4 = threadIdx.x / kSub;
 
-    constexpr int kBatch = 4;   // chunks whose loads are issued together
-    float m = -INFINITY, l = 0.f;
-    f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    for (int s0 = g; s0 < n_valid; s0 += kBatch * kGroups) {
-        f32x4 v[kBatch];
-        f32x2 ml[kBatch];
+    // kBatch chunks per thread have their loads issued together; the loads
+    // are unconditional (a chunk past the last re-reads the last one), so
+    // none waits on a branch, and such chunks get the factor 0.
+    auto load_batch = [&](int s0, f32x4 (&v)[kBatch], f32x2 (&ml)[kBatch]) {
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
-            const int s = s0 + j * kGroups;
-            v[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-            ml[j] = f32x2{-INFINITY, 0.f};
-            if (s < n_valid) {
-                const float* e = hp + (size_t)s * ent;
-                ml[j] = *reinterpret_cast<const f32x2*>(e + HD);
-                v[j] = *reinterpret_cast<const f32x4*>(e + 4 * d4);
-            }
+            const float* e = hp + (size_t)min(s0 + j * kSub, n_valid - 1) * ent;
+            ml[j] = *reinterpret_cast<const f32x2*>(e + HD);
+            v[j] = *reinterpret_cast<const f32x4*>(e + 4 * d4);
         }
-        float mn = m;
-#pragma unroll
-        for (int j = 0; j < kBatch; ++j) mn = fmaxf(mn, ml[j].x);
-        const float fo = m == -INFINITY ? 0.f : exp2f(m - mn);
-        a *= fo;
-        l *= fo;
+    };
+    f32x4 v[kBatch];
+    f32x2 ml[kBatch];
+    load_batch(g, v, ml);
+    // the largest chunk max (its loads go out behind the first batch's)
+    float mx = -INFINITY;
+    for (int s = lane; s < kMaxSplits; s += kWave) {   // uniform trip count
+        mx = fmaxf(mx, hp[(size_t)min(s, n_valid - 1) * ent + HD]);
+        if (s - lane + kWave >= n_valid) break;
+    }
+    const float M = wave_max(mx);
+
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    float l = 0.f;
+    for (int s0 = g;;) {
 #pragma unroll
         for (int j = 0; j < kBatch; ++j) {
-            const float f = ml[j].x == -INFINITY ? 0.f : exp2f(ml[j].x - mn);
+            const float mj = s0 + j * kSub < n_valid ? ml[j].x : -INFINITY;
+            const float f = mj == -INFINITY ? 0.f : exp2f(mj - M);
             a += v[j] * f;
             l += ml[j].y * f;
         }
-        m = mn;
+        s0 += kBatch * kSub;
+        if (s0 - g >= n_valid) break;   // uniform: no chunk left for any subset
+        load_batch(s0, v, ml);
     }
-    f32x4* ra = reinterpret_cast<f32x4*>(smem);                // [kBlock]
-    f32x2* rm = reinterpret_cast<f32x2*>(ra + kBlock);         // [kBlock] (max, sum)
-    ra[threadIdx.x] = a;
-    rm[threadIdx.x] = f32x2{m, l};
-    __syncthreads();
+    a.x = lane_group_sum<kSub>(a.x);
+    a.y = lane_group_sum<kSub>(a.y);
+    a.z = lane_group_sum<kSub>(a.z);
+    a.w = lane_group_sum<kSub>(a.w);
+    l = lane_group_sum<kSub>(l);
     if (g == 0) {
-        // every group's (max, sum) and accumulator are read before the
-        // arithmetic, so the combine waits for LDS once
-        f32x2 x[kGroups];
-        f32x4 r[kGroups];
-#pragma unroll
-        for (int gg = 0; gg < kGroups; ++gg) {
-            x[gg] = rm[gg * kQuads + d4];
-            r[gg] = ra[gg * kQuads + d4];
-        }
-        float M = m;
-#pragma unroll
-        for (int gg = 1; gg < kGroups; ++gg) M = fmaxf(M, x[gg].x);
-        f32x4 A = {0.f, 0.f, 0.f, 0.f};
-        float L = 0.f;
-#pragma unroll
-        for (int gg = 0; gg < kGroups; ++gg) {
-            const float f = x[gg].x == -INFINITY ? 0.f : exp2f(x[gg].x - M);
-            A += r[gg] * f;
-            L += x[gg].y * f;
-        }
-        const float inv = 1.f / L;
+        const float inv = 1.f / l;
         uint16_t* o = out + h0 * HD + 4 * d4;
-        o[0] = f2h_rne(A.x * inv);
-        o[1] = f2h_rne(A.y * inv);
-        o[2] = f2h_rne(A.z * inv);
-        o[3] = f2h_rne(A.w * inv);
+        o[0] = f2h_rne(a.x * inv);
+        o[1] = f2h_rne(a.y * inv);
+        o[2] = f2h_rne(a.z * inv);
+        o[3] = f2h_rne(a.w * inv);
     }
+}
+
+// The merge launch, its per-thread batch sized to the plan's chunk count
+// (HD / 4 lanes of a wave hold one subset of the chunks each).
+template <int HD>
+void launch_merge(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
+    constexpr int kSub = kBlock / (HD / 4);
+    const int per = (p.n_splits + kSub - 1) / kSub;
+    auto go = [&](auto kernel) {
+        launch_kernel(kernel, dim3(a.heads, a.nseq), dim3(kBlock), kMergeLds, stream, a.workspace, a.positions,
+                      a.position, a.max_len, a.heads, p.chunk, p.n_splits, a.out);
+    };
+    if (per <= 2) go(attn_merge_kernel<HD, 2>);
+    else if (per <= 4) go(attn_merge_kernel<HD, 4>);
+    else go(attn_merge_kernel<HD, 8>);
 }
 
 template <int HD, int GP, int kDepth>
@@ -815,8 +818,7 @@ hipError_t launch_split(const AttnArgs& a, const AttnPlan& p, hipStream_t stream
                           a.workspace, p.n_splits, a.out);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_splits <= 1) return e;
-    launch_kernel((attn_merge_kernel<HD>), dim3(a.heads, a.nseq), dim3(kBlock), kMergeLds, stream, a.workspace,
-                  a.positions, a.position, a.max_len, a.heads, p.chunk, p.n_splits, a.out);
+    launch_merge<HD>(a, p, stream);
     return hipGetLastError();
 }
 
@@ -837,8 +839,7 @@ hipError_t launch_mfma(const AttnArgs& a, const AttnPlan& p, hipStream_t stream)
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.n_splits <= 1) return e;
-    launch_kernel((attn_merge_kernel<128>), dim3(a.heads, a.nseq), dim3(kBlock), kMergeLds, stream, a.workspace,
-                  a.positions, a.position, a.max_len, a.heads, p.chunk, p.n_splits, a.out);
+    launch_merge<128>(a, p, stream);
     return hipGetLastError();
 }
 

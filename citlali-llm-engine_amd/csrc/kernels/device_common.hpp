@@ -70,6 +70,8 @@ constexpr int kDppXor1 = 0xB1;     // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;     // quad_perm [2,3,0,1]
 template <int N>
 struct DppRor { static constexpr int value = 0x120 + N; };   // row_ror:N (N = 1..15)
+constexpr int kDppMirror = 0x140;       // row_mirror: lane i <-> 15 - i of each 16
+constexpr int kDppHalfMirror = 0x141;   // row_half_mirror: lane i <-> 7 - i of each 8
 
 template <int Ctrl>
 __device__ __forceinline__ float dpp(float v) {
@@ -130,6 +132,19 @@ __device__ __forceinline__ float wave_max(float v) {
     const float lo = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
     const float hi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
     return fmaxf(lo, hi);
+}
+
+// Sum over each group of N consecutive lanes (N = 8 or 16); every lane of a
+// group gets the same bits (each step adds a lane's value and its partner's,
+// and a + b = b + a).
+template <int N>
+__device__ __forceinline__ float lane_group_sum(float v) {
+    static_assert(N == 8 || N == 16, "group");
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    if constexpr (N == 16) v += dpp<kDppMirror>(v);
+    return v;
 }
 
 // Reductions over the lanes that share lane % G (G = 1, 2, 4, 8, 16): the
