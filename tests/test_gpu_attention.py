@@ -64,14 +64,17 @@ def test_attention_matches_oracle(hip, orc, heads, kv_heads, hd, L, max_ctx):
     assert np.all(np.abs(got - ref) <= np.abs(ref) * 2 ** -10 + 1e-4)
 
 
-# Plans with more chunks than the merge kernel folds in one pass (32 for
-# head_dim 128, 64 for head_dim 64): its loop over chunk batches runs 2 to 10
-# passes.  (heads, kv_heads, head_dim, L, chunks the plan must make)
+# Plans of many chunks.  The merge kernel folds up to 64 chunks per pass at
+# head_dim 128 and 128 at head_dim 64 (8 per thread), and each wave lane
+# reads the maxima of chunks lane, lane + 64, ...: these run one to five
+# fold passes and one to five maxima reads per lane.
+# (heads, kv_heads, head_dim, L, chunks the plan must make)
 MANY_SPLITS = [
     (32, 4, 128, 16384, 64),
     (16, 2, 128, 32768, 128),
     (8, 1, 128, 300000, 293),
     (16, 2, 64, 40000, 125),
+    (16, 2, 64, 80000, 157),
 ]
 
 
@@ -92,8 +95,8 @@ def test_config4_batched_at_its_lengths(hip, orc):
     """BASELINE config 4 at its workload: 16 sequences at 32/8/128 with KV
     lengths uniform in [4096, 32768] drawn as bench.py draws them
     (numpy default_rng(4)), one batched launch planned for 32768 positions
-    (64 chunks per sequence, so the merge runs two passes), every sequence
-    against the oracle."""
+    (64 chunks per sequence: the merge's largest batch, 8 chunks per
+    thread), every sequence against the oracle."""
     nseq, heads, kv, hd, max_len = 16, 32, 8, 128, 32768
     lens = np.random.default_rng(4).integers(4096, max_len + 1, nseq)
     print(f"[attention cfg4] lengths {lens.tolist()}", flush=True)
