@@ -166,10 +166,6 @@ __device__ __forceinline__ float column_max(float v) {
     return max32(max16(v));
 }
 
-// Waits until every earlier vector memory operation of this wave has
-// completed (s_waitcnt vmcnt(0)), e.g. write-through stores before a flag.
-__device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // Workgroup barrier that orders LDS only: earlier global loads stay in
 // flight across it (a full __syncthreads would wait for them).
 __device__ __forceinline__ void lds_barrier() {

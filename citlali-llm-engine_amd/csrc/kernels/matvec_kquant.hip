@@ -428,12 +428,8 @@ struct RowSet {
 // (all loaded up front) and stops; the grid then has M * W >= rows.  NB (an
 // even block count that is not a multiple of 16, S = ceil(NB / 16)): rows
 // ending in a partial wave step; in that step the lanes of blocks NB.. load
-// block NB - 1 (in bounds) and add nothing.  kXFirst: the first fragments
-// are issued only once x (and the norm inputs) have arrived.  With three
-// workgroups per CU, a later workgroup's x otherwise comes back behind the
-// earlier ones' weight loads; waiting evens out the start.
-template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false, int NB = 0,
-          bool kXFirst = false>
+// block NB - 1 (in bounds) and add nothing.
+template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false, int NB = 0>
 __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __restrict__ x, int K, uint8_t* smem,
                                             int gw, int W, const NormIn& nrm) {
     static_assert(NB == 0 || (NB % 2 == 0 && (NB + QT::kSbPerStep - 1) / QT::kSbPerStep == S), "partial last step");
@@ -464,10 +460,6 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
     XStage<QT::kSumLayout, nb * 32, kNorm> xs;   // K / 8 = 32 nb runs of eight values
     xs.load(x, nrm);
     __builtin_amdgcn_sched_barrier(0);   // issue order: x, first fragments, staging
-    if constexpr (kXFirst) {
-        wait_vm_all();
-        __builtin_amdgcn_sched_barrier(0);
-    }
     typename QT::Frag fr[D];
 #pragma unroll
     for (int m = 0; m < M; ++m)
@@ -525,19 +517,19 @@ __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_stream_kernel(Ro
 // Two row sets of different types in one launch: blocks [0, blocks_a) walk
 // set `a` (type QA), the rest walk set `b` (type QB).  Each row is computed
 // exactly as the single-matrix launch computes it.
-template <class QA, class QB, int S, int M, bool kRefill = true, bool kNorm = false, int NB = 0, bool kXFirst = false>
+template <class QA, class QB, int S, int M, bool kRefill = true, bool kNorm = false, int NB = 0>
 __global__ __launch_bounds__(kBlock, kWavesPerSimd) void matvec_group_kernel(RowSet a, RowSet b, int blocks_a,
                                                                             const uint16_t* __restrict__ x, int K,
                                                                             NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
     const int wave = threadIdx.x / kWave;
     if ((int)blockIdx.x < blocks_a)
-        stream_rows<QA, false, S, M, 3, kRefill, kNorm, NB, kXFirst>(a, x, K, smem, blockIdx.x * kWavesPerBlock + wave,
-                                                                     blocks_a * kWavesPerBlock, nrm);
+        stream_rows<QA, false, S, M, 3, kRefill, kNorm, NB>(a, x, K, smem, blockIdx.x * kWavesPerBlock + wave,
+                                                            blocks_a * kWavesPerBlock, nrm);
     else
-        stream_rows<QB, false, S, M, 3, kRefill, kNorm, NB, kXFirst>(b, x, K, smem,
-                                                                     (blockIdx.x - blocks_a) * kWavesPerBlock + wave,
-                                                                     (gridDim.x - blocks_a) * kWavesPerBlock, nrm);
+        stream_rows<QB, false, S, M, 3, kRefill, kNorm, NB>(b, x, K, smem,
+                                                            (blockIdx.x - blocks_a) * kWavesPerBlock + wave,
+                                                            (gridDim.x - blocks_a) * kWavesPerBlock, nrm);
 }
 
 // ffn_gate and ffn_up GEMVs plus SwiGLU in one launch (the reference's two
@@ -861,13 +853,12 @@ void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int
     if constexpr (S == 1) {
         if (na + nbr <= 8192) {
             // one pass, two rows per wave (attn_q/k/v at hidden 4096: measured
-            // faster than streaming), three workgroups per CU, x first
-            // (config 5: 619 against 617 tok/s)
+            // faster than streaming)
             constexpr int kM = 2;
             const int ga = (na + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
             const int gb = (nbr + kM * kWavesPerBlock - 1) / (kM * kWavesPerBlock);
-            launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false, kNorm, NB, true>), dim3(ga + gb), dim3(kBlock),
-                          lds, stream, a, b, ga, x, K, nrm);
+            launch_kernel((matvec_group_kernel<Q4K, Q6K, 1, kM, false, kNorm, NB>), dim3(ga + gb), dim3(kBlock), lds,
+                          stream, a, b, ga, x, K, nrm);
             return;
         }
     }
