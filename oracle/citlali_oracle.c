@@ -249,33 +249,92 @@ void orc_dequant_q6k_f32(const uint8_t* blocks, uint64_t count, float* out) {
  * GEMV
  * ------------------------------------------------------------------------ */
 
-/* kernels.cu:195-251 / 253-291 / 293-338: y[row] = sum over the row's
- * super-blocks of value(e) * x[256*b + e], weights kept in fp32 (never
- * rounded to fp16).  Accumulated here in double. */
-void orc_matvec_q4k(const uint8_t* w, const uint16_t* x, double* y, int in_f, int out_f, int nthreads) {
-    const int nb = in_f / ORC_QK;
-    #pragma omp parallel for schedule(static) num_threads(pick_threads(nthreads))
-    for (int r = 0; r < out_f; ++r) {
-        double acc = 0.0;
-        const uint8_t* row = w + (size_t)r * nb * ORC_Q4K_BYTES;
-        for (int b = 0; b < nb; ++b)
-            for (int e = 0; e < ORC_QK; ++e)
-                acc += (double)q4k_value(row + (size_t)b * ORC_Q4K_BYTES, e) * (double)orc_h2f(x[b * ORC_QK + e]);
-        y[r] = acc;
+/* All 256 values of one block, q4k_value(blk, e) for e = 0..255, with the
+ * block's d, dmin and (scale, min) pairs read once per block instead of once
+ * per value.  Same fp32 expressions, so the same values. */
+static void q4k_block_values(const uint8_t* blk, float* out) {
+    const float d = blk_half(blk), dmin = blk_half(blk + 2);
+    for (int j = 0; j < 4; ++j) {
+        uint8_t sc0, m0, sc1, m1;
+        orc_q4k_scale_min(2 * j, blk + 4, &sc0, &m0);
+        orc_q4k_scale_min(2 * j + 1, blk + 4, &sc1, &m1);
+        const float ds0 = d * (float)sc0, mm0 = dmin * (float)m0;
+        const float ds1 = d * (float)sc1, mm1 = dmin * (float)m1;
+        const uint8_t* qs = blk + 16 + 32 * j;
+        for (int i = 0; i < 32; ++i) {
+            out[64 * j + i] = ds0 * (float)(qs[i] & 0x0f) - mm0;
+            out[64 * j + 32 + i] = ds1 * (float)(qs[i] >> 4) - mm1;
+        }
     }
 }
 
-void orc_matvec_q6k(const uint8_t* w, const uint16_t* x, double* y, int in_f, int out_f, int nthreads) {
+/* q6k_value(blk, e) for e = 0..255 (e = 128h + 32part + i). */
+static void q6k_block_values(const uint8_t* blk, float* out) {
+    const float d = blk_half(blk + 208);
+    const int8_t* sc = (const int8_t*)(blk + 192);
+    for (int h = 0; h < 2; ++h)
+        for (int part = 0; part < 4; ++part)
+            for (int i = 0; i < 32; ++i) {
+                const uint8_t lb = blk[64 * h + 32 * (part & 1) + i];
+                const int lo = part < 2 ? (lb & 0x0f) : (lb >> 4);
+                const int hi2 = (blk[128 + 32 * h + i] >> (2 * part)) & 3;
+                const int q = (lo | (hi2 << 4)) - 32;
+                out[128 * h + 32 * part + i] = (d * (float)sc[8 * h + i / 16 + 2 * part]) * (float)q;
+            }
+}
+
+/* kernels.cu:195-251 / 253-291 / 293-338: y[row] = sum over the row's
+ * super-blocks of value(e) * x[256*b + e], weights kept in fp32 (never
+ * rounded to fp16).  Accumulated here in double, one running sum per row in
+ * element order: acc += w*x with the product exact in double (24 + 11
+ * significant bits) and the add the only rounding, so the result depends
+ * on nothing but that order.  Four rows are decoded and summed side by side
+ * (each with its own sum) so the adds of different rows overlap. */
+#define ORC_ROW_GROUP 4
+static void matvec_kquant(int q6, const uint8_t* w, const uint16_t* x, double* y, int in_f, int out_f, int nthreads) {
     const int nb = in_f / ORC_QK;
+    const size_t bb = q6 ? ORC_Q6K_BYTES : ORC_Q4K_BYTES;
+    double* xd = (double*)malloc((size_t)(in_f > 0 ? in_f : 1) * sizeof(double));
+    for (int k = 0; k < in_f; ++k) xd[k] = (double)orc_h2f(x[k]);
+    const int groups = (out_f + ORC_ROW_GROUP - 1) / ORC_ROW_GROUP;
     #pragma omp parallel for schedule(static) num_threads(pick_threads(nthreads))
-    for (int r = 0; r < out_f; ++r) {
-        double acc = 0.0;
-        const uint8_t* row = w + (size_t)r * nb * ORC_Q6K_BYTES;
-        for (int b = 0; b < nb; ++b)
-            for (int e = 0; e < ORC_QK; ++e)
-                acc += (double)q6k_value(row + (size_t)b * ORC_Q6K_BYTES, e) * (double)orc_h2f(x[b * ORC_QK + e]);
-        y[r] = acc;
+    for (int g = 0; g < groups; ++g) {
+        const int r0 = g * ORC_ROW_GROUP;
+        const int nr = out_f - r0 < ORC_ROW_GROUP ? out_f - r0 : ORC_ROW_GROUP;
+        float v[ORC_ROW_GROUP][ORC_QK];
+        double acc[ORC_ROW_GROUP] = {0.0, 0.0, 0.0, 0.0};
+        for (int b = 0; b < nb; ++b) {
+            for (int r = 0; r < nr; ++r) {
+                const uint8_t* blk = w + ((size_t)(r0 + r) * nb + b) * bb;
+                if (q6) q6k_block_values(blk, v[r]);
+                else q4k_block_values(blk, v[r]);
+            }
+            const double* xb = xd + (size_t)b * ORC_QK;
+            if (nr == ORC_ROW_GROUP) {
+                double a0 = acc[0], a1 = acc[1], a2 = acc[2], a3 = acc[3];
+                for (int e = 0; e < ORC_QK; ++e) {
+                    a0 += (double)v[0][e] * xb[e];
+                    a1 += (double)v[1][e] * xb[e];
+                    a2 += (double)v[2][e] * xb[e];
+                    a3 += (double)v[3][e] * xb[e];
+                }
+                acc[0] = a0; acc[1] = a1; acc[2] = a2; acc[3] = a3;
+            } else {
+                for (int r = 0; r < nr; ++r)
+                    for (int e = 0; e < ORC_QK; ++e) acc[r] += (double)v[r][e] * xb[e];
+            }
+        }
+        for (int r = 0; r < nr; ++r) y[r0 + r] = acc[r];
     }
+    free(xd);
+}
+
+void orc_matvec_q4k(const uint8_t* w, const uint16_t* x, double* y, int in_f, int out_f, int nthreads) {
+    matvec_kquant(0, w, x, y, in_f, out_f, nthreads);
+}
+
+void orc_matvec_q6k(const uint8_t* w, const uint16_t* x, double* y, int in_f, int out_f, int nthreads) {
+    matvec_kquant(1, w, x, y, in_f, out_f, nthreads);
 }
 
 /* CPU baseline (i): the reference's host arithmetic -- repo dequant of the
@@ -531,10 +590,12 @@ static void linear(const OrcMatrix* w, const uint16_t* bias, const uint16_t* x, 
     if (bias) orc_add_inplace(y, bias, out_f);
 }
 
-int32_t orc_forward_token(const OrcModel* m, uint16_t* const* caches, int32_t token, int position, float* logits) {
+/* The embedding and every layer of one step (qwen_model.cpp:256-374): the
+ * caches gain this position and x (hidden fp16) holds the residual stream
+ * that the final norm reads. */
+static void forward_layers(const OrcModel* m, uint16_t* const* caches, int32_t token, int position, uint16_t* x) {
     const int H = m->hidden, hd = m->head_dim, nq = m->heads * hd, nkv = m->kv_heads * hd, ff = m->ff;
-    const size_t big = (size_t)(m->vocab > ff ? m->vocab : ff) + (size_t)nq + H;
-    uint16_t* x = (uint16_t*)malloc((size_t)H * 2);
+    const size_t big = (size_t)ff + (size_t)nq + H;
     uint16_t* norm = (uint16_t*)malloc((size_t)H * 2);
     uint16_t* q = (uint16_t*)malloc((size_t)nq * 2);
     uint16_t* k = (uint16_t*)malloc((size_t)nkv * 2);
@@ -576,7 +637,16 @@ int32_t orc_forward_token(const OrcModel* m, uint16_t* const* caches, int32_t to
         linear(&L->down, L->down_bias, act, ff, H, proj, tmp);
         orc_add_inplace(x, proj, H);
     }
+    free(norm); free(q); free(k); free(v); free(att); free(proj);
+    free(gate); free(up); free(act); free(tmp);
+}
 
+int32_t orc_forward_token(const OrcModel* m, uint16_t* const* caches, int32_t token, int position, float* logits) {
+    const int H = m->hidden;
+    uint16_t* x = (uint16_t*)malloc((size_t)H * 2);
+    uint16_t* norm = (uint16_t*)malloc((size_t)H * 2);
+    double* tmp = (double*)malloc((size_t)m->vocab * sizeof(double));
+    forward_layers(m, caches, token, position, x);
     /* final norm, fp32 logits, greedy pick (qwen_model.cpp:385-419, 448-465) */
     orc_rms_norm(x, m->output_norm, norm, H, m->eps);
     matvec_any(&m->output, norm, tmp, H, m->vocab);
@@ -584,7 +654,12 @@ int32_t orc_forward_token(const OrcModel* m, uint16_t* const* caches, int32_t to
     for (int i = 0; i < m->vocab; ++i) lg[i] = (float)tmp[i];
     const int32_t next = orc_argmax(lg, m->vocab);
     if (!logits) free(lg);
-    free(x); free(norm); free(q); free(k); free(v); free(att); free(proj);
-    free(gate); free(up); free(act); free(tmp);
+    free(x); free(norm); free(tmp);
     return next;
+}
+
+void orc_prefill_token(const OrcModel* m, uint16_t* const* caches, int32_t token, int position) {
+    uint16_t* x = (uint16_t*)malloc((size_t)m->hidden * 2);
+    forward_layers(m, caches, token, position, x);
+    free(x);
 }

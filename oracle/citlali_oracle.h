@@ -131,6 +131,9 @@ typedef struct {
  * (k0, v0, k1, v1, ...).  logits (vocab floats) may be NULL.  Returns the
  * greedy token of the fp32 logits (orc_argmax rule). */
 int32_t orc_forward_token(const OrcModel* m, uint16_t* const* caches, int32_t token, int position, float* logits);
+/* The same step without the final norm and output GEMV: for prompt positions
+ * whose logits nobody reads (the caches are filled identically). */
+void orc_prefill_token(const OrcModel* m, uint16_t* const* caches, int32_t token, int position);
 
 /* ---- misc ---------------------------------------------------------------- */
 int orc_num_threads(void);

@@ -1,16 +1,21 @@
-// make_cfg5_greedy.cpp -- writes tests/golden/cfg5_greedy.txt: the oracle's
-// greedy decode of BASELINE config 5's synthetic Qwen3-8B (36 layers, each
-// with its own weights, hidden 4096, FFN 12288, 32/8 heads, vocab 151936,
-// Q4_K_M types; the recipe of csrc/bench/synth_qwen3.hpp, model seed 1):
-// an 8-token prompt, then 64 greedy steps, with each step's top-2 logits.
-// The GPU test (tests/cpp/test_host_layer cfg5) builds the same model in
-// QwenModel and must reproduce every token id.
+// make_cfg5_greedy.cpp -- writes the config-5 greedy fixtures
+// (tests/golden/cfg5_greedy*.txt): the oracle's greedy decode of BASELINE
+// config 5's synthetic Qwen3-8B (36 layers, each with its own weights,
+// hidden 4096, FFN 12288, 32/8 heads, vocab 151936, Q4_K_M types; the recipe
+// of csrc/bench/synth_qwen3.hpp, model seed 1): a prompt of seeded random
+// ids, then greedy steps, with each step's top-2 logits.  The GPU test
+// (tests/cpp/test_host_layer cfg5) builds the same model in QwenModel and
+// must reproduce every token id.
 //
 // The oracle (oracle/citlali_oracle.c, orc_forward_token) follows
-// qwen_model.cpp:239-419 with its fp16 store points, accumulating in double.
+// qwen_model.cpp:239-419 with its fp16 store points, accumulating in double;
+// prompt positions before the last run orc_prefill_token (no logits), as
+// the session's prompt loop asks forward_token for no logits there.
 //
 // usage:
-//   make_cfg5_greedy write PATH [PROMPT_SEED]   the fixture (PROMPT_SEED default 1)
+//   make_cfg5_greedy write PATH [PROMPT_SEED [PROMPT_LEN [STEPS]]]
+//       the fixture (defaults: seed 1, 8 prompt tokens, 64 steps; BASELINE
+//       config 5 itself is 512 and 256, the benchmark's prompt is seed 1)
 //   make_cfg5_greedy probe GAIN STEPS [LAYERS]  sensitivity of the recipe with
 //       attn_output / ffn_down gain GAIN: the oracle against itself with half
 //       of the embedding values moved by one fp16 ulp, teacher-forced, per
@@ -30,7 +35,7 @@
 namespace {
 
 constexpr uint64_t kModelSeed = 1;
-constexpr int kPrompt = 8, kSteps = 64;
+constexpr int kPrompt = 8;   // the probe's prompt
 
 struct Model {
     const citlali::bench::Qwen3Shape& shape = citlali::bench::kConfig5;
@@ -113,10 +118,14 @@ Top2 top2(const std::vector<float>& lg) {
     return t;
 }
 
-int write_fixture(const char* path, uint64_t prompt_seed) {
-    Model model(citlali::bench::kLayerOutGain, citlali::bench::kConfig5.layers, kPrompt + kSteps);
+int write_fixture(const char* path, uint64_t prompt_seed, int n_prompt, int n_steps) {
+    if (n_prompt < 1 || n_steps < 1) {
+        std::fprintf(stderr, "prompt length and steps must be positive\n");
+        return 2;
+    }
+    Model model(citlali::bench::kLayerOutGain, citlali::bench::kConfig5.layers, n_prompt + n_steps);
     Caches caches(model.m);
-    const std::vector<int32_t> prompt = citlali::bench::prompt_ids(prompt_seed, kPrompt, model.shape.vocab);
+    const std::vector<int32_t> prompt = citlali::bench::prompt_ids(prompt_seed, n_prompt, model.shape.vocab);
     std::vector<float> lg(model.shape.vocab);
     std::FILE* f = std::fopen(path, "w");
     if (!f) {
@@ -126,31 +135,42 @@ int write_fixture(const char* path, uint64_t prompt_seed) {
     std::fprintf(f, "# oracle greedy decode, BASELINE config 5 synthetic Qwen3-8B (model seed %llu, "
                     "attn_output/ffn_down gain %.3g), written by tests/golden/make_cfg5_greedy\n",
                  (unsigned long long)kModelSeed, citlali::bench::kLayerOutGain);
-    std::fprintf(f, "prompt_seed %llu\nprompt %d", (unsigned long long)prompt_seed, kPrompt);
+    std::fprintf(f, "prompt_seed %llu\nprompt %d", (unsigned long long)prompt_seed, n_prompt);
     for (int32_t t : prompt) std::fprintf(f, " %d", t);
-    std::fprintf(f, "\nsteps %d\n# step id logit second_id second_logit rms_logits\n", kSteps);
+    std::fprintf(f, "\nsteps %d\n# step id logit second_id second_logit rms_logits\n", n_steps);
     int32_t tok = 0;
     double min_margin = 1e30;
+    int min_step = 0;
     const auto t0 = std::chrono::steady_clock::now();
-    for (int p = 0; p < kPrompt + kSteps; ++p) {
-        const int32_t in = p < kPrompt ? prompt[p] : tok;
+    const auto secs = [&] { return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count(); };
+    for (int p = 0; p < n_prompt + n_steps - 1; ++p) {
+        const int32_t in = p < n_prompt ? prompt[p] : tok;
+        if (p < n_prompt - 1) {
+            orc_prefill_token(&model.m, caches.p.data(), in, p);
+            if ((p + 1) % 64 == 0) {
+                std::printf("prompt position %d (%.0f s)\n", p, secs());
+                std::fflush(stdout);
+            }
+            continue;
+        }
         tok = orc_forward_token(&model.m, caches.p.data(), in, p, lg.data());
-        if (p < kPrompt - 1) continue;
         const Top2 t = top2(lg);
         if (t.a != tok) {
             std::fprintf(stderr, "top-2 scan disagrees with orc_argmax at position %d\n", p);
             return 1;
         }
-        const int step = p - (kPrompt - 1);   // the token this position picks is greedy step `step`
-        if (step >= kSteps) break;
+        const int step = p - (n_prompt - 1);   // the token this position picks is greedy step `step`
         std::fprintf(f, "%d %d %.9g %d %.9g %.9g\n", step, t.a, t.va, t.b, t.vb, t.rms);
-        min_margin = std::min(min_margin, (t.va - t.vb) / t.rms);
-        std::printf("step %2d: id %6d margin / rms %.3e (%.0f s)\n", step, t.a, (t.va - t.vb) / t.rms,
-                    std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count());
+        std::fflush(f);
+        if ((t.va - t.vb) / t.rms < min_margin) {
+            min_margin = (t.va - t.vb) / t.rms;
+            min_step = step;
+        }
+        std::printf("step %3d: id %6d margin / rms %.3e (%.0f s)\n", step, t.a, (t.va - t.vb) / t.rms, secs());
         std::fflush(stdout);
     }
     std::fclose(f);
-    std::printf("wrote %s: min top-2 margin / rms = %.3e\n", path, min_margin);
+    std::printf("wrote %s: min top-2 margin / rms = %.3e (step %d)\n", path, min_margin, min_step);
     return 0;
 }
 
@@ -187,9 +207,11 @@ int probe(double gain, int steps, int n_layers) {
 
 int main(int argc, char** argv) {
     const std::string mode = argc > 1 ? argv[1] : "";
-    if (mode == "write" && argc >= 3) return write_fixture(argv[2], argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 1);
+    if (mode == "write" && argc >= 3)
+        return write_fixture(argv[2], argc > 3 ? std::strtoull(argv[3], nullptr, 10) : 1,
+                             argc > 4 ? std::atoi(argv[4]) : 8, argc > 5 ? std::atoi(argv[5]) : 64);
     if (mode == "probe" && argc >= 4)
         return probe(std::atof(argv[2]), std::atoi(argv[3]), argc > 4 ? std::atoi(argv[4]) : citlali::bench::kConfig5.layers);
-    std::fprintf(stderr, "usage: %s write PATH [PROMPT_SEED] | probe GAIN STEPS [LAYERS]\n", argv[0]);
+    std::fprintf(stderr, "usage: %s write PATH [PROMPT_SEED [PROMPT_LEN [STEPS]]] | probe GAIN STEPS [LAYERS]\n", argv[0]);
     return 2;
 }
