@@ -12,7 +12,7 @@
 //                         loop.
 //   test_host_layer gguf  QwenModel loaded from a GGUF file of the model.
 //   test_host_layer cfg5 FIXTURE   BASELINE config 5's full Qwen3-8B shape:
-//                         64 greedy tokens equal the oracle's fixture.
+//                         the fixture's greedy tokens equal the oracle's.
 // Prints one line per check and exits non-zero on the first failure.
 #include "citlali/common.h"
 #include "citlali/compute/common/dtype.h"
@@ -596,6 +596,144 @@ void test_oracle_forward_pins() {
     h1.step(9, 1, a.data());
     h2.step(9, 1, b.data());
     check(a != b, "the cache feeds attention");
+
+    // The closed forms below recompute one layer from the separately pinned
+    // routines (embed, rms_norm, the GEMVs, swiglu, add) with one branch made
+    // trivial, so a wiring slip in the composition fails them: the residual
+    // added to the wrong buffer, a norm taking the other norm's weight,
+    // gate/up exchanged, the attention range off by one, RoPE before the
+    // q/k norm.  fp16 roundings here go by way of float, so values are
+    // compared to a bound (1 ulp for cache rows, 5e-3 of the logit rms).
+    const int H = 1024, V = 512, NQ = 8 * 128, NKV = 4 * 128, F = 2048, group = 2;
+    const float eps = s.cfg.rms_norm_eps;
+    const auto f16 = [](const std::vector<double>& v) {
+        std::vector<uint16_t> h(v.size());
+        for (size_t i = 0; i < v.size(); ++i) h[i] = orc_f2h_rne((float)v[i]);
+        return h;
+    };
+    const auto embed = [&](int tok) {
+        std::vector<uint16_t> e(H);
+        orc_embed_q6k(s.embd.bytes.data(), tok, e.data(), H);
+        return e;
+    };
+    const auto gemv = [](const HostMatrix& w, const std::vector<uint16_t>& x) {
+        std::vector<double> y(w.rows);
+        if (w.type == GgufTensorType::Q4_K) {
+            orc_matvec_q4k(w.bytes.data(), x.data(), y.data(), w.cols, w.rows, 0);
+        } else {
+            orc_matvec_q6k(w.bytes.data(), x.data(), y.data(), w.cols, w.rows, 0);
+        }
+        return y;
+    };
+    const auto norm = [&](const std::vector<uint16_t>& x, const std::vector<uint16_t>& w) {
+        std::vector<uint16_t> n(x.size());
+        orc_rms_norm(x.data(), w.data(), n.data(), (int)x.size(), eps);
+        return n;
+    };
+    const auto logit_err = [&](const std::vector<float>& got, const std::vector<uint16_t>& x) {
+        const std::vector<double> want = gemv(s.output, norm(x, s.output_norm));
+        double e = 0, ss = 0;
+        for (int i = 0; i < V; ++i) {
+            e = std::max(e, std::fabs(got[i] - want[i]));
+            ss += want[i] * want[i];
+        }
+        return e / std::sqrt(ss / V);
+    };
+    const auto within_ulp = [](uint16_t got, double want) {
+        return std::fabs(orc_h2f(got) - want) <= std::ldexp(std::fabs(want), -10) + 1e-7;
+    };
+    const std::vector<int> seq = {4, 9, 100, 33, 250, 71};
+
+    // (4) attn_q zero: q = 0 after its norm and RoPE, every score is 0 and
+    // attention is the mean of V over positions 0..pos inclusive; with
+    // ffn_down zero the layer adds o(mean V) to the residual stream only.
+    SynthModel qz = s;
+    std::fill(qz.layers[0].q.bytes.begin(), qz.layers[0].q.bytes.end(), 0);
+    std::fill(qz.layers[0].down.bytes.begin(), qz.layers[0].down.bytes.end(), 0);
+    OracleModel oq(qz, ctx, 1);
+    std::vector<std::vector<uint16_t>> vrows;
+    for (int p = 0; p < (int)seq.size(); ++p) {
+        oq.step(seq[p], p, a.data());
+        const std::vector<uint16_t> x0 = embed(seq[p]);
+        const std::vector<double> v = gemv(s.layers[0].v, norm(x0, s.layers[0].attn_norm));
+        const uint16_t* vc = oq.caches[1].data() + (size_t)p * NKV;
+        bool row_ok = true;
+        for (int i = 0; i < NKV; ++i) row_ok = row_ok && within_ulp(vc[i], v[i]);
+        check(row_ok, "V cache row " + std::to_string(p) + " = v(attn_norm(embed))");
+        vrows.push_back(f16(v));
+        std::vector<double> att(NQ, 0.0);
+        for (int h = 0; h < 8; ++h)
+            for (int d = 0; d < 128; ++d) {
+                double sum = 0;
+                for (int t = 0; t <= p; ++t) sum += orc_h2f(vrows[t][(h / group) * 128 + d]);
+                att[h * 128 + d] = sum / (p + 1);
+            }
+        const std::vector<uint16_t> proj = f16(gemv(s.layers[0].o, f16(att)));
+        std::vector<uint16_t> x1 = x0;
+        orc_add_inplace(x1.data(), proj.data(), H);
+        const double e = logit_err(a, x1);
+        check(e < 5e-3, "attn_q zero, position " + std::to_string(p) +
+                            ": logits = output(norm(embed + o(mean of V[0..pos]))), error / rms " + std::to_string(e));
+    }
+
+    // (5) attn_o zero: the layer adds down(silu(gate(n)) * up(n)) with
+    // n = rms_norm(x, ffn_norm) -- the FFN's norm weight and operand order.
+    SynthModel oz2 = s;
+    std::fill(oz2.layers[0].o.bytes.begin(), oz2.layers[0].o.bytes.end(), 0);
+    OracleModel of(oz2, ctx, 1);
+    for (int p = 0; p < 3; ++p) {
+        of.step(seq[p], p, a.data());
+        const std::vector<uint16_t> x0 = embed(seq[p]);
+        const std::vector<uint16_t> n = norm(x0, s.layers[0].ffn_norm);
+        const std::vector<uint16_t> g = f16(gemv(s.layers[0].gate, n)), u = f16(gemv(s.layers[0].up, n));
+        std::vector<uint16_t> act(F);
+        orc_swiglu(g.data(), u.data(), act.data(), F);
+        const std::vector<uint16_t> dn = f16(gemv(s.layers[0].down, act));
+        std::vector<uint16_t> x1 = x0;
+        orc_add_inplace(x1.data(), dn.data(), H);
+        const double e = logit_err(a, x1);
+        check(e < 5e-3, "attn_o zero, position " + std::to_string(p) +
+                            ": logits = output(norm(embed + down(swiglu(gate, up)(ffn_norm)))), error / rms " +
+                            std::to_string(e));
+    }
+
+    // (6) RoPE acts after the k norm, V is not rotated: layer 0's k and v of
+    // a token depend only on the token, so its cache rows at position P are
+    // its rows at position 0 with each pair (i, i + 64) of K rotated by
+    // P * theta^(-2i/128).  The other order -- RoPE on the raw k, then the
+    // norm with this model's uneven k_norm weights -- misses by far more.
+    const int P = 5, tok = 71;
+    OracleModel o0(s, ctx, 1), oP(s, ctx, 1);
+    o0.step(tok, 0, a.data());
+    for (int p = 0; p <= P; ++p) oP.step(p < P ? seq[p] : tok, p, b.data());
+    const uint16_t* k0 = o0.caches[0].data();
+    const uint16_t* kP = oP.caches[0].data() + (size_t)P * NKV;
+    check(std::memcmp(o0.caches[1].data(), oP.caches[1].data() + (size_t)P * NKV, NKV * 2) == 0,
+          "V cache row of a token is the same at positions 0 and 5");
+    const std::vector<double> kraw = gemv(s.layers[0].k, norm(embed(tok), s.layers[0].attn_norm));
+    const std::vector<uint16_t> kraw16 = f16(kraw);
+    bool rot_ok = true;
+    double other = 0;
+    for (int h = 0; h < 4; ++h) {
+        // the other order: rotate the raw k, then rms-normalise with k_norm
+        std::vector<double> r(128);
+        for (int i = 0; i < 64; ++i) {
+            const double ang = P * std::pow((double)s.cfg.rope_theta, -2.0 * i / 128.0);
+            const double x0 = orc_h2f(k0[h * 128 + i]), x1 = orc_h2f(k0[h * 128 + 64 + i]);
+            rot_ok = rot_ok && within_ulp(kP[h * 128 + i], x0 * std::cos(ang) - x1 * std::sin(ang)) &&
+                     within_ulp(kP[h * 128 + 64 + i], x0 * std::sin(ang) + x1 * std::cos(ang));
+            const double y0 = orc_h2f(kraw16[h * 128 + i]), y1 = orc_h2f(kraw16[h * 128 + 64 + i]);
+            r[i] = y0 * std::cos(ang) - y1 * std::sin(ang);
+            r[64 + i] = y0 * std::sin(ang) + y1 * std::cos(ang);
+        }
+        double ss = 0;
+        for (double v : r) ss += v * v;
+        const double inv = 1.0 / std::sqrt(ss / 128 + eps);
+        for (int i = 0; i < 128; ++i)
+            other = std::max(other, std::fabs(r[i] * inv * orc_h2f(s.layers[0].k_norm[i]) - orc_h2f(kP[h * 128 + i])));
+    }
+    check(rot_ok, "K cache row at position 5 = its position-0 row rotated by RoPE (norm, then RoPE)");
+    check(other > 0.05, "RoPE-then-norm would differ from the oracle's K row by " + std::to_string(other));
     std::printf("oracle forward pins ok\n");
 }
 
@@ -810,27 +948,37 @@ void test_long_context_buckets() {
 // BASELINE config 5 at its full shape: the benchmark's synthetic Qwen3-8B
 // (csrc/bench/synth_qwen3.hpp, model seed 1: 36 layers with their own
 // weights, hidden 4096, FFN 12288, 32/8 heads, vocab 151936, Q4_K_M types)
-// decodes the fixture's 8-token prompt, then 64 greedy steps free-running;
-// every token must equal the oracle's (tests/golden/cfg5_greedy.txt, written
-// by tests/golden/make_cfg5_greedy), through the forward_token loop and
-// through the graph-replayed decode_greedy.  The GPU's top-2 logits are
-// logged against the oracle's, with the oracle's smallest top-2 margin.
+// decodes the fixture's prompt (forward_token without logits but at its last
+// position, as the session's prompt loop does), then its greedy steps
+// free-running; every token must equal the oracle's
+// (tests/golden/cfg5_greedy*.txt, written by tests/golden/make_cfg5_greedy),
+// through the forward_token loop and through the graph-replayed
+// decode_greedy.  The GPU's logits at the oracle's top-2 tokens are logged
+// against the oracle's; a differing pick reports that step's GPU logit error
+// beside the oracle's top-2 margin, so a near-tie resolved the other way
+// reads differently from a wrong result.
 void test_config5_greedy(const std::string& fixture) {
     std::FILE* f = std::fopen(fixture.c_str(), "r");
     check(f != nullptr, "open " + fixture);
     std::vector<int32_t> prompt, ids, second;
     std::vector<double> top, top2, rms;
-    char line[512];
-    while (std::fgets(line, sizeof line, f)) {
+    int want_steps = -1;
+    std::vector<char> buf(1 << 16);
+    while (std::fgets(buf.data(), (int)buf.size(), f)) {
+        const char* line = buf.data();
         if (line[0] == '#' || line[0] == '\n') continue;
-        if (std::strncmp(line, "prompt_seed", 11) == 0 || std::strncmp(line, "steps", 5) == 0) continue;
+        if (std::strncmp(line, "prompt_seed", 11) == 0) continue;
+        if (std::strncmp(line, "steps", 5) == 0) {
+            want_steps = std::atoi(line + 5);
+            continue;
+        }
         if (std::strncmp(line, "prompt", 6) == 0) {
-            int n = 0, off = 0, used = 0;
+            int n = 0, used = 0;
             std::sscanf(line + 6, "%d%n", &n, &used);
-            off = 6 + used;
+            int off = 6 + used;
             for (int i = 0; i < n; ++i) {
                 int32_t t = 0;
-                std::sscanf(line + off, "%d%n", &t, &used);
+                check(std::sscanf(line + off, "%d%n", &t, &used) == 1, "fixture prompt id " + std::to_string(i));
                 off += used;
                 prompt.push_back(t);
             }
@@ -848,7 +996,8 @@ void test_config5_greedy(const std::string& fixture) {
         }
     }
     std::fclose(f);
-    check(prompt.size() == 8 && ids.size() == 64, "fixture holds an 8-token prompt and 64 steps");
+    const int P = (int)prompt.size(), S = (int)ids.size();
+    check(P > 0 && S > 1 && S == want_steps, "fixture holds a prompt and all of its steps");
 
     namespace bq = citlali::bench;
     const bq::Qwen3Shape& shape = bq::kConfig5;
@@ -886,7 +1035,7 @@ void test_config5_greedy(const std::string& fixture) {
         L.down = {Q6, H, F, std::move(b.down)};
         s.layers.push_back(std::move(L));
     }
-    const int ctx = 8 + 64;
+    const int ctx = P + S;
     model::QwenModel gpu;
     gpu.load(s.cfg, device_weights(s), ctx);
     s.layers.clear();
@@ -895,36 +1044,43 @@ void test_config5_greedy(const std::string& fixture) {
     int32_t tok = 0;
     std::vector<int32_t> got;
     double worst = 0, min_margin = 1e30;
-    int worst_step = 0;
-    for (int p = 0; p < 8 + 63; ++p) {
-        tok = gpu.forward_token(p < 8 ? prompt[p] : tok, (uint32_t)p);
-        if (p < 7) continue;
-        const int step = p - 7;
+    int worst_step = 0, min_step = 0;
+    for (int p = 0; p < P + S - 1; ++p) {
+        tok = gpu.forward_token(p < P ? prompt[p] : tok, (uint32_t)p, p >= P - 1);
+        if (p < P - 1) continue;
+        const int step = p - (P - 1);
         gpu.logits()->copy_to_host(lg.data(), lg.size() * 4);
         got.push_back(tok);
         // the GPU's logits of the oracle's two best tokens against the oracle's
         const double e = std::max(std::fabs(lg[ids[step]] - top[step]), std::fabs(lg[second[step]] - top2[step]));
+        const double margin = (top[step] - top2[step]) / rms[step];
         if (e / rms[step] > worst) {
             worst = e / rms[step];
             worst_step = step;
         }
-        min_margin = std::min(min_margin, (top[step] - top2[step]) / rms[step]);
-        check(tok == ids[step], "config 5 greedy step " + std::to_string(step) + ": gpu " + std::to_string(tok) +
-                                    " oracle " + std::to_string(ids[step]) + " (oracle margin / rms " +
-                                    std::to_string((top[step] - top2[step]) / rms[step]) + ")");
-        std::printf("  step %2d: id %6d ok; top-2 logits gpu %.6f %.6f oracle %.6f %.6f\n", step, tok, lg[ids[step]],
+        if (margin < min_margin) {
+            min_margin = margin;
+            min_step = step;
+        }
+        char why[256];
+        std::snprintf(why, sizeof why,
+                      "config 5 greedy step %d: gpu %d oracle %d (oracle top-2 margin / rms %.3e; gpu logit error "
+                      "at the oracle's top-2 tokens / rms %.3e, largest so far %.3e at step %d)",
+                      step, tok, ids[step], margin, e / rms[step], worst, worst_step);
+        check(tok == ids[step], why);
+        std::printf("  step %3d: id %6d ok; top-2 logits gpu %.6f %.6f oracle %.6f %.6f\n", step, tok, lg[ids[step]],
                     lg[second[step]], top[step], top2[step]);
         std::fflush(stdout);
     }
-    // the last step (63) through the graph-replayed decode: all 64 again
-    const std::vector<int32_t> g = gpu.decode_greedy(got[0], 8, 63);
+    // the last step through the graph-replayed decode: all steps again
+    const std::vector<int32_t> g = gpu.decode_greedy(got[0], (uint32_t)P, (uint32_t)(S - 1));
     std::vector<int32_t> all = {got[0]};
     all.insert(all.end(), g.begin(), g.end());
-    check(all == ids, "config 5: decode_greedy (graph replay) reproduces all 64 oracle tokens");
-    std::printf("config 5 (36 layers, hidden 4096, vocab 151936): 64 of 64 greedy tokens equal the oracle's, "
-                "forward_token loop and decode_greedy; max |logit error| / rms at the top-2 tokens %.2e (step %d); "
-                "min oracle top-2 margin / rms %.2e\n",
-                worst, worst_step, min_margin);
+    check(all == ids, "config 5: decode_greedy (graph replay) reproduces all " + std::to_string(S) + " oracle tokens");
+    std::printf("config 5 (36 layers, hidden 4096, vocab 151936, %d-token prompt): %d of %d greedy tokens equal the "
+                "oracle's, forward_token loop and decode_greedy; max |logit error| / rms at the top-2 tokens %.2e "
+                "(step %d); min oracle top-2 margin / rms %.2e (step %d)\n",
+                P, S, S, worst, worst_step, min_margin, min_step);
 }
 
 // ---- the synthetic model as a GGUF file ----------------------------------
@@ -1280,6 +1436,51 @@ void write_session_model(const std::string& tok_path, const std::string& path) {
     std::printf("wrote %s (vocab %d)\n", path.c_str(), vocab);
 }
 
+// CPU: the reference's load signatures with a RemoteOptions argument
+// (include/citlali/model/qwen_model.h:38-40, include/citlali/runtime/
+// session.h:39-42), called as the reference's session.cpp:15 and cli/main.cpp
+// call them.  Options that offload layers are refused before any weight
+// reaches the device; an out-of-range layer gets the reference's message.
+void test_remote_options() {
+    char exe[4096];
+    const ssize_t n = readlink("/proc/self/exe", exe, sizeof exe - 1);
+    check(n > 0, "locate the test program");
+    exe[n] = 0;
+    std::string dir(exe);
+    dir = dir.substr(0, dir.rfind('/'));
+    const std::string tok = dir + "/../golden/tokenizer/qwen_like.gguf";
+    const std::string path = "/tmp/citlali_remote_" + std::to_string(getpid()) + ".gguf";
+    write_session_model(tok, path);
+    io::GgufFile g;
+    g.load(path);
+
+    remote::RemoteOptions r;
+    r.endpoint = "127.0.0.1:9000";
+    r.transport = remote::Transport::Wifi6;
+    r.backend = remote::Backend::Hybrid;
+    r.layers = {1};
+    check(r.enabled() && r.offloads_layer(1) && !r.offloads_layer(0), "RemoteOptions::enabled / offloads_layer");
+    model::QwenModel m;
+    expect_error([&] { m.load(g, 0, true, r); }, "remote layer offload is not supported by this build",
+                 "QwenModel::load with a remote layer");
+    r.layers = {0, 7};
+    expect_error([&] { m.load(g, 0, true, r); }, "remote layer index is out of range: 7",
+                 "QwenModel::load with an out-of-range remote layer");
+    remote::RemoteOptions no_endpoint;
+    no_endpoint.layers = {0};
+    check(!no_endpoint.enabled(), "layers without an endpoint: not enabled");
+    expect_error([&] { m.load(g, 0, false, no_endpoint); }, "remote layer offload is not supported",
+                 "QwenModel::load with layers and no endpoint");
+    expect_error([&] { m.forward_token(0, 0); }, "model is not loaded", "a refused load loads nothing");
+
+    runtime::InferenceSession session;
+    r.layers = {0};
+    expect_error([&] { session.load_model(path, 2048, true, r); }, "remote layer offload is not supported",
+                 "InferenceSession::load_model with a remote layer");
+    std::remove(path.c_str());
+    std::printf("remote options ok\n");
+}
+
 // One InferenceSession generation, printed as "tokens N stop S text HEX".
 void session_text(const std::string& model, const std::string& prompt, uint32_t max_new, bool chat, bool quantized) {
     runtime::InferenceSession sess;
@@ -1308,6 +1509,7 @@ int main(int argc, char** argv) {
             test_dispatch_errors();
             test_oracle_forward_pins();
             test_model_load_errors();
+            test_remote_options();
         } else if (mode == "write_session_model") {
             check(argc > 3, "write_session_model TOKENIZER_GGUF OUT");
             write_session_model(argv[2], argv[3]);
