@@ -3,9 +3,9 @@
 // forward_token follows the reference's QwenModel::forward_token
 // (src/model/qwen_model.cpp:239-419) operation by operation, with its fp16
 // store points and output-weight rule, over the gfx950 compute:: launchers.
-// The weights arrive as WeightHandles (QwenWeights) instead of being read
-// from a GGUF file by the reference's load(); remote layer ranges are not
-// part of this build.  Greedy sampling picks the first largest finite logit
+// The weights arrive from a GGUF file (the reference's load()) or as
+// WeightHandles (QwenWeights); remote layer ranges are not part of this
+// build (a load that asks for them is refused).  Greedy sampling picks the first largest finite logit
 // (qwen_model.cpp:448-465) on the device and copies back one index.
 #pragma once
 
@@ -15,6 +15,7 @@
 #include "citlali/model/qwen_config.h"
 #include "citlali/model/weight_handle.h"
 #include "citlali/model/weight_loader.h"
+#include "citlali/remote/remote_client.h"
 
 #include <cstdint>
 #include <memory>
@@ -55,11 +56,18 @@ public:
     QwenModel(const QwenModel&) = delete;
     QwenModel& operator=(const QwenModel&) = delete;
 
-    // From a GGUF file, as the reference's load (qwen_model.cpp:45-186,
-    // remote layers aside): config by QwenConfig::from_gguf, tensors by their
-    // GGUF names through a WeightLoader (KeepQuantized when `quantized`,
-    // else DequantizeToFp16), then the load below.
-    void load(const io::GgufFile& gguf, uint32_t max_context = 0, bool quantized = false);
+    // From a GGUF file, as the reference's load (qwen_model.cpp:45-186):
+    // config by QwenConfig::from_gguf, tensors by their GGUF names through a
+    // WeightLoader (KeepQuantized when `quantized`, else DequantizeToFp16),
+    // then the load below.  remote_options keeps the reference's signature
+    // (include/citlali/model/qwen_model.h:38-40): options that offload
+    // layers (enabled(): an endpoint and a layer list) get the reference's
+    // range check ("remote layer index is out of range: N"), then
+    // citlali::Error, before any weight is read; a layer list without an
+    // endpoint is refused too (the reference would dereference a missing
+    // client).  Otherwise every layer runs on the GPU.
+    void load(const io::GgufFile& gguf, uint32_t max_context = 0, bool quantized = false,
+              const remote::RemoteOptions& remote_options = {});
     // max_context 0 -> min(context_length, 2048), as the reference.
     void load(const QwenConfig& config, QwenWeights weights, uint32_t max_context = 0);
     // Runs one token at `position`; returns the greedy next token, or -1

@@ -17,7 +17,8 @@
 // tokens, text, callbacks and stop reasons are the same.  A chunk may run up
 // to chunk - 1 steps past an EOS; those cache positions are rewritten by the
 // next prompt, which always starts at position 0.  Remote layers are not
-// part of this build.
+// part of this build: load_model passes its RemoteOptions to
+// QwenModel::load, which refuses any that offload layers.
 #pragma once
 
 #include "citlali/io/gguf_reader.h"
@@ -55,8 +56,10 @@ using TokenCallback = std::function<void(const std::string&)>;
 class InferenceSession {
 public:
     // GGUF file -> tokenizer + model (KeepQuantized when `quantized`), history
-    // cleared; a summary line goes to stderr (session.cpp:9-25).
-    void load_model(const std::string& model_path, uint32_t max_context = 2048, bool quantized = false);
+    // cleared; a summary line goes to stderr (session.cpp:9-25).  The
+    // signature is the reference's (include/citlali/runtime/session.h:39-42).
+    void load_model(const std::string& model_path, uint32_t max_context = 2048, bool quantized = false,
+                    const remote::RemoteOptions& remote_options = {});
 
     std::string generate_once(const std::string& prompt, const GenerationOptions& options,
                               const TokenCallback& on_token = {});

@@ -34,8 +34,18 @@ void add_bias_if_present(const WeightHandle& bias, const compute::DeviceBufferPt
 
 }  // namespace
 
-void QwenModel::load(const io::GgufFile& gguf, uint32_t max_context, bool quantized) {
+void QwenModel::load(const io::GgufFile& gguf, uint32_t max_context, bool quantized,
+                     const remote::RemoteOptions& remote_options) {
     const QwenConfig config = QwenConfig::from_gguf(gguf);
+    if (remote_options.enabled()) {
+        for (const uint32_t layer_index : remote_options.layers)
+            require(layer_index < config.block_count,
+                    "remote layer index is out of range: " + std::to_string(layer_index));
+    }
+    require(remote_options.layers.empty(),
+            "remote layer offload is not supported by this build (" + std::to_string(remote_options.layers.size()) +
+                " layer(s) requested" + (remote_options.endpoint.empty() ? ", no endpoint" : " at " + remote_options.endpoint) +
+                "): load with no remote layers");
     const WeightLoader loader(gguf, quantized ? WeightLoadPolicy::KeepQuantized : WeightLoadPolicy::DequantizeToFp16);
     const auto blk = [](uint32_t i, const char* suffix) { return "blk." + std::to_string(i) + "." + suffix; };
     QwenWeights w;

@@ -1,6 +1,6 @@
 // InferenceSession (the reference's src/runtime/session.cpp).
 //
-//   load_model                 session.cpp:9-25 (remote layers aside)
+//   load_model                 session.cpp:9-25 (remote layers refused by QwenModel::load)
 //   generate_* / chat_*        session.cpp:27-59
 //   generate_from_prompt_text  session.cpp:61-104
 #include "citlali/runtime/session.h"
@@ -12,11 +12,12 @@
 
 namespace citlali::runtime {
 
-void InferenceSession::load_model(const std::string& model_path, uint32_t max_context, bool quantized) {
+void InferenceSession::load_model(const std::string& model_path, uint32_t max_context, bool quantized,
+                                  const remote::RemoteOptions& remote_options) {
     std::cerr << "Reading GGUF: " << model_path << std::endl;
     gguf_.load(model_path);
     tokenizer_.load_from_gguf(gguf_);
-    model_.load(gguf_, max_context, quantized);
+    model_.load(gguf_, max_context, quantized, remote_options);
     history_.clear();
     const model::QwenConfig& c = config();
     std::cerr << "Model loaded. vocab=" << c.vocab_size << " layers=" << c.block_count
