@@ -80,7 +80,10 @@ Args parse(int argc, char** argv) {
         else if (f == "--prompt") a.prompt = value();
         else if (f == "--max-new-tokens") a.max_new_tokens = to_u32(f, value());
         else if (f == "--ctx" || f == "--context") a.max_context = to_u32(f, value());
-        else if (f == "--decode-chunk") a.decode_chunk = to_u32(f, value());
+        else if (f == "--decode-chunk") {
+            a.decode_chunk = to_u32(f, value());
+            if (a.decode_chunk < 1) throw citlali::Error("--decode-chunk must be at least 1");   // before any load
+        }
         else if (f == "--no-chat-template") a.chat = false;
         else if (f == "--interactive") a.interactive = true;
         else if (f == "--info") a.info = true;

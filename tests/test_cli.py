@@ -60,6 +60,9 @@ def test_usage_and_argument_errors():
                       (("--offload", "layer:0"), b"remote layer offload is not part of this build"),
                       (("--bogus",), b"unknown argument: --bogus"),
                       (("--max-new-tokens", "12x"), b"--max-new-tokens needs a number"),
+                      # refused while parsing, before any model file is opened
+                      (("--model", os.path.join(ROOT, "no_such_file.gguf"), "--decode-chunk", "0"),
+                       b"--decode-chunk must be at least 1"),
                       (("--model",), b"missing value for --model")):
         r = cli(*args)
         assert r.returncode == 1 and msg in r.stderr, (args, r.stderr)

@@ -91,6 +91,24 @@ def test_fused_long_context(hip, device_position):
             assert np.array_equal(a, b), (name, pos)
 
 
+@pytest.mark.parametrize("device_position", [False, True])
+def test_fused_row_loads(hip, device_position):
+    """Past 64K positions one sequence of 8 KV heads plans more than 512
+    (KV head, chunk) units, and the split kernel switches to its row-load form
+    (rows staged through LDS instead of direct loads), where the prologue
+    substitutes the step's k/v row into the staged K/V rows.  ctx 70000: the
+    plan is 69 chunks of 1024 (72 units of 8 KV heads would be 576)."""
+    ctx = 70000
+    for pos in (66000, 69999):
+        plan = hip.device.attention_plan_length(pos + 1, ctx)
+        chunk, splits = hip.device.attention_plan_info(plan, 1, 32, 8, 128)
+        assert 8 * splits > 512, (plan, chunk, splits)
+        ref, got = run_pair(hip, 32, 8, ctx, pos, 5 + pos, device_position)
+        for name, a, b in zip(("out", "k_cache", "v_cache"), ref, got):
+            assert np.array_equal(a, b), (name, pos)
+        assert not np.isnan(ref[0].view(np.float16)).any(), pos
+
+
 def test_fused_declines_other_shapes(hip):
     heads, kv_heads, hd, ctx = 8, 8, 128, 64
     z = hip.DeviceArray(heads * ctx * hd * 2)

@@ -69,5 +69,9 @@ def test_noalloc_rejects_plans_beyond_the_scratch():
     assert st == pycitlali._lib.ERR_INVALID
     msg = pycitlali.last_error()
     assert "scratch" in msg and str(64 * 512 * 132 * 4) in msg
-    # the largest plan of 32 query heads (512 chunks) fits
-    assert 32 * 512 * 132 * 4 <= 16 << 20
+    # every plan of up to 32 query heads fits: the library's own bound over
+    # every plan length up to the largest position it accepts
+    for bound in (L, 1 << 30, (1 << 31) - 1):
+        for hd in (128, 64):
+            assert dev.attention_workspace_bytes(bound, 1, 32, 8, hd) <= 16 << 20, (bound, hd)
+    assert dev.attention_workspace_bytes(L, 1, 64, 8, 128) > 16 << 20
