@@ -70,9 +70,6 @@ size_t split_lds_bytes() {
     return tiles > C::kMergeLds ? tiles : C::kMergeLds;
 }
 
-// the merge kernel keeps everything in registers
-constexpr size_t kMergeLds = 0;
-
 // Positions a sequence covers and its chunk count.  A position at or beyond
 // the caller's bound `max_len` is cut there, so neither the cache reads nor
 // the chunk index leave their buffers.
@@ -718,29 +715,31 @@ __global__ __launch_bounds__(NW * kWave, kRows ? 4 : 1) void attn_mfma_kernel(
     }
 }
 
-// Grid: (query head, seq).  Log-sum-exp merge of one head's chunk partials
-// ([chunk][HD + 4]: acc[HD], max, sum) in one global round trip, without
-// LDS: every wave finds the largest chunk max M (lane j reads the maxima of
-// chunks j, j + 64, ...) while thread (dim quad, subset g) loads the
-// accumulators and (max, sum) of its chunks g, g + kSub, ...; it folds them
-// with the factors exp2(max - M) in chunk order, and the kSub consecutive
-// lanes of a dim quad add their folds by DPP.
-template <int HD, int kBatch>
+// Grid: (query head x dim part, seq).  Log-sum-exp merge of one head's chunk
+// partials ([chunk][HD + 4]: acc[HD], max, sum) in one global round trip,
+// without LDS: a workgroup owns HD / kParts dims of one head; every wave
+// finds the largest chunk max M (lane j reads the maxima of chunks j,
+// j + 64, ...) while thread (dim quad, subset g) loads the accumulators and
+// (max, sum) of its chunks g, g + kSub, ...; it folds them with the factors
+// exp2(max - M) in chunk order, and the kSub consecutive lanes of a dim quad
+// add their folds by DPP.  More parts give more workgroups, each thread
+// fewer chunks.
+template <int HD, int kParts, int kBatch>
 __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restrict__ part,
                                                             const int32_t* __restrict__ positions, int position,
                                                             int max_len, int heads, int chunk, int n_splits,
                                                             uint16_t* __restrict__ out) {
-    const int hq = blockIdx.x, seq = blockIdx.y;
+    const int hq = blockIdx.x / kParts, dpart = blockIdx.x % kParts, seq = blockIdx.y;
     const int n_valid = seq_span(positions, position, seq, chunk, max_len).n_valid;
     if (n_valid <= 1) return;   // written by the split kernel
     const size_t h0 = (size_t)seq * heads + hq;
     constexpr size_t ent = HD + 4;
     const float* hp = part + h0 * n_splits * ent;
-    constexpr int kQuads = HD / 4;
-    constexpr int kSub = kBlock / kQuads;   // lanes per dim quad: 8 (HD 128) or 16 (HD 64)
-    static_assert(kSub == 8 || kSub == 16, "subsets of consecutive lanes");
+    constexpr int kQuads = HD / 4 / kParts;   // dim quads of this workgroup
+    constexpr int kSub = kBlock / kQuads;     // lanes per dim quad
+    static_assert(kSub == 8 || kSub == 16 || kSub == 32, "subsets of consecutive lanes");
     const int lane = threadIdx.x & (kWave - 1);
-    const int g = threadIdx.x % kSub, d4 = threadIdx.x / kSub;
+    const int g = threadIdx.x % kSub, d4 = dpart * kQuads + threadIdx.x / kSub;
 
     // kBatch chunks per thread have their loads issued together; the loads
     // are unconditional (a chunk past the last re-reads the last one), so
@@ -793,19 +792,42 @@ __global__ __launch_bounds__(kBlock) void attn_merge_kernel(const float* __restr
     }
 }
 
-// The merge launch, its per-thread batch sized to the plan's chunk count
-// (HD / 4 lanes of a wave hold one subset of the chunks each).
-template <int HD>
-void launch_merge(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
-    constexpr int kSub = kBlock / (HD / 4);
+// The merge launch, its per-thread batch sized to the plan's chunk count.
+template <int HD, int kParts>
+void launch_merge_parts(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
+    constexpr int kSub = kBlock / (HD / 4 / kParts);
     const int per = (p.n_splits + kSub - 1) / kSub;
     auto go = [&](auto kernel) {
-        launch_kernel(kernel, dim3(a.heads, a.nseq), dim3(kBlock), kMergeLds, stream, a.workspace, a.positions,
+        // no LDS: the merge keeps everything in registers
+        launch_kernel(kernel, dim3(a.heads * kParts, a.nseq), dim3(kBlock), 0, stream, a.workspace, a.positions,
                       a.position, a.max_len, a.heads, p.chunk, p.n_splits, a.out);
     };
-    if (per <= 2) go(attn_merge_kernel<HD, 2>);
-    else if (per <= 4) go(attn_merge_kernel<HD, 4>);
-    else go(attn_merge_kernel<HD, 8>);
+    if (per <= 1) go(attn_merge_kernel<HD, kParts, 1>);
+    else if (per <= 2) go(attn_merge_kernel<HD, kParts, 2>);
+    else if (per <= 4) go(attn_merge_kernel<HD, kParts, 4>);
+    else go(attn_merge_kernel<HD, kParts, 8>);
+}
+
+// Launches of fewer than kMergeSpreadBelow (head, sequence) pairs -- one
+// sequence -- split each head's dims over up to four workgroups, so that a
+// thread folds one chunk where the lanes allow (config 3, L = 8192, 32 chunks:
+// 128 workgroups; config-5 lengths, 9-12 chunks: 64).  Measured on MI355X
+// against one workgroup per head: split + merge 13.40 against 13.50 us at
+// config 3, 6.29 against 6.38 us per attention at config-5 lengths in a
+// graph; config 4 (16 sequences, 512 heads) measured 1-2% slower spread, so
+// launches of many heads keep one workgroup per head.
+constexpr int kMergeSpreadBelow = 256;
+template <int HD>
+void launch_merge(const AttnArgs& a, const AttnPlan& p, hipStream_t stream) {
+    constexpr int kSub1 = kBlock / (HD / 4);   // lanes per dim quad with one part: 8 (HD 128), 16 (HD 64)
+    if (a.heads * a.nseq >= kMergeSpreadBelow || p.n_splits <= kSub1) {
+        launch_merge_parts<HD, 1>(a, p, stream);
+    } else if constexpr (kSub1 * 4 <= 32) {
+        if (p.n_splits <= 2 * kSub1) launch_merge_parts<HD, 2>(a, p, stream);
+        else launch_merge_parts<HD, 4>(a, p, stream);
+    } else {
+        launch_merge_parts<HD, 2>(a, p, stream);
+    }
 }
 
 template <int HD, int GP, int kDepth>
@@ -900,7 +922,7 @@ AttnPlan plan_attention(int max_len, int nseq, int kv_heads, int heads, int head
     const long long lo = mfma ? 64 : 256, hi = mfma ? (units <= 16 ? 1024 : 512) : 512;
     long long chunk = ((long long)max_len * units + target_blocks - 1) / target_blocks;
     chunk = chunk < lo ? lo : chunk > hi ? hi : chunk;
-    const long long min_chunk = (max_len + kMaxSplits - 1) / kMaxSplits;
+    const long long min_chunk = ((long long)max_len + kMaxSplits - 1) / kMaxSplits;
     if (chunk < min_chunk) chunk = min_chunk;
     chunk = ((chunk + quantum - 1) / quantum) * quantum;
     p.chunk = (int)chunk;

@@ -134,16 +134,17 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(lo, hi);
 }
 
-// Sum over each group of N consecutive lanes (N = 8 or 16); every lane of a
-// group gets the same bits (each step adds a lane's value and its partner's,
-// and a + b = b + a).
+// Sum over each group of N consecutive lanes (N = 8, 16 or 32); every lane
+// of a group gets the same bits (each step adds a lane's value and its
+// partner's, and a + b = b + a).
 template <int N>
 __device__ __forceinline__ float lane_group_sum(float v) {
-    static_assert(N == 8 || N == 16, "group");
+    static_assert(N == 8 || N == 16 || N == 32, "group");
     v += dpp<kDppXor1>(v);
     v += dpp<kDppXor2>(v);
     v += dpp<kDppHalfMirror>(v);
-    if constexpr (N == 16) v += dpp<kDppMirror>(v);
+    if constexpr (N >= 16) v += dpp<kDppMirror>(v);
+    if constexpr (N == 32) v = sum16(v);
     return v;
 }
 
