@@ -418,39 +418,66 @@ struct RowSet {
     int end[3];
 };
 
-// Rows of 16*S super-blocks, streamed: each wave walks rows gw, gw + W, ...
-// (W = waves walking this row set), a row being S steps of 16 super-blocks,
-// and keeps the next D = S*M steps' fragments in flight while it computes
-// the current one (a ring of D register slots, indices fixed at compile time
-// by unrolling M rows).  x is loaded before the first fragments and staged
-// in LDS behind them.  Loads are branch-free (rows past the end re-read the
-// last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave computes its M rows
-// (all loaded up front) and stops; the grid then has M * W >= rows.  NB (an
-// even block count that is not a multiple of 16, S = ceil(NB / 16)): rows
-// ending in a partial wave step; in that step the lanes of blocks NB.. load
-// block NB - 1 (in bounds) and add nothing.
+// Rows packed per wave step: rows of NB blocks, NB dividing the 16 blocks of
+// a step (4 or 8: Qwen3-0.6B / 1.7B hidden sizes), take 16 / NB rows per
+// step, lane group sub / NB reading block sub % NB of its own row; other row
+// lengths take one row per step.  A "unit" is the rows one step covers.
+template <class QT, int NB>
+struct Pack {
+    static constexpr int P = (NB > 0 && NB < QT::kSbPerStep && QT::kSbPerStep % NB == 0) ? QT::kSbPerStep / NB : 1;
+    static constexpr int kGroupLanes = P > 1 ? NB * QT::kLanesPerSb : kWave;   // lanes summing one row
+    __host__ __device__ static constexpr int units(int rows) { return (rows + P - 1) / P; }
+    // the row of unit u that lane group `sub` works on
+    __device__ static __forceinline__ int row(int u, int sub) { return P > 1 ? u * P + sub / NB : u; }
+    // a row's sum over its lanes; with packing, lanes of one row only
+    __device__ static __forceinline__ float reduce(float v) {
+        if constexpr (P > 1) return lane_group_sum<kGroupLanes>(v);
+        else return wave_sum(v);
+    }
+    // the lane that stores its row's result
+    __device__ static __forceinline__ bool leader(int lane) { return lane % kGroupLanes == 0; }
+};
+
+// Rows of 16*S super-blocks, streamed: each wave walks units gw, gw + W, ...
+// (W = waves walking this row set; a unit is one row, or 16 / NB rows of a
+// short length, see Pack), a unit being S steps of 16 super-blocks, and
+// keeps the next D = S*M steps' fragments in flight while it computes the
+// current one (a ring of D register slots, indices fixed at compile time by
+// unrolling M units).  x is loaded before the first fragments and staged in
+// LDS behind them.  Loads are branch-free (rows past the end re-read the
+// last row).  kSegs = 1 reads only w[0] / y[0].  kRefill = false: the wave
+// computes its M units (all loaded up front) and stops; the grid then has
+// M * W >= units.  NB (an even block count that is not a multiple of 16,
+// S = ceil(NB / 16)): rows ending in a partial wave step; unless NB packs,
+// the lanes of blocks NB.. in that step load block NB - 1 (in bounds) and add
+// nothing.
 template <class QT, bool kF32, int S, int M, int kSegs, bool kRefill = true, bool kNorm = false, int NB = 0>
 __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __restrict__ x, int K, uint8_t* smem,
                                             int gw, int W, const NormIn& nrm) {
     static_assert(NB == 0 || (NB % 2 == 0 && (NB + QT::kSbPerStep - 1) / QT::kSbPerStep == S), "partial last step");
+    using PK = Pack<QT, NB>;
     constexpr int nb = NB ? NB : S * QT::kSbPerStep;   // K = 256 nb
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
     const int N = rs.end[kSegs - 1];
+    const int U = PK::units(N);
 
     const int lane = threadIdx.x & (kWave - 1);
     const int l4 = lane % QT::kLanesPerSb;
     const int sub = lane / QT::kLanesPerSb;
     // block of step t this lane reads; false: past the row end (adds nothing)
-    auto blk = [&](int t) { return NB ? min(t * QT::kSbPerStep + sub, nb - 1) : t * QT::kSbPerStep + sub; };
-    auto live = [&](int t) { return NB == 0 || t * QT::kSbPerStep + sub < nb; };
+    auto blk = [&](int t) {
+        if constexpr (PK::P > 1) return sub % NB;
+        else return NB ? min(t * QT::kSbPerStep + sub, nb - 1) : t * QT::kSbPerStep + sub;
+    };
+    auto live = [&](int t) { return NB == 0 || PK::P > 1 || t * QT::kSbPerStep + sub < nb; };
     constexpr int D = S * M;
 
     // matrix of row r and r's first row index in it
     auto seg_of = [&](int r) { return kSegs == 1 ? 0 : (int)(r >= rs.end[0]) + (int)(r >= rs.end[1]); };
     auto seg_base = [&](int sg) { return sg == 0 ? 0 : sg == 1 ? rs.end[0] : rs.end[1]; };
-    auto frag_at = [&](int row, int t) {
-        const int r = min(row, N - 1);
+    auto frag_at = [&](int unit, int t) {
+        const int r = min(PK::row(unit, sub), N - 1);
         const int sg = seg_of(r);
         const uint8_t* w = sg == 0 ? rs.w[0] : sg == 1 ? rs.w[1] : rs.w[2];
         const size_t f = (size_t)(r - seg_base(sg)) * nb + blk(t);
@@ -476,10 +503,10 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
         for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, blk(t));
     }
 
-    for (int row = gw; row < N; row += M * W) {
+    for (int unit = gw; unit < U; unit += M * W) {
 #pragma unroll
         for (int m = 0; m < M; ++m) {
-            const int r = row + m * W;
+            const int u = unit + m * W;
             float acc = 0.f;
 #pragma unroll
             for (int t = 0; t < S; ++t) {
@@ -491,12 +518,13 @@ __device__ __forceinline__ void stream_rows(const RowSet& rs, const uint16_t* __
                 // slot order (vmcnt retires loads in issue order: a reordered
                 // refill would make the next slot's wait cover it).
                 if constexpr (kRefill) {
-                    fr[m * S + t] = frag_at(issue_after(r + M * W, c, c), t);
+                    fr[m * S + t] = frag_at(issue_after(u + M * W, c, c), t);
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
-            acc = wave_sum(acc);
-            if (lane == 0 && r < N) {
+            acc = PK::reduce(acc);
+            const int r = PK::row(u, sub);
+            if (PK::leader(lane) && r < N) {
                 const int sg = seg_of(r);
                 store_y<kF32>(sg == 0 ? rs.y[0] : sg == 1 ? rs.y[1] : rs.y[2], r - seg_base(sg), acc);
             }
@@ -560,10 +588,11 @@ __global__ __launch_bounds__(kGateUpBlock, 2) void matvec_gate_up_kernel(const u
                                                                          NormIn nrm) {
     extern __shared__ __align__(16) uint8_t smem[];
     static_assert(NB == 0 || (NB % 2 == 0 && (NB + QT::kSbPerStep - 1) / QT::kSbPerStep == S), "partial last step");
+    using PK = Pack<QT, NB>;
     constexpr int nb = NB ? NB : S * QT::kSbPerStep;
     uint32_t* xp = reinterpret_cast<uint32_t*>(smem);
     float* sx = reinterpret_cast<float*>(smem + (size_t)K * 2);
-    // the row counter follows the x tables and the 4 floats of norm scratch
+    // the unit counter follows the x tables and the 4 floats of norm scratch
     int* next = reinterpret_cast<int*>(smem + (size_t)nb * kQK * 2 + (size_t)nb * QT::kSxPerBlock * sizeof(float) +
                                        4 * sizeof(float));
 
@@ -571,14 +600,18 @@ __global__ __launch_bounds__(kGateUpBlock, 2) void matvec_gate_up_kernel(const u
     const int wave = threadIdx.x / kWave;
     const int l4 = lane % QT::kLanesPerSb;
     const int sub = lane / QT::kLanesPerSb;
-    auto blk = [&](int t) { return NB ? min(t * QT::kSbPerStep + sub, nb - 1) : t * QT::kSbPerStep + sub; };
-    auto live = [&](int t) { return NB == 0 || t * QT::kSbPerStep + sub < nb; };
-    const int span = (N + (int)gridDim.x - 1) / (int)gridDim.x;
-    const int r0 = (int)blockIdx.x * span;
-    const int nrows = max(0, min(span, N - r0));
+    auto blk = [&](int t) {
+        if constexpr (PK::P > 1) return sub % NB;
+        else return NB ? min(t * QT::kSbPerStep + sub, nb - 1) : t * QT::kSbPerStep + sub;
+    };
+    auto live = [&](int t) { return NB == 0 || PK::P > 1 || t * QT::kSbPerStep + sub < nb; };
+    const int U = PK::units(N);
+    const int span = (U + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int u0 = (int)blockIdx.x * span;
+    const int nunits = max(0, min(span, U - u0));
 
-    auto frag_at = [&](const uint8_t* w, int row, int t) {
-        const size_t f = (size_t)min(row, N - 1) * nb + blk(t);
+    auto frag_at = [&](const uint8_t* w, int unit, int t) {
+        const size_t f = (size_t)min(PK::row(unit, sub), N - 1) * nb + blk(t);
         return QT::load(w + f * QT::kBytes, l4);
     };
 
@@ -586,12 +619,12 @@ __global__ __launch_bounds__(kGateUpBlock, 2) void matvec_gate_up_kernel(const u
     XStage<QT::kSumLayout, nb * 32, kNorm> xs;   // K = 256 nb
     if (wave < kWavesPerBlock) xs.load(x, nrm);
     __builtin_amdgcn_sched_barrier(0);
-    int k = wave;   // this wave's row r0 + k
+    int k = wave;   // this wave's unit u0 + k
     typename QT::Frag fg[S], fu[S];
 #pragma unroll
     for (int t = 0; t < S; ++t) {
-        fg[t] = frag_at(wg, r0 + k, t);
-        fu[t] = frag_at(wu, r0 + k, t);
+        fg[t] = frag_at(wg, u0 + k, t);
+        fu[t] = frag_at(wu, u0 + k, t);
         __builtin_amdgcn_sched_barrier(0);   // slot order, as the refills below
     }
     if (wave < kWavesPerBlock) {
@@ -605,18 +638,18 @@ __global__ __launch_bounds__(kGateUpBlock, 2) void matvec_gate_up_kernel(const u
 #pragma unroll
     for (int t = 0; t < S; ++t) xr[t] = QT::xload(xp, sx, l4, blk(t));
 
-    while (k < nrows) {   // wave-uniform
+    while (k < nunits) {   // wave-uniform
         int kn = 0;
         if (lane == 0) kn = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         kn = __builtin_amdgcn_readfirstlane(kn);
-        const bool more = kn < nrows;
-        const int r = r0 + k;
+        const bool more = kn < nunits;
+        const int unit = u0 + k;
         // Each slot is reloaded with the next row once its dots have read it
         // (issue_after), in slot order.  A one-step row (S = 1) reloads after
         // both dots and skips the reload on its last row; longer rows reload
         // unconditionally (their last row re-reads itself), since a branch
         // there let the compiler move every reload behind the last dot.
-        const int rn = more ? r0 + kn : r;
+        const int un = more ? u0 + kn : unit;
         float ag = 0.f, au = 0.f;
 #pragma unroll
         for (int t = 0; t < S; ++t) {
@@ -629,21 +662,22 @@ __global__ __launch_bounds__(kGateUpBlock, 2) void matvec_gate_up_kernel(const u
             ag += cg;
             au += cu;
             if (S > 1 || more) {
-                const int nr = issue_after(rn, cg, cu);
-                fg[t] = frag_at(wg, nr, t);
-                fu[t] = frag_at(wu, nr, t);
+                const int nu = issue_after(un, cg, cu);
+                fg[t] = frag_at(wg, nu, t);
+                fu[t] = frag_at(wu, nu, t);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
-        ag = wave_sum(ag);
-        au = wave_sum(au);
+        ag = PK::reduce(ag);
+        au = PK::reduce(au);
         // computed in every lane, so the branch holds only the store (a
         // longer branch region keeps the fragment registers from being
         // reused across rows: the loop edge then copies them and waits for
         // every refill)
         const float g = h2f(f2h_rne(ag)), u = h2f(f2h_rne(au));
         const uint16_t a = f2h_rne(g / (1.0f + expf(-g)) * u);
-        if (lane == 0) act[r] = a;
+        const int r = PK::row(unit, sub);
+        if (PK::leader(lane) && r < N) act[r] = a;
         k = kn;
     }
 }
@@ -727,29 +761,31 @@ int stream_grid(int rows, int per_cu = 2) {
 template <class QT, bool kF32, int S, int M, int kSegs, bool kNorm, int NB = 0>
 void launch_stream(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
     constexpr int K = (NB ? NB : S * QT::kSbPerStep) * kQK;
+    const int units = Pack<QT, NB>::units(rs.end[kSegs - 1]);
     launch_kernel((matvec_stream_kernel<QT, kF32, S, M, kSegs, true, kNorm, NB>),
-                  dim3(stream_grid(rs.end[kSegs - 1], S >= 2 ? 1 : 2)), dim3(kBlock), lds, stream, rs, x, K, nrm);
+                  dim3(stream_grid(units, S >= 2 ? 1 : 2)), dim3(kBlock), lds, stream, rs, x, K, nrm);
 }
 
-// Rows of one wave step (K <= 4096), few rows: every wave loads its M rows
-// up front and computes them, no refills (M * waves >= rows).
+// Rows of one wave step (K <= 4096), few rows: every wave loads its M units
+// up front and computes them, no refills (M * waves >= units).
 template <class QT, bool kF32, int M, int kSegs, bool kNorm, int NB = 0>
 void launch_rows_once(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
     constexpr int K = (NB ? NB : QT::kSbPerStep) * kQK;
-    const int rows = rs.end[kSegs - 1];
-    const int grid = (rows + M * kWavesPerBlock - 1) / (M * kWavesPerBlock);
+    const int units = Pack<QT, NB>::units(rs.end[kSegs - 1]);
+    const int grid = (units + M * kWavesPerBlock - 1) / (M * kWavesPerBlock);
     launch_kernel((matvec_stream_kernel<QT, kF32, 1, M, kSegs, false, kNorm, NB>), dim3(grid), dim3(kBlock), lds,
                   stream, rs, x, K, nrm);
 }
 
 // Rows ending in a partial wave step (NB blocks, not a multiple of 16).
 // Shorter than one step (K = 1024, 2048, 2560, 3072: Qwen3-0.6B / 4B): one
-// pass of one row per wave up to 1024 rows, of two up to 4096, streamed
-// with one row in flight beyond; longer rows stream with one row in flight.
+// pass of one unit per wave up to 1024 units, of two up to 4096, streamed
+// with one unit in flight beyond (a unit: 16 / NB rows for NB = 4 or 8, one
+// row else); longer rows stream with one row in flight.
 template <class QT, bool kF32, int kSegs, bool kNorm, int NB>
 void launch_partial(const RowSet& rs, const uint16_t* x, size_t lds, const NormIn& nrm, hipStream_t stream) {
     constexpr int S = (NB + QT::kSbPerStep - 1) / QT::kSbPerStep;
-    const int rows = rs.end[kSegs - 1];
+    const int rows = Pack<QT, NB>::units(rs.end[kSegs - 1]);
     if constexpr (S == 1) {
         if (rows <= 1024)
             launch_rows_once<QT, kF32, 1, kSegs, kNorm, NB>(rs, x, lds, nrm, stream);
@@ -848,7 +884,9 @@ hipError_t launch_matvec_prologue(const uint8_t* w, const uint16_t* x, const Nor
 template <int S, int M, bool kNorm, int NB = 0>
 void launch_group_mixed(const RowSet& a, const RowSet& b, const uint16_t* x, int K, const NormIn& nrm,
                         hipStream_t stream) {
-    const int na = a.end[2], nbr = b.end[2];
+    // units of each set (Q4_K and Q6_K pack alike: four lanes per block)
+    static_assert(Pack<Q4K, NB>::P == Pack<Q6K, NB>::P, "same packing");
+    const int na = Pack<Q4K, NB>::units(a.end[2]), nbr = Pack<Q6K, NB>::units(b.end[2]);
     const size_t lds = std::max(lds_bytes<Q4K>(K), lds_bytes<Q6K>(K));
     if constexpr (S == 1) {
         if (na + nbr <= 8192) {
@@ -897,9 +935,11 @@ bool launch_group(int nb, RowSet (&set)[2], const int (&cnt)[2], bool f16, const
 template <class QT, bool kNorm>
 hipError_t launch_gate_up_t(const uint8_t* wg, const uint8_t* wu, const uint16_t* x, uint16_t* act, int K, int N,
                           const NormIn& nrm, hipStream_t stream) {
-    const size_t lds = lds_bytes<QT>(K) + sizeof(int);   // + the row counter
+    const size_t lds = lds_bytes<QT>(K) + sizeof(int);   // + the unit counter
     int grid = device_cus();
-    const int need = (N + kGateUpWaves - 1) / kGateUpWaves;
+    const int nb = K / kQK;
+    const int units = nb < QT::kSbPerStep && QT::kSbPerStep % nb == 0 ? (N + QT::kSbPerStep / nb - 1) / (QT::kSbPerStep / nb) : N;
+    const int need = (units + kGateUpWaves - 1) / kGateUpWaves;
     if (grid > need) grid = need;
     const dim3 g(grid), b(kGateUpBlock);
     switch (K / kQK) {

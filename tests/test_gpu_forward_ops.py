@@ -256,10 +256,13 @@ def test_qk_norm_rope_store_equals_separate_launches(hip, heads, kv, hd, pos, wi
                                       ("fp16", 12288, 4096), ("fp16", 3000, 8192), ("q4k", 3072, 1024),
                                       ("q6k", 700, 3072), ("fp16", 5000, 2048), ("q4k", 1000, 2560),
                                       ("q6k", 500, 5120), ("fp16", 700, 5120), ("q4k", 5, 4096), ("q6k", 1, 2048),
-                                      ("q4k", 2049, 4096)])
+                                      ("q4k", 2049, 4096), ("q4k", 3, 1024), ("q4k", 3073, 1024),
+                                      ("q6k", 7, 2048), ("fp16", 2051, 1024)])
 def test_gate_up_swiglu_equals_two_gemvs_and_swiglu(hip, kind, n, k):
-    """Also fewer rows than one workgroup's eight waves (waves without a row)
-    and a row count that leaves the last workgroup a short range."""
+    """Also fewer rows than one workgroup's eight waves (waves without a row),
+    a row count that leaves the last workgroup a short range, and rows of 4
+    or 8 blocks (four / two rows per wave step) whose count leaves the last
+    step part-filled."""
     rng = hip.synth.Rng(n + k)
     wg, wu = hip.synth.quant_matrix(kind, rng, n, k), hip.synth.quant_matrix(kind, rng, n, k)
     x = hip.synth.normal_f16(rng, k)

@@ -41,6 +41,14 @@ SHAPES = [
     # pass covers: streamed)
     ("q4k", 1024, 2048),
     ("q6k", 6000, 1024),
+    # rows of 4 and 8 blocks pack 4 / 2 rows per wave step: row counts that
+    # leave a partial last unit, one pass and streamed
+    ("q4k", 3, 1024),
+    ("q6k", 4099, 1024),
+    ("q4k", 16387, 1024),
+    ("q4k", 5, 2048),
+    ("q6k", 2049, 2048),
+    ("q4k", 9001, 2048),
     # the other Qwen3 sizes: rows ending in a partial wave step
     ("q4k", 300, 2560),      # 4B hidden (nb = 10)
     ("q4k", 257, 5120),      # 14B / 32B hidden (nb = 20)

@@ -65,6 +65,12 @@ CASES = [
     (("q6k", "q6k", "q6k"), (1024, 1024, 3000), 1024),
     (("fp16", "fp16", "fp16"), (2048, 1024, 1024), 1024),
     (("fp16",), (6000,), 3072),
+    # rows of 4 / 8 blocks pack four / two rows per wave step: units that
+    # straddle two matrices and a part-filled last unit
+    (("q4k", "q4k", "q6k"), (2047, 1025, 1023), 1024),
+    (("q6k", "q4k"), (701, 301), 2048),
+    (("fp16", "fp16", "fp16"), (1023, 1, 2), 1024),
+    (("q4k", "q4k", "q4k"), (9001, 4093, 3), 1024),
     # the other Qwen3 sizes (4B hidden 2560, 14B / 32B hidden 5120, 1.7B /
     # 4B FFN 6144 / 9728): partial last wave step
     (("q4k", "q4k", "q6k"), (4096, 1024, 1024), 2560),
