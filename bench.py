@@ -20,7 +20,11 @@ step; HIP events on the launch stream around the K timed steps).  roofline:
 the kernel with the largest share of step time, its algorithmic bytes per
 launch over its average launch duration over a second pass of the same K
 steps, from HIP events that the kernel's own dispatches stamp
-(hipExtLaunchKernel; for attention, split start to merge end).  cpu_baseline: the
+(hipExtLaunchKernel; for attention, split start to merge end).
+rocprof_step: the same steps re-run in a child process under rocprofv3
+--kernel-trace, each op's mean kernel duration as the trace records it (the
+figures of the committed profiles/ summaries; roofline.rocprof is the
+dominant kernel's roofline from them).  cpu_baseline: the
 oracle's restatement of the reference's host arithmetic (dequant to fp16 with
 the host rule, fp32 dot; fp32 attention) on a bounded sample of the same
 layer, on this machine's host cores.  attention_cfg4
@@ -146,6 +150,12 @@ def run_gpu(args):
     for s in range(args.warmup):
         step(s)
     hip.synchronize()
+    if args.trace_child:
+        # under the parent's rocprofv3 kernel trace: the K steps, nothing else
+        for s in range(args.steps):
+            step(s)
+        hip.synchronize()
+        return None
     cal = max(8, 2 * LAYERS)
     cal_timers = [{n: hip.device.KernelTimer() for n in ORDER} for _ in range(cal)]
     for s in range(cal):
@@ -513,6 +523,68 @@ def decode_cfg5(fp16=False):
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
+# the dispatches of one step, in launch order, and the step op each belongs to
+STEP_DISPATCHES = [("matvec_group_kernel", "attn_qkv"), ("attn_mfma_kernel", "attention"),
+                   ("attn_merge_kernel", "attention"), ("matvec_stream_kernel", "attn_o"),
+                   ("matvec_gate_up_kernel", "ffn_gate_up"), ("matvec_stream_kernel", "ffn_down")]
+
+
+def rocprof_step_kernels(args):
+    """Kernel durations of the config-3 step as rocprofv3 measures them:
+    this script in --trace-child mode (the same warmup and K steps, nothing
+    else) under `rocprofv3 --kernel-trace`, a child process.  The last 6 K
+    dispatches of the trace are the K steps (q/k/v, attention split,
+    attention merge, attn_o, gate/up, ffn_down); per op, the mean of its
+    kernels' end - start over the K steps (attention: split + merge, the gap
+    between them excluded).  These are the figures the committed rocprofv3
+    summaries report; the event-stamped kernels_us include each dispatch's
+    event overhead.  None when rocprofv3 is absent or its trace is
+    unusable."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None
+    with tempfile.TemporaryDirectory(dir="/tmp" if os.path.isdir("/tmp") else None) as d:
+        cmd = [exe, "--kernel-trace", "--output-format", "csv", "-d", d, "-o", "step", "--", sys.executable,
+               os.path.abspath(__file__), "--trace-child", "--steps", str(args.steps), "--warmup", str(args.warmup)]
+        env = dict(os.environ, TMPDIR=d)
+        try:
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=300, cwd=d, env=env)
+        except subprocess.TimeoutExpired:
+            return {"error": "rocprofv3 pass timed out"}
+        files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+        if not files:
+            return {"error": f"no kernel trace (rocprofv3 exit {p.returncode}): {(p.stderr or p.stdout)[-200:]}"}
+        rows = []
+        for f in files:
+            rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    n = len(STEP_DISPATCHES) * args.steps
+    if len(rows) < n:
+        return {"error": f"{len(rows)} dispatches traced, {n} expected"}
+    rows = rows[-n:]
+    sums = {op: 0.0 for op in ORDER}
+    split = merge = 0.0
+    for i, r in enumerate(rows):
+        want, op = STEP_DISPATCHES[i % len(STEP_DISPATCHES)]
+        if want not in r["Kernel_Name"]:
+            return {"error": f"dispatch {i} of the timed steps is {r['Kernel_Name'][:80]}, expected {want}"}
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        sums[op] += us
+        if want == "attn_mfma_kernel":
+            split += us
+        elif want == "attn_merge_kernel":
+            merge += us
+    k = args.steps
+    return {"kernels_us": {op: round(v / k, 3) for op, v in sums.items()},
+            "attention_split_us": round(split / k, 3), "attention_merge_us": round(merge / k, 3),
+            "step_kernel_us": round(sum(sums.values()) / k, 3)}
+
+
 def read_traffic(kernel):
     """HBM bytes per launch of `kernel` (a step-kernel name) from the
     committed rocprofv3 PMC summary: the line 'traffic_bytes_per_launch
@@ -534,12 +606,17 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=2.0, help="per CPU-baseline measurement")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 whole-model decode run")
+    ap.add_argument("--no-rocprof", action="store_true", help="skip the rocprofv3 kernel-trace pass")
+    ap.add_argument("--trace-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the decode hot path here is a single-GPU build "
               "(multi-GPU sharding is a design note, not a measured mode)", file=sys.stderr)
         sys.exit(2)
 
+    if args.trace_child:
+        run_gpu(args)
+        return
     total_ms, dominant, dom_ms, per, (stream_gbps, copy_gbps), host = run_gpu(args)
     kb = kernel_bytes()
     step_bytes = sum(kb.values())
@@ -574,6 +651,14 @@ def main():
         "copy_GBps": round(copy_gbps, 1),
         "cpu_baseline": None,
     }
+    rp = None if args.no_rocprof else rocprof_step_kernels(args)
+    if rp and "kernels_us" in rp:
+        ku = rp["kernels_us"]
+        rp["kernels_GBps"] = {n: round(kb[n] / (ku[n] * 1e-6) / 1e9, 1) for n in ORDER}
+        a = kb[dominant] / (ku[dominant] * 1e-6) / 1e9
+        line["roofline"]["rocprof"] = {"us_per_launch": ku[dominant], "achieved": round(a, 1),
+                                       "frac": round(a / HBM_PEAK_GBPS, 4)}
+    line["rocprof_step"] = rp
     line["matvec_cfg1"] = matvec_cfg1()
     line["attention_cfg2"] = attention_cfg2()
     line["attention_cfg4"] = attention_cfg4()
