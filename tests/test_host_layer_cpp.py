@@ -41,14 +41,18 @@ def test_host_layer_model(mode):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fixture", ["cfg5_greedy.txt", "cfg5_greedy_p512.txt"])
+@pytest.mark.parametrize("fixture", ["cfg5_greedy.txt", "cfg5_greedy_s4.txt", "cfg5_greedy_p512.txt"])
 def test_host_layer_config5_greedy(fixture):
     """BASELINE config 5 at its full shape (the benchmark's synthetic
     Qwen3-8B: 36 layers with their own weights, vocab 151936): QwenModel's
     greedy tokens equal the oracle's fixture (tests/golden/cfg5_greedy*.txt,
     from tests/golden/make_cfg5_greedy) through the forward_token loop and
     the graph-replayed decode_greedy.  cfg5_greedy.txt: an 8-token prompt and
-    64 steps; cfg5_greedy_p512.txt: config 5 as stated, the benchmark's
+    64 steps (prompt seed 1; its step 27 is a near-tie: oracle margin 1.6e-3
+    of the logit rms against a GPU top-2 gap error of 2.0e-3 there);
+    cfg5_greedy_s4.txt: the same with prompt seed 4, chosen among seeds 2-7
+    for its margins (smallest 1.9e-2 of the rms; smallest margin / GPU gap
+    error 28.9); cfg5_greedy_p512.txt: config 5 as stated, the benchmark's
     512-token prompt (seed 1) and 256 steps (positions up to 766, the
     1024-position attention plan)."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", fixture)
