@@ -418,13 +418,18 @@ struct RowSet {
     int end[3];
 };
 
+// Rows per wave step for rows of nb super-blocks (`per_step` blocks a step).
+__host__ __device__ constexpr int pack_rows(int nb, int per_step) {
+    return (nb > 0 && nb < per_step && per_step % nb == 0) ? per_step / nb : 1;
+}
+
 // Rows packed per wave step: rows of NB blocks, NB dividing the 16 blocks of
 // a step (4 or 8: Qwen3-0.6B / 1.7B hidden sizes), take 16 / NB rows per
 // step, lane group sub / NB reading block sub % NB of its own row; other row
 // lengths take one row per step.  A "unit" is the rows one step covers.
 template <class QT, int NB>
 struct Pack {
-    static constexpr int P = (NB > 0 && NB < QT::kSbPerStep && QT::kSbPerStep % NB == 0) ? QT::kSbPerStep / NB : 1;
+    static constexpr int P = pack_rows(NB, QT::kSbPerStep);
     static constexpr int kGroupLanes = P > 1 ? NB * QT::kLanesPerSb : kWave;   // lanes summing one row
     __host__ __device__ static constexpr int units(int rows) { return (rows + P - 1) / P; }
     // the row of unit u that lane group `sub` works on
@@ -938,7 +943,8 @@ hipError_t launch_gate_up_t(const uint8_t* wg, const uint8_t* wu, const uint16_t
     const size_t lds = lds_bytes<QT>(K) + sizeof(int);   // + the unit counter
     int grid = device_cus();
     const int nb = K / kQK;
-    const int units = nb < QT::kSbPerStep && QT::kSbPerStep % nb == 0 ? (N + QT::kSbPerStep / nb - 1) / (QT::kSbPerStep / nb) : N;
+    const int per_unit = pack_rows(nb, QT::kSbPerStep);
+    const int units = (N + per_unit - 1) / per_unit;
     const int need = (units + kGateUpWaves - 1) / kGateUpWaves;
     if (grid > need) grid = need;
     const dim3 g(grid), b(kGateUpBlock);
