@@ -24,7 +24,9 @@ steps, from HIP events that the kernel's own dispatches stamp
 rocprof_step: the same steps re-run in a child process under rocprofv3
 --kernel-trace, each op's mean kernel duration as the trace records it (the
 figures of the committed profiles/ summaries; roofline.rocprof is the
-dominant kernel's roofline from them).  cpu_baseline: the
+dominant kernel's roofline from them); configs 1 and 2 likewise re-run
+under rocprofv3 (their kernel_us; kernel_us_stamped is the dispatch-stamped
+figure).  cpu_baseline: the
 oracle's restatement of the reference's host arithmetic (dequant to fp16 with
 the host rule, fp32 dot; fp32 attention) on a bounded sample of the same
 layer, on this machine's host cores.  attention_cfg4
@@ -223,10 +225,15 @@ def _rotated_copies(hip, host_bytes, unit_bytes):
     return buf, slot, n
 
 
-def _time_rotated(hip, launch, n, reps):
+CONFIG_REPS = 10   # timed passes over the rotated copies, configs 1 and 2
+
+
+def _time_rotated(hip, launch, n, reps, stamped=True):
     """Mean launch time (us) over reps passes of n back-to-back launches
     (launch(i) uses copy i): HIP events around all of them, and the kernels'
-    own dispatch-stamped time of one more pass."""
+    own dispatch-stamped time of one more pass (stamped=False: that pass is
+    left out, for the rocprofv3 child, whose trace then holds one untimed
+    pass and the reps timed ones)."""
     for i in range(n):
         launch(i)
     e0, e1 = hip.Event(), hip.Event()
@@ -237,6 +244,8 @@ def _time_rotated(hip, launch, n, reps):
     e1.record()
     e1.synchronize()
     wall_us = e0.elapsed_ms(e1) / (reps * n) * 1e3
+    if not stamped:
+        return wall_us, None
     timers = [hip.device.KernelTimer() for _ in range(n)]
     for i in range(n):
         with timers[i]:
@@ -246,7 +255,7 @@ def _time_rotated(hip, launch, n, reps):
     return wall_us, kern_us
 
 
-def matvec_cfg1():
+def matvec_cfg1(stamped=True):
     """Q4_K GEMV of a 3072 x 1024 matrix (4 super-blocks
     per row, seed 0), x N(0,1) fp16, y fp32 (citlali_hip_matvec_q4k_to_float);
     also the same bytes read as 1024 rows of 12 super-blocks (K = 3072).
@@ -261,18 +270,20 @@ def matvec_cfg1():
     out = {}
     for name, rows, cols in (("3072x1024", 3072, 1024), ("1024x3072", 1024, 3072)):
         wall, kern = _time_rotated(hip, lambda i: hip.device.matvec("q4k", buf.at(i * slot), dx, dy, cols, rows,
-                                                                   f32_out=True), n, 10)
+                                                                   f32_out=True), n, CONFIG_REPS, stamped)
         alg = w.nbytes + cols * 2 + rows * 4
         out[name] = {"bytes_per_launch": alg, "copies_rotated": n, "us_per_launch": round(wall, 3),
-                     "GBps": round(alg / (wall * 1e-6) / 1e9, 1), "frac_of_8TBps": round(alg / (wall * 1e-6) / 8e12, 4),
-                     "kernel_us": round(kern, 3), "kernel_GBps": round(alg / (kern * 1e-6) / 1e9, 1)}
+                     "GBps": round(alg / (wall * 1e-6) / 1e9, 1), "frac_of_8TBps": round(alg / (wall * 1e-6) / 8e12, 4)}
+        if kern is not None:
+            out[name].update({"kernel_us_stamped": round(kern, 3),
+                              "kernel_GBps_stamped": round(alg / (kern * 1e-6) / 1e9, 1)})
     for a in (buf, dx, dy):
         a.close()
     return {"workload": "BASELINE config 1: Q4_K GEMV 3072 rows x 1024 cols (4 super-blocks/row), fp32 y; "
                         "also read as 1024 x 3072 (12 super-blocks/row)", **out}
 
 
-def attention_cfg2():
+def attention_cfg2(stamped=True):
     """Qwen3-0.6B decode attention, 16 query / 8 kv heads,
     head_dim 128, 1024 cached positions (position 1023), q/K/V N(0,1) fp16
     (seed 0), fp16 output; rotated over >= 512 MB of K/V copies."""
@@ -288,14 +299,17 @@ def attention_cfg2():
     scores = hip.DeviceArray(heads * L * 4)
     do = hip.DeviceArray(heads * hd * 2)
     wall, kern = _time_rotated(hip, lambda i: hip.device.attention(dq, kb.at(i * slot), kb.at(i * slot + kv_bytes),
-                                                                  scores, do, L - 1, L, heads, kv, hd), n, 10)
+                                                                  scores, do, L - 1, L, heads, kv, hd), n, CONFIG_REPS,
+                               stamped)
     alg = 2 * kv_bytes + 2 * heads * hd * 2
     for a in (kb, dq, scores, do):
         a.close()
-    return {"workload": "BASELINE config 2: Qwen3-0.6B decode attention, 16/8 heads, head_dim 128, L=1024",
-            "bytes_per_launch": alg, "copies_rotated": n, "us_per_launch": round(wall, 3),
-            "GBps": round(alg / (wall * 1e-6) / 1e9, 1), "frac_of_8TBps": round(alg / (wall * 1e-6) / 8e12, 4),
-            "kernel_us": round(kern, 3), "kernel_GBps": round(alg / (kern * 1e-6) / 1e9, 1)}
+    out = {"workload": "BASELINE config 2: Qwen3-0.6B decode attention, 16/8 heads, head_dim 128, L=1024",
+           "bytes_per_launch": alg, "copies_rotated": n, "us_per_launch": round(wall, 3),
+           "GBps": round(alg / (wall * 1e-6) / 1e9, 1), "frac_of_8TBps": round(alg / (wall * 1e-6) / 8e12, 4)}
+    if kern is not None:
+        out.update({"kernel_us_stamped": round(kern, 3), "kernel_GBps_stamped": round(alg / (kern * 1e-6) / 1e9, 1)})
+    return out
 
 
 def attention_cfg4():
@@ -529,6 +543,78 @@ STEP_DISPATCHES = [("matvec_group_kernel", "attn_qkv"), ("attn_mfma_kernel", "at
                    ("matvec_gate_up_kernel", "ffn_gate_up"), ("matvec_stream_kernel", "ffn_down")]
 
 
+def _rocprof_rows(child_args):
+    """This script with `child_args` in a child process under `rocprofv3
+    --kernel-trace`: (the trace's dispatches sorted by start, the child's
+    stdout); (None, None) without rocprofv3, ({"error": ...}, None) when the
+    run or its trace is unusable."""
+    import csv
+    import glob
+    import shutil
+    import subprocess
+    import tempfile
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        return None, None
+    with tempfile.TemporaryDirectory(dir="/tmp" if os.path.isdir("/tmp") else None) as d:
+        cmd = [exe, "--kernel-trace", "--output-format", "csv", "-d", d, "-o", "trace", "--", sys.executable,
+               os.path.abspath(__file__), *child_args]
+        env = dict(os.environ, TMPDIR=d)
+        try:
+            p = subprocess.run(cmd, capture_output=True, text=True, timeout=300, cwd=d, env=env)
+        except subprocess.TimeoutExpired:
+            return {"error": "rocprofv3 pass timed out"}, None
+        files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
+        if not files:
+            return {"error": f"no kernel trace (rocprofv3 exit {p.returncode}): {(p.stderr or p.stdout)[-200:]}"}, None
+        rows = []
+        for f in files:
+            rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    return rows, p.stdout
+
+
+def _dur_us(r):
+    return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+
+def rocprof_config_kernels():
+    """Kernel durations of configs 1 and 2 as rocprofv3 measures them: the
+    same rotated launches (one untimed pass, CONFIG_REPS timed passes, no
+    dispatch-stamped pass) run by this script in --trace-configs mode under
+    `rocprofv3 --kernel-trace`.  Config 1: the mean duration of the GEMV
+    dispatches of the timed passes, per shape; config 2: the mean split and
+    merge durations and their sum per launch.  {} without rocprofv3."""
+    rows, out = _rocprof_rows(["--trace-configs"])
+    if rows is None:
+        return {}
+    if isinstance(rows, dict):
+        return {"error": rows["error"]}
+    try:
+        copies = json.loads([ln for ln in out.splitlines() if ln.startswith("{")][-1])
+    except (IndexError, ValueError):
+        return {"error": "the --trace-configs child printed no launch counts"}
+    res = {}
+    mv = [r for r in rows if "matvec" in r["Kernel_Name"]]
+    shapes = list(copies["cfg1"].items())
+    if len(mv) != sum(n * (1 + CONFIG_REPS) for _, n in shapes):
+        return {"error": f"{len(mv)} GEMV dispatches traced for config 1"}
+    at = 0
+    for name, n in shapes:
+        timed = mv[at + n: at + n * (1 + CONFIG_REPS)]
+        at += n * (1 + CONFIG_REPS)
+        res[name] = round(sum(_dur_us(r) for r in timed) / len(timed), 3)
+    n2 = copies["cfg2"] * CONFIG_REPS
+    split = [r for r in rows if "attn_" in r["Kernel_Name"] and "merge" not in r["Kernel_Name"]][-n2:]
+    merge = [r for r in rows if "attn_merge" in r["Kernel_Name"]][-n2:]
+    if len(split) != n2 or len(merge) not in (0, n2):
+        return {"error": f"{len(split)} split / {len(merge)} merge dispatches traced for config 2, {n2} timed"}
+    s_us = sum(_dur_us(r) for r in split) / n2
+    m_us = sum(_dur_us(r) for r in merge) / n2 if merge else 0.0
+    res["cfg2"] = {"split_us": round(s_us, 3), "merge_us": round(m_us, 3), "kernel_us": round(s_us + m_us, 3)}
+    return res
+
+
 def rocprof_step_kernels(args):
     """Kernel durations of the config-3 step as rocprofv3 measures them:
     this script in --trace-child mode (the same warmup and K steps, nothing
@@ -538,31 +624,11 @@ def rocprof_step_kernels(args):
     kernels' end - start over the K steps (attention: split + merge, the gap
     between them excluded).  These are the figures the committed rocprofv3
     summaries report; the event-stamped kernels_us include each dispatch's
-    event overhead.  None when rocprofv3 is absent or its trace is
-    unusable."""
-    import csv
-    import glob
-    import shutil
-    import subprocess
-    import tempfile
-    exe = shutil.which("rocprofv3")
-    if exe is None:
-        return None
-    with tempfile.TemporaryDirectory(dir="/tmp" if os.path.isdir("/tmp") else None) as d:
-        cmd = [exe, "--kernel-trace", "--output-format", "csv", "-d", d, "-o", "step", "--", sys.executable,
-               os.path.abspath(__file__), "--trace-child", "--steps", str(args.steps), "--warmup", str(args.warmup)]
-        env = dict(os.environ, TMPDIR=d)
-        try:
-            p = subprocess.run(cmd, capture_output=True, text=True, timeout=300, cwd=d, env=env)
-        except subprocess.TimeoutExpired:
-            return {"error": "rocprofv3 pass timed out"}
-        files = glob.glob(os.path.join(d, "**", "*kernel_trace.csv"), recursive=True)
-        if not files:
-            return {"error": f"no kernel trace (rocprofv3 exit {p.returncode}): {(p.stderr or p.stdout)[-200:]}"}
-        rows = []
-        for f in files:
-            rows += list(csv.DictReader(open(f)))
-    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    event overhead.  None when rocprofv3 is absent, an error entry when its
+    trace is unusable."""
+    rows, _ = _rocprof_rows(["--trace-child", "--steps", str(args.steps), "--warmup", str(args.warmup)])
+    if rows is None or isinstance(rows, dict):
+        return rows
     n = len(STEP_DISPATCHES) * args.steps
     if len(rows) < n:
         return {"error": f"{len(rows)} dispatches traced, {n} expected"}
@@ -573,7 +639,7 @@ def rocprof_step_kernels(args):
         want, op = STEP_DISPATCHES[i % len(STEP_DISPATCHES)]
         if want not in r["Kernel_Name"]:
             return {"error": f"dispatch {i} of the timed steps is {r['Kernel_Name'][:80]}, expected {want}"}
-        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        us = _dur_us(r)
         sums[op] += us
         if want == "attn_mfma_kernel":
             split += us
@@ -608,6 +674,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the config-5 whole-model decode run")
     ap.add_argument("--no-rocprof", action="store_true", help="skip the rocprofv3 kernel-trace pass")
     ap.add_argument("--trace-child", action="store_true", help=argparse.SUPPRESS)
+    ap.add_argument("--trace-configs", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the decode hot path here is a single-GPU build "
@@ -616,6 +683,12 @@ def main():
 
     if args.trace_child:
         run_gpu(args)
+        return
+    if args.trace_configs:
+        # under the parent's rocprofv3 kernel trace: configs 1 and 2, unstamped
+        c1, c2 = matvec_cfg1(stamped=False), attention_cfg2(stamped=False)
+        print(json.dumps({"cfg1": {k: v["copies_rotated"] for k, v in c1.items() if isinstance(v, dict)},
+                          "cfg2": c2["copies_rotated"]}), flush=True)
         return
     total_ms, dominant, dom_ms, per, (stream_gbps, copy_gbps), host = run_gpu(args)
     kb = kernel_bytes()
@@ -661,6 +734,18 @@ def main():
     line["rocprof_step"] = rp
     line["matvec_cfg1"] = matvec_cfg1()
     line["attention_cfg2"] = attention_cfg2()
+    rc = {} if args.no_rocprof else rocprof_config_kernels()
+    if "error" in rc:
+        line["matvec_cfg1"]["rocprof"] = line["attention_cfg2"]["rocprof"] = rc
+    for shape, us in rc.items():
+        if shape in line["matvec_cfg1"]:
+            c = line["matvec_cfg1"][shape]
+            c.update({"kernel_us": us, "kernel_GBps": round(c["bytes_per_launch"] / (us * 1e-6) / 1e9, 1)})
+    if "cfg2" in rc:
+        c = line["attention_cfg2"]
+        c.update({"kernel_us": rc["cfg2"]["kernel_us"], "split_us": rc["cfg2"]["split_us"],
+                  "merge_us": rc["cfg2"]["merge_us"],
+                  "kernel_GBps": round(c["bytes_per_launch"] / (rc["cfg2"]["kernel_us"] * 1e-6) / 1e9, 1)})
     line["attention_cfg4"] = attention_cfg4()
     if not args.no_cpu:
         line["cpu_baseline"], line["cpu_baseline_configs"] = cpu_baseline(host, args.cpu_seconds)
