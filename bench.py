@@ -19,8 +19,12 @@ value = algorithmic bytes per step / time per step (GB/s, all kernels of the
 step; HIP events on the launch stream around the K timed steps).  roofline:
 the kernel with the largest share of step time, its algorithmic bytes per
 launch over its average launch duration over a second pass of the same K
-steps, from HIP events that the kernel's own dispatches stamp
-(hipExtLaunchKernel; for attention, split start to merge end).
+steps, from HIP events that each of its kernels' dispatches stamps
+(hipExtLaunchKernel; for attention, the split and merge kernels' durations
+added, as rocprofv3 counts them), every launch of that pass run with the
+queue drained before and after it (a stamped dispatch's events otherwise
+also count the wait for the kernel before it and the launches queued
+behind it).
 rocprof_step: the same steps re-run in a child process under rocprofv3
 --kernel-trace, each op's mean kernel duration as the trace records it (the
 figures of the committed profiles/ summaries; roofline.rocprof is the
@@ -138,13 +142,18 @@ def run_gpu(args):
             hip.device.matvec(k, layer.w[name], act[i], act[o], c, r)
 
     def step(s, timed=None):
-        """One layer; `timed` maps kernel names to KernelTimers (HIP events
-        stamped by the kernels' own dispatches on the launch stream)."""
+        """One layer; `timed` maps kernel names to DispatchTimers (HIP events
+        stamped by each kernel's own dispatch on the launch stream)."""
         layer = layers[s % LAYERS]
         for name in ORDER:
             if timed and name in timed:
+                # the queue drained before and after: a stamped dispatch's
+                # events would otherwise also count the wait for the kernel
+                # before it and the launches queued behind it
+                hip.synchronize()
                 with timed[name]:
                     launch(name, layer)
+                hip.synchronize()
             else:
                 launch(name, layer)
 
@@ -159,7 +168,7 @@ def run_gpu(args):
         hip.synchronize()
         return None
     cal = max(8, 2 * LAYERS)
-    cal_timers = [{n: hip.device.KernelTimer() for n in ORDER} for _ in range(cal)]
+    cal_timers = [{n: hip.device.DispatchTimer() for n in ORDER} for _ in range(cal)]
     for s in range(cal):
         step(s, cal_timers[s])
     hip.synchronize()
@@ -176,12 +185,14 @@ def run_gpu(args):
     t1.synchronize()
     hip.synchronize()
     total_ms = t0.elapsed_ms(t1)
-    # the same K steps again with the dominant kernel's launches timed (a
-    # dispatch that stamps events is scheduled slightly differently, so this
-    # pass is kept out of `value`)
-    dom_timers = [hip.device.KernelTimer() for _ in range(args.steps)]
+    # the same K steps again with every launch timed, each kernel by its own
+    # dispatch and each launch with the queue drained before and after it
+    # (so this pass is kept out of `value`); the dominant kernel's figure
+    # is the mean of its K launches
+    all_timers = [{n: hip.device.DispatchTimer() for n in ORDER} for _ in range(args.steps)]
     for s in range(args.steps):
-        step(s, {dominant: dom_timers[s]})
+        step(s, all_timers[s])
+    dom_timers = [t[dominant] for t in all_timers]
     hip.synchronize()
     dom_ms = sum(t.ms() for t in dom_timers) / args.steps
 

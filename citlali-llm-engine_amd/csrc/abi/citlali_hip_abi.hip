@@ -715,7 +715,7 @@ CITLALI_EXPORT int citlali_hip_stream_destroy(void* stream) {
 
 CITLALI_EXPORT int citlali_hip_graph_begin(void) {
     REQUIRE(g_stream != nullptr, "graph_begin: capture needs a library stream other than the null stream");
-    REQUIRE(kernel_timing().start == nullptr, "graph_begin: kernel timing is armed");
+    REQUIRE(kernel_timing().start == nullptr && kernel_timing().starts.empty(), "graph_begin: kernel timing is armed");
     HIP_TRY(hipStreamBeginCapture(g_stream, hipStreamCaptureModeThreadLocal));
     return CITLALI_OK;
 }
@@ -879,8 +879,34 @@ CITLALI_EXPORT int citlali_hip_matvec_norm(int gguf_type, const uint8_t* w, cons
 CITLALI_EXPORT int citlali_hip_set_kernel_timing(void* start, void* stop) {
     REQUIRE((start == nullptr) == (stop == nullptr), "set_kernel_timing: give both events or neither");
     KernelTiming& t = kernel_timing();
+    REQUIRE(start == nullptr || t.starts.empty(), "set_kernel_timing: per-dispatch timing is armed");
     t.start = static_cast<hipEvent_t>(start);
     t.stop = static_cast<hipEvent_t>(stop);
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_set_dispatch_timing(void* const* starts, void* const* stops, int n) {
+    REQUIRE(n >= 0 && n <= CITLALI_MAX_TIMED_DISPATCHES, "set_dispatch_timing: n = %d outside [0, %d]", n,
+            CITLALI_MAX_TIMED_DISPATCHES);
+    KernelTiming& t = kernel_timing();
+    if (n == 0) {   // disarm; the count stays readable
+        t.starts.clear();
+        t.stops.clear();
+        return CITLALI_OK;
+    }
+    REQUIRE(starts != nullptr && stops != nullptr, "set_dispatch_timing: null event array");
+    REQUIRE(t.start == nullptr, "set_dispatch_timing: call-span timing is armed");
+    for (int i = 0; i < n; ++i)
+        REQUIRE(starts[i] != nullptr && stops[i] != nullptr, "set_dispatch_timing: null event in pair %d", i);
+    t.starts.assign(reinterpret_cast<const hipEvent_t*>(starts), reinterpret_cast<const hipEvent_t*>(starts) + n);
+    t.stops.assign(reinterpret_cast<const hipEvent_t*>(stops), reinterpret_cast<const hipEvent_t*>(stops) + n);
+    t.used = 0;
+    return CITLALI_OK;
+}
+
+CITLALI_EXPORT int citlali_hip_dispatch_timing_count(int* count) {
+    REQUIRE(count, "null output pointer");
+    *count = kernel_timing().used;
     return CITLALI_OK;
 }
 

@@ -7,6 +7,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace citlali::hip {
 
 // ---- kernel timing (citlali_hip_set_kernel_timing) ----
@@ -15,9 +17,15 @@ namespace citlali::hip {
 // when it ends (hipExtLaunchKernel stamps the events from the dispatch
 // itself), so the elapsed time is the kernels' own time, without the
 // queueing gap an event recorded on the stream would add.
+// Per-dispatch mode (citlali_hip_set_dispatch_timing): while `starts` is not
+// empty, the i-th kernel launched (i < starts.size()) records starts[i] when
+// it begins and stops[i] when it ends; `used` counts every kernel launched
+// while armed, stamped or not.
 struct KernelTiming {
     hipEvent_t start = nullptr;
     hipEvent_t stop = nullptr;
+    std::vector<hipEvent_t> starts, stops;
+    int used = 0;
 };
 KernelTiming& kernel_timing();   // thread-local state, defined by the ABI unit
 
@@ -27,6 +35,15 @@ template <typename Kernel, typename... Args>
 inline void launch_kernel_in_call(bool last, Kernel kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
                                   Args... args) {
     KernelTiming& t = kernel_timing();
+    if (!t.starts.empty()) {
+        const size_t i = (size_t)t.used++;
+        if (i < t.starts.size()) {
+            hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, t.starts[i], t.stops[i], 0u, args...);
+        } else {
+            hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+        }
+        return;
+    }
     if (t.start == nullptr && (t.stop == nullptr || !last)) {
         hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
         return;

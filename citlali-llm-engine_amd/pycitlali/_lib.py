@@ -99,6 +99,8 @@ SIGNATURES = [
     ("citlali_hip_matvec_gate_up_swiglu_norm", c_int, [c_int, _P, _P, _P, POINTER(Norm), _P, c_int, c_int]),
     ("citlali_hip_matvec_norm", c_int, [c_int, _P, _P, POINTER(Norm), _P, c_int, c_int, c_int]),
     ("citlali_hip_set_kernel_timing", c_int, [_P, _P]),
+    ("citlali_hip_set_dispatch_timing", c_int, [POINTER(c_void_p), POINTER(c_void_p), c_int]),
+    ("citlali_hip_dispatch_timing_count", c_int, [POINTER(c_int)]),
     ("citlali_hip_event_create", c_int, [POINTER(c_void_p)]),
     ("citlali_hip_event_record", c_int, [_P]),
     ("citlali_hip_event_synchronize", c_int, [_P]),

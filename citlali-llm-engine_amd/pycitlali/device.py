@@ -119,6 +119,45 @@ class KernelTimer:
         return self.start.elapsed_ms(self.stop)
 
 
+class DispatchTimer:
+    """Each kernel's own time for the library calls made inside `with
+    timer:`, stamped by its own dispatch (at most `n` kernels; more raise on
+    exit).  `each_ms()` lists them in launch order, `ms()` is their sum: the
+    kernels' durations without the gaps between them.  Use after the stream
+    has passed the calls."""
+
+    def __init__(self, n: int = 4):
+        self.starts = [Event() for _ in range(n)]
+        self.stops = [Event() for _ in range(n)]
+        self.count = 0
+
+    def __enter__(self):
+        n = len(self.starts)
+        arr = ctypes.c_void_p * n
+        _lib.call("citlali_hip_set_dispatch_timing", arr(*[e.h for e in self.starts]),
+                  arr(*[e.h for e in self.stops]), n)
+        return self
+
+    def __exit__(self, *exc):
+        c = ctypes.c_int()
+        _lib.call("citlali_hip_dispatch_timing_count", ctypes.byref(c))
+        _lib.call("citlali_hip_set_dispatch_timing", None, None, 0)
+        self.count = c.value
+        if exc[0] is None and self.count > len(self.starts):
+            raise RuntimeError(f"DispatchTimer: {self.count} kernels launched, {len(self.starts)} event pairs")
+        return False
+
+    def each_ms(self) -> list:
+        out = []
+        for i in range(self.count):
+            self.stops[i].synchronize()
+            out.append(self.starts[i].elapsed_ms(self.stops[i]))
+        return out
+
+    def ms(self) -> float:
+        return sum(self.each_ms())
+
+
 def _vp(x) -> ctypes.c_void_p:
     if isinstance(x, DeviceArray):
         return x.vp

@@ -329,6 +329,18 @@ int citlali_hip_matvec_norm(int gguf_type, const uint8_t* w, const uint16_t* x, 
  * citlali_hip_event_elapsed_ms(start, stop) is the kernels' own time.  Arm
  * before a call, disarm with (NULL, NULL) after it. */
 int citlali_hip_set_kernel_timing(void* start, void* stop);
+/* Per-dispatch kernel timing (no reference counterpart; for benchmarks):
+ * while armed with n pairs of events (1 <= n <= CITLALI_MAX_TIMED_DISPATCHES),
+ * the i-th kernel the calling thread launches, i < n, records starts[i] when
+ * it begins and stops[i] when it ends, stamped from the dispatch itself, so a
+ * call of several kernels gives each kernel's own time without the gaps
+ * between them.  citlali_hip_dispatch_timing_count gives how many kernels
+ * were launched since arming (those past n are not stamped), also after
+ * disarming with (NULL, NULL, 0).  Not together with
+ * citlali_hip_set_kernel_timing, nor during graph capture. */
+#define CITLALI_MAX_TIMED_DISPATCHES 64
+int citlali_hip_set_dispatch_timing(void* const* starts, void* const* stops, int n);
+int citlali_hip_dispatch_timing_count(int* count);
 int citlali_hip_event_create(void** event);
 int citlali_hip_event_record(void* event);                  /* on the current stream */
 int citlali_hip_event_synchronize(void* event);

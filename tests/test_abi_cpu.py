@@ -224,6 +224,34 @@ def test_synth_is_deterministic_and_shaped():
     assert abs(z.mean()) < 0.01 and abs(z.std() - 1) < 0.01
 
 
+def test_dispatch_timing_arguments():
+    """Per-dispatch timing checks its arguments on the host and excludes the
+    call-span timing (no HIP call: the events here are never used)."""
+    import ctypes
+    import pycitlali
+    lib = pycitlali.load()
+    arr = ctypes.c_void_p * 2
+    fake = arr(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000))
+    for n in (-1, 65):
+        assert lib.citlali_hip_set_dispatch_timing(fake, fake, n) == pycitlali._lib.ERR_INVALID
+        assert "outside [0, 64]" in pycitlali.last_error()
+    assert lib.citlali_hip_set_dispatch_timing(None, fake, 1) == pycitlali._lib.ERR_INVALID
+    assert "null event array" in pycitlali.last_error()
+    assert lib.citlali_hip_set_dispatch_timing(fake, arr(ctypes.c_void_p(0x1000), None), 2) == pycitlali._lib.ERR_INVALID
+    assert "null event in pair 1" in pycitlali.last_error()
+    assert lib.citlali_hip_set_kernel_timing(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000)) == 0
+    assert lib.citlali_hip_set_dispatch_timing(fake, fake, 2) == pycitlali._lib.ERR_INVALID
+    assert "call-span timing is armed" in pycitlali.last_error()
+    assert lib.citlali_hip_set_kernel_timing(None, None) == 0
+    assert lib.citlali_hip_set_dispatch_timing(fake, fake, 2) == 0
+    assert lib.citlali_hip_set_kernel_timing(ctypes.c_void_p(0x1000), ctypes.c_void_p(0x2000)) == pycitlali._lib.ERR_INVALID
+    assert "per-dispatch timing is armed" in pycitlali.last_error()
+    cnt = ctypes.c_int(-1)
+    assert lib.citlali_hip_dispatch_timing_count(ctypes.byref(cnt)) == 0 and cnt.value == 0
+    assert lib.citlali_hip_set_dispatch_timing(None, None, 0) == 0
+    assert lib.citlali_hip_dispatch_timing_count(None) == pycitlali._lib.ERR_INVALID
+
+
 def test_kernel_timing_needs_both_events():
     import ctypes
     import pycitlali

@@ -195,6 +195,51 @@ def test_kernel_timer_brackets_the_calls_kernels(hip):
     assert 0 < t1 < 5 and t3 > 2.0 * t1, (t1, t3)
 
 
+def test_dispatch_timer_stamps_each_kernel(hip):
+    """DispatchTimer gives each kernel of the armed calls its own duration:
+    one for a GEMV, two for a split attention (split + merge, 16 chunks at
+    L = 1024), whose sum leaves out the gap the call-span KernelTimer
+    includes; more kernels than event pairs raise, and the library is
+    disarmed afterwards."""
+    n, k = 4096, 4096
+    w = hip.synth.quant_matrix("q4k", hip.synth.Rng(1), n, k)
+    dw, dx, dy = up(hip, w), up(hip, hip.synth.normal_f16(hip.synth.Rng(2), k)), hip.DeviceArray(n * 2)
+    t = hip.device.DispatchTimer()
+    with t:
+        hip.device.matvec("q4k", dw, dx, dy, k, n)
+    hip.synchronize()
+    assert t.count == 1 and 0 < t.ms() < 1.0
+
+    heads, kv, hd, L = 16, 8, 128, 1024
+    rng = hip.synth.Rng(3)
+    q = up(hip, hip.synth.normal_f16(rng, heads * hd))
+    kc, vc = up(hip, hip.synth.normal_f16(rng, L * kv * hd)), up(hip, hip.synth.normal_f16(rng, L * kv * hd))
+    ws, out = hip.DeviceArray(heads * L * 4), hip.DeviceArray(heads * hd * 2)
+    attn = lambda: hip.device.attention(q, kc, vc, ws, out, L - 1, L, heads, kv, hd)
+    attn()
+    best_sum, best_span = float("inf"), float("inf")
+    for _ in range(5):
+        t, span = hip.device.DispatchTimer(), hip.device.KernelTimer()
+        with t:
+            attn()
+        with span:
+            attn()
+        hip.synchronize()
+        each = t.each_ms()
+        assert t.count == 2 and all(0 < e < 1.0 for e in each), each
+        best_sum, best_span = min(best_sum, sum(each)), min(best_span, span.ms())
+    assert best_sum <= best_span * 1.05, (best_sum, best_span)
+
+    with pytest.raises(RuntimeError, match="2 kernels launched, 1 event pairs"):
+        with hip.device.DispatchTimer(1):
+            attn()
+    hip.synchronize()
+    cnt = __import__("ctypes").c_int()
+    assert hip.load().citlali_hip_dispatch_timing_count(__import__("ctypes").byref(cnt)) == 0 and cnt.value == 2
+    attn()   # disarmed: launches unstamped
+    hip.synchronize()
+
+
 def test_argmax_signed_zero_and_block_edges(hip, orc):
     """-0.0 and +0.0 are equal for the host's `>`: the first one wins.  The
     device reduces ranges of about 1024 values per block: maxima placed at
