@@ -135,6 +135,28 @@ def test_attention_without_scores_buffer(hip, orc):
     assert np.all(tol_ok(got, orc.attention(q, k, v, L - 1, heads, kv, hd)))
 
 
+@pytest.mark.parametrize("heads,kv_heads,L", [(32, 8, 8192), (16, 8, 1024), (32, 8, 32768)])
+def test_full_size_value_scaling(hip, heads, kv_heads, L):
+    """At the benchmark lengths (configs 3 and 2, and config 4's longest
+    sequence): doubling every V value doubles the output bit for bit
+    wherever it is a normal fp16 number (the softmax weights do not change;
+    the products, sums, the normalisation and the rounding commute with a
+    power-of-two factor).  Below 2^-14 the fp16 spacing is a fixed 2^-24, so
+    there the doubled output is the rounding of twice the exact value, within
+    one such step of twice the first output."""
+    hd = 128
+    k, v = _cache(hip, 31, L, kv_heads, hd)
+    q = hip.synth.normal_f16(hip.synth.Rng(32), heads * hd)
+    v2 = (v.view(np.float16) * np.float16(2)).view(np.uint16)
+    a = _run(hip, q, k, v, L - 1, L, heads, kv_heads, hd)
+    b = _run(hip, q, k, v2, L - 1, L, heads, kv_heads, hd)
+    assert np.all(np.isfinite(a))
+    normal = np.abs(a) >= 2.0 ** -14
+    assert normal.mean() > 0.9
+    np.testing.assert_array_equal(b[normal], 2 * a[normal])
+    assert np.all(np.abs(b[~normal] - 2 * a[~normal]) <= 2.0 ** -24)
+
+
 def test_single_position_returns_v0(hip):
     heads, kv, hd = 32, 8, 128
     k, v = _cache(hip, 9, 16, kv, hd)

@@ -131,6 +131,47 @@ def test_linearity_and_row_sums(hip, orc):
     np.testing.assert_array_equal(dy.download(np.float32, n), 2 * y1)
 
 
+# BASELINE's full shapes: config 3's largest GEMVs and config 5's output
+# GEMV (fp32 logits, 510 MB), through size-independent exact properties
+FULL = [("q4k", 12288, 4096, False), ("q6k", 4096, 12288, False), ("q6k", 151936, 4096, True)]
+
+
+@pytest.mark.parametrize("kind,n,k,f32", FULL)
+def test_full_size_scaling_and_row_order(hip, kind, n, k, f32):
+    """y(2x) = 2 y(x) bit for bit (power-of-two scaling commutes with every
+    product, sum and rounding while nothing overflows and, for fp16 y, the
+    value is a normal number: below 2^-14 the fp16 spacing is a fixed 2^-24,
+    so there y(2x) is within one such step of 2 y(x)), and a matrix with its
+    rows reversed gives the reversed y bit for bit (a row's result does not
+    depend on which wave or workgroup computes it)."""
+    rng = hip.synth.Rng(23)
+    w = hip.synth.quant_matrix(kind, rng, n, k)
+    x = hip.synth.normal_f16(rng, k)
+    x2 = (x.view(np.float16) * np.float16(2)).view(np.uint16)
+    dw = hip.DeviceArray.from_numpy(w)
+    dy = hip.DeviceArray(n * 4)
+    out = np.float32 if f32 else np.float16
+
+    def run(wd, xv):
+        hip.device.matvec(kind, wd, hip.DeviceArray.from_numpy(xv), dy, k, n, f32_out=f32)
+        return dy.download(np.float32 if f32 else np.uint16, n).view(out).copy()
+
+    y1 = run(dw, x)
+    assert np.all(np.isfinite(y1))
+    y2 = run(dw, x2)
+    exact = np.ones(n, bool) if f32 else np.abs(y1.astype(np.float64)) >= 2.0 ** -14
+    np.testing.assert_array_equal(y2[exact], y1[exact] * out(2))
+    assert np.all(np.abs(y2[~exact].astype(np.float64) - 2 * y1[~exact].astype(np.float64)) <= 2.0 ** -24)
+    dw.close()
+    wr = np.ascontiguousarray(w.reshape(n, -1)[::-1])
+    del w
+    drev = hip.DeviceArray.from_numpy(wr)
+    del wr
+    np.testing.assert_array_equal(run(drev, x), y1[::-1])
+    drev.close()
+    dy.close()
+
+
 def test_rows_permute_with_weights(hip):
     n, k = 96, 1024
     rng = hip.synth.Rng(5)
