@@ -219,9 +219,13 @@ def test_dispatch_timer_stamps_each_kernel(hip):
     attn()
     best_sum, best_span = float("inf"), float("inf")
     for _ in range(5):
+        # each timed call with the queue drained around it (a stamped
+        # dispatch's events otherwise also count the launches queued behind)
         t, span = hip.device.DispatchTimer(), hip.device.KernelTimer()
+        hip.synchronize()
         with t:
             attn()
+        hip.synchronize()
         with span:
             attn()
         hip.synchronize()
