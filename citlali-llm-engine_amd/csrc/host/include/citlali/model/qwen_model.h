@@ -92,7 +92,7 @@ private:
     bool launch_qkv_grouped(const QwenLayerWeights& layer, int hidden, const uint16_t* input,
                             const compute::NormInput* norm);
     void enqueue_token(int32_t token_id, int position, int32_t* state, int plan_length, bool compute_logits);
-    void* step_graph(int plan_length);
+    void* step_graph(int plan_length, int steps);
     void release_graphs() noexcept;
     int32_t sample_greedy_from_logits();
 
@@ -108,7 +108,11 @@ private:
     compute::DeviceBufferPtr state_, tokens_;   // decode_greedy: {token, position, step, 0}, picks
     std::unique_ptr<LinearBackend> linear_backend_;
     void* stream_ = nullptr;                                  // decode_greedy's stream
-    std::vector<std::pair<int, void*>> graphs_;               // plan length -> captured step
+    struct StepGraph {
+        int plan_length, steps;
+        void* graph;
+    };
+    std::vector<StepGraph> graphs_;   // captured decode steps, by plan length and step count
 };
 
 }  // namespace citlali::model
