@@ -289,6 +289,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(int parts,
                                                                       int32_t* __restrict__ state,
                                                                       int32_t* __restrict__ tokens, int capacity) {
     __shared__ uint64_t red[kArgmaxThreads / kWave];
+    // the position and step are read with the partials, not after the
+    // reduction
+    const bool lead = state && threadIdx.x == 0;
+    const int32_t position = lead ? state[1] : 0, step = lead ? state[2] : 0;
     uint64_t k = 0;
     for (int i = threadIdx.x; i < parts; i += kArgmaxThreads) k = g_argmax_partial[i] > k ? g_argmax_partial[i] : k;
     const uint64_t m = block_max_u64(k, red);
@@ -296,10 +300,9 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(int parts,
         const int32_t pick = m == 0 ? 0 : (int32_t)~(uint32_t)(m & 0xffffffffu);
         if (out) out[0] = pick;
         if (state) {
-            const int32_t step = state[2];
             if (step >= 0 && step < capacity) tokens[step] = pick;
             state[0] = pick;
-            state[1] += 1;
+            state[1] = position + 1;
             state[2] = step + 1;
         }
     }
