@@ -242,9 +242,10 @@ CONFIG_REPS = 10   # timed passes over the rotated copies, configs 1 and 2
 def _time_rotated(hip, launch, n, reps, stamped=True):
     """Mean launch time (us) over reps passes of n back-to-back launches
     (launch(i) uses copy i): HIP events around all of them, and the kernels'
-    own dispatch-stamped time of one more pass (stamped=False: that pass is
-    left out, for the rocprofv3 child, whose trace then holds one untimed
-    pass and the reps timed ones)."""
+    own dispatch-stamped time (each kernel's duration, added per launch) of
+    one more pass (stamped=False: that pass is left out, for the rocprofv3
+    child, whose trace then holds one untimed pass and the reps timed
+    ones)."""
     for i in range(n):
         launch(i)
     e0, e1 = hip.Event(), hip.Event()
@@ -257,11 +258,14 @@ def _time_rotated(hip, launch, n, reps, stamped=True):
     wall_us = e0.elapsed_ms(e1) / (reps * n) * 1e3
     if not stamped:
         return wall_us, None
-    timers = [hip.device.KernelTimer() for _ in range(n)]
+    # each kernel stamped by its own dispatch, the queue drained around each
+    # launch (as in the step's roofline pass)
+    timers = [hip.device.DispatchTimer() for _ in range(n)]
     for i in range(n):
+        hip.synchronize()
         with timers[i]:
             launch(i)
-    hip.synchronize()
+        hip.synchronize()
     kern_us = sum(t.ms() for t in timers) / n * 1e3
     return wall_us, kern_us
 
