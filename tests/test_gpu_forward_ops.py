@@ -198,9 +198,10 @@ def test_kernel_timer_brackets_the_calls_kernels(hip):
 def test_dispatch_timer_stamps_each_kernel(hip):
     """DispatchTimer gives each kernel of the armed calls its own duration:
     one for a GEMV, two for a split attention (split + merge, 16 chunks at
-    L = 1024), whose sum leaves out the gap the call-span KernelTimer
-    includes; more kernels than event pairs raise, and the library is
-    disarmed afterwards."""
+    L = 1024), each positive and their sum of the order of the call-span
+    KernelTimer's (each stamped dispatch carries its own event overhead, so
+    the sum is only bounded loosely); more kernels than event pairs raise,
+    and the library is disarmed afterwards."""
     n, k = 4096, 4096
     w = hip.synth.quant_matrix("q4k", hip.synth.Rng(1), n, k)
     dw, dx, dy = up(hip, w), up(hip, hip.synth.normal_f16(hip.synth.Rng(2), k)), hip.DeviceArray(n * 2)
@@ -232,7 +233,7 @@ def test_dispatch_timer_stamps_each_kernel(hip):
         each = t.each_ms()
         assert t.count == 2 and all(0 < e < 1.0 for e in each), each
         best_sum, best_span = min(best_sum, sum(each)), min(best_span, span.ms())
-    assert best_sum <= best_span * 1.05, (best_sum, best_span)
+    assert 0.25 * best_span <= best_sum <= 1.5 * best_span, (best_sum, best_span)
 
     with pytest.raises(RuntimeError, match="2 kernels launched, 1 event pairs"):
         with hip.device.DispatchTimer(1):
